@@ -1,0 +1,57 @@
+/* tallymap_rocm.h -- the C ABI of libtallymap_rocm.so, the MI355X (gfx950) launch library of the tallymap_amd
+ * kernel backend.  Plain pointers and sizes only.  Every entry returns 0 on success and a nonzero code on failure;
+ * tm_last_error() then holds the message (per thread).
+ *
+ * It replaces the reference's CUDA launch shim, tallymap/backends/kernel/shim.cc (and the NVRTC calls of
+ * compile.py), entry for entry:
+ *   tm_register      <- tallymap_register      (shim.cc:134-142)
+ *   tm_kernel_info   <- tallymap_kernel_info   (shim.cc:147-155)
+ *   tm_launch        <- SjLaunchImpl, the body of the XLA FFI handler TallymapLaunch (shim.cc:157-250), as a
+ *                       plain C call: an XLA FFI binding for platform "ROCM" forwards to it
+ *   tm_compile       <- compile.compile_cubin's NVRTC sequence (compile.py:160-173), with hipRTC for gfx950
+ *   tm_init          <- compile.py's Drv / dlopen of the driver (shim.cc:44-82): binds the HIP runtime the process
+ *                       already uses (no second runtime, no device code in this library)
+ */
+#ifndef TALLYMAP_ROCM_H
+#define TALLYMAP_ROCM_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Bind the HIP runtime library `hip_path` and hipRTC library `hiprtc_path` (NULL: the system's libamdhip64.so.7 /
+ * libhiprtc.so.7).  Idempotent: later calls with other paths keep the first binding. */
+int tm_init(const char* hip_path, const char* hiprtc_path);
+
+/* Compile HIP source `src` with hipRTC (options `opts[0..nopts)`, e.g. --offload-arch=gfx950).  On success
+ * *image / *n hold the code object (free with tm_free); *log (may be NULL) receives the compiler log (tm_free). */
+int tm_compile(const char* src, const char* name, const char* const* opts, int nopts, void** image, size_t* n,
+               char** log);
+
+/* Register code object `image` (n bytes, copied) under `id`.  The first registration of an id wins; `note` is a
+ * label for error messages.  Modules are loaded per device lazily, on the first launch there. */
+int tm_register(long long id, const void* image, size_t n, const char* note);
+
+/* Launch program `id` on `stream` (a hipStream_t; NULL: the null stream) over n_items items.  bufs: the n buffer
+ * pointers in the program's layout ([per-item operands][broadcast operands][results]).  n_zero > 0: run tm_zero
+ * first (it clears the program's accumulators and counters); flags bit 1: run tm_post after tm_main (exact
+ * readout, truncation poison).  block: threads per block of tm_main (the program's compiled block size).
+ * Asynchronous: nothing waits for the kernels. */
+int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, int flags, long long n_items,
+              int block);
+
+/* out[8]: registers per lane of tm_main, private (scratch) bytes per lane, static LDS bytes per block, achieved
+ * blocks per CU at `block` threads, resident threads on the device, compute units, max threads per block, and the
+ * grid tm_launch uses for 2^31 - 1 items. */
+int tm_kernel_info(long long id, int block, long long out[8]);
+
+const char* tm_last_error(void);
+void tm_free(void* p);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,179 @@
+"""The parity oracle and CPU baseline -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the
+checker: the product (tallymap_amd) never imports, links or calls it.  `libtmref.so` is a plain-C/OpenMP restatement
+of what the reference's CPU kernel backend computes for the benchmark item programs (tmref.c states each rule and
+the reference file:line it follows).  `exact.py` is the Python-integer exact sum of the reference's tests
+(tests/edge.py:2038-2065), used to pin tmref's exact accumulator.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libtmref.so")
+_lib = None
+
+_f = ctypes.c_float
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+_p = ctypes.c_void_p
+
+
+def build():
+    """compile libtmref.so in place (make, gcc -fopenmp)."""
+    subprocess.run(["make", "-s", "-C", HERE, "libtmref.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = ctypes.CDLL(LIB)
+        L.tmref_threefry.argtypes = [_u32, _u32, _u32, _u32, _p]
+        L.tmref_erfinvf.restype = _f
+        L.tmref_erfinvf.argtypes = [_f]
+        L.tmref_fold_in.argtypes = [_p, _u32, _p]
+        L.tmref_split.argtypes = [_p, ctypes.c_uint64, _p]
+        L.tmref_uniform.restype = _f
+        L.tmref_uniform.argtypes = [_p, _f, _f]
+        L.tmref_normal.restype = _f
+        L.tmref_normal.argtypes = [_p]
+        L.tmref_bits32.restype = _u32
+        L.tmref_bits32.argtypes = [_p]
+        L.tmref_exact_sum.restype = _f
+        L.tmref_exact_sum.argtypes = [_p, _i64, _p]
+        L.tmref_c1_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
+        L.tmref_c1_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p]
+        L.tmref_c2_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p]
+        L.tmref_c2_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
+        L.tmref_c2_x0.argtypes = [_p, _i64, _p]
+        L.tmref_max_threads.restype = _i
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def threefry(k0, k1, c0, c1):
+    out = np.zeros(2, np.uint32)
+    lib().tmref_threefry(k0, k1, c0, c1, _ptr(out))
+    return int(out[0]), int(out[1])
+
+
+def erfinvf(y):
+    return np.float32(lib().tmref_erfinvf(float(np.float32(y))))
+
+
+def fold_in(key, d):
+    key = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(2, np.uint32)
+    lib().tmref_fold_in(_ptr(key), int(d) & 0xFFFFFFFF, _ptr(out))
+    return out
+
+
+def split(key, n):
+    key = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros((n, 2), np.uint32)
+    lib().tmref_split(_ptr(key), n, _ptr(out))
+    return out
+
+
+def uniform(key, lo=0.0, hi=1.0):
+    key = np.ascontiguousarray(key, np.uint32)
+    return np.float32(lib().tmref_uniform(_ptr(key), float(np.float32(lo)), float(np.float32(hi))))
+
+
+def normal(key):
+    key = np.ascontiguousarray(key, np.uint32)
+    return np.float32(lib().tmref_normal(_ptr(key)))
+
+
+def bits32(key):
+    key = np.ascontiguousarray(key, np.uint32)
+    return int(lib().tmref_bits32(_ptr(key)))
+
+
+def exact_sum(v):
+    v = np.ascontiguousarray(v, np.float32)
+    bad = np.zeros(1, np.int32)
+    r = lib().tmref_exact_sum(_ptr(v), v.size, _ptr(bad))
+    return np.float32(r), bool(bad[0])
+
+
+def max_threads():
+    return int(lib().tmref_max_threads())
+
+
+class Fwd:
+    """an oracle forward run: f32 tallies (reference semantics), their float64 re-summation, per-item results,
+    truncation flags and the stats vector."""
+
+    def __init__(self, tallies, tallies64, per_item, trunc, stats):
+        self.tallies, self.tallies64, self.per_item, self.trunc, self.stats = tallies, tallies64, per_item, trunc, stats
+
+
+def c1_fwd(xs, keys, theta, max_steps=100, nthreads=0, shadow=True):
+    xs = np.ascontiguousarray(xs, np.float32)
+    keys = np.ascontiguousarray(keys, np.uint32)
+    n = xs.shape[0]
+    hist = np.zeros(16, np.float32)
+    h64 = np.zeros(16, np.float64) if shadow else None
+    ks = np.zeros(n, np.int32)
+    tr = np.zeros(n, np.uint8)
+    st = np.zeros(5, np.int32)
+    lib().tmref_c1_fwd(_ptr(xs), _ptr(keys), float(np.float32(theta)), n, max_steps, nthreads, _ptr(hist), _ptr(h64),
+                       _ptr(ks), _ptr(tr), _ptr(st))
+    return Fwd({"hist": hist}, {"hist": h64}, ks, tr.astype(bool), st)
+
+
+def c1_grad(xs, keys, theta, ct, max_steps=100, nthreads=0):
+    xs = np.ascontiguousarray(xs, np.float32)
+    keys = np.ascontiguousarray(keys, np.uint32)
+    ct = np.ascontiguousarray(ct, np.float32)
+    out = np.zeros(1, np.float32)
+    ntr = np.zeros(1, np.int32)
+    lib().tmref_c1_grad(_ptr(xs), _ptr(keys), float(np.float32(theta)), xs.shape[0], max_steps, nthreads, _ptr(ct),
+                        _ptr(out), _ptr(ntr))
+    return out[0], int(ntr[0])
+
+
+def c2_fwd(x0, keys, drift, max_steps=65536, nthreads=0, shadow=True, per_item=True):
+    x0 = np.ascontiguousarray(x0, np.float32)
+    keys = np.ascontiguousarray(keys, np.uint32)
+    n = x0.shape[0]
+    occ, wall = np.zeros(128, np.float32), np.zeros(2, np.float32)
+    o64 = np.zeros(128, np.float64) if shadow else None
+    w64 = np.zeros(2, np.float64) if shadow else None
+    ks = np.zeros(n, np.int32) if per_item else None
+    tr = np.zeros(n, np.uint8) if per_item else None
+    st = np.zeros(5, np.int32)
+    lib().tmref_c2_fwd(_ptr(x0), _ptr(keys), float(np.float32(drift)), n, max_steps, nthreads, _ptr(occ), _ptr(wall),
+                       _ptr(o64), _ptr(w64), _ptr(ks), _ptr(tr), _ptr(st))
+    return Fwd({"occ": occ, "wall": wall}, {"occ": o64, "wall": w64}, ks,
+               tr.astype(bool) if tr is not None else None, st)
+
+
+def c2_grad(x0, keys, drift, ct_occ, ct_wall, max_steps=65536, nthreads=0):
+    x0 = np.ascontiguousarray(x0, np.float32)
+    keys = np.ascontiguousarray(keys, np.uint32)
+    ct_occ = np.ascontiguousarray(ct_occ, np.float32)
+    ct_wall = np.ascontiguousarray(ct_wall, np.float32)
+    out = np.zeros(1, np.float32)
+    ntr = np.zeros(1, np.int32)
+    lib().tmref_c2_grad(_ptr(x0), _ptr(keys), float(np.float32(drift)), x0.shape[0], max_steps, nthreads,
+                        _ptr(ct_occ), _ptr(ct_wall), _ptr(out), _ptr(ntr))
+    return out[0], int(ntr[0])
+
+
+def c2_x0(keys):
+    keys = np.ascontiguousarray(keys, np.uint32)
+    out = np.zeros(keys.shape[0], np.float32)
+    lib().tmref_c2_x0(_ptr(keys), keys.shape[0], _ptr(out))
+    return out

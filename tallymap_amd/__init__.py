@@ -1,0 +1,13 @@
+"""tallymap_amd: an MI355X-native (gfx950, HIP) kernel backend for tallymap-style `vmap` programs.
+
+An item function of ONE item (its own while loop, its own jax.random draws, results added into write-only
+tallies) is traced into a jaxpr-shaped program, lowered to HIP, compiled with hipRTC for gfx950 and launched as
+one persistent wave64 kernel through the C-ABI library libtallymap_rocm.so.  Reverse-mode gradients run the
+checkpointed replay adjoint through the same path.
+"""
+from . import lax, numpy, random
+from ._api import STATS, Result, Sum, TallyError, UnsupportedError, vmap
+from ._tally import Tally
+
+__version__ = "0.1.0"
+__all__ = ["vmap", "Sum", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]

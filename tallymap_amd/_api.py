@@ -1,0 +1,371 @@
+"""The user contract: Sum, Result, STATS, ItemProgram and vmap (reference tallymap/_api.py).
+
+`vmap(item, outputs={name: Sum(shape)}, in_axes=..., max_steps=...)` returns `mapped(*args)`.  A call traces the
+item once per argument signature into an ItemProgram (invars [tallies] + [per-item operands] + [broadcast
+operands]; outvars [tallies] + [per-item results] (+ [truncated])), checks that the tallies are used linearly,
+and launches the HIP kernel backend (tallymap_amd.backend).  Its meaning is the reference's: jax.vmap(item) over
+the items followed by a sum of their tallies, with the resource-limit poison of _api.py:898-958 (any truncated
+item makes every float tally NaN; integer tallies are left alone).
+"""
+import collections
+import dataclasses
+import hashlib
+
+import numpy as np
+
+from . import _core as C
+from . import lax as L
+from ._tally import Tally
+from ._tree import flatten, unflatten
+
+STATS = ("spawned", "children_dropped", "children_truncated", "fixed_point_overflow", "dropped_emits")
+ST = {n: i for i, n in enumerate(STATS)}
+MAX_ITEMS = 2 ** 31 - 1
+PROG_CACHE = 64
+OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill")
+
+
+class UnsupportedError(NotImplementedError):
+    """the backend cannot run this program (it never falls back: reference _api.py:198-200)."""
+
+
+class TallyError(TypeError):
+    """a tally used non-linearly: read, forked or dropped (reference _rewrite.py:31)."""
+
+
+@dataclasses.dataclass(frozen=True)
+class Sum:
+    """a commutative (sum) output of `shape` and `dtype` (reference _api.py:55-84).  fixed_point=True with float32
+    is the EXACT sum: each bin the correctly rounded f32 of the exact sum of every finite value emitted into it."""
+    shape: object
+    dtype: object = np.float32
+    fixed_point: bool = False
+
+
+class Result(collections.namedtuple("Result", "outputs per_item truncated stats")):
+    """outputs: {name: summed output}; per_item: per-item results (None if the item returns only its tally);
+    truncated: bool[N]; stats: {name: int32 scalar} (reference _api.py:180-189)."""
+
+
+@dataclasses.dataclass(frozen=True)
+class TSpec:
+    name: str
+    shape: tuple
+    dtype: np.dtype
+    exact: bool = False
+    kind: str = "sum"          # 'sum' | 'discard' (a derived program's tally that is not output)
+
+    @property
+    def S(self):
+        return int(np.prod(self.shape, dtype=np.int64))
+
+
+@dataclasses.dataclass(eq=False)
+class ItemProgram:
+    """jaxpr invars: [tallies] + [per-item operands] + [broadcast operands]; outvars: [tallies (same slots)] +
+    [per-item results]; trunc: index of the truncation flag among the per-item results (None: no cap)."""
+    jaxpr: C.Jaxpr
+    tallies: tuple
+    nP: int
+    nB: int
+    trunc: object = None
+    tag: str = "primal"
+    where: str = ""
+
+    @property
+    def nT(self):
+        return len(self.tallies)
+
+    def y_avals(self):
+        return [v.aval for v in self.jaxpr.outvars[self.nT:]]
+
+    def p_avals(self):
+        return [v.aval for v in self.jaxpr.invars[self.nT:self.nT + self.nP]]
+
+    def b_avals(self):
+        return [v.aval for v in self.jaxpr.invars[self.nT + self.nP:]]
+
+    @property
+    def out_tallies(self):
+        return [k for k, s in enumerate(self.tallies) if s.kind == "sum"]
+
+    def digest(self):
+        return digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag))
+
+
+# ----------------------------------------------------------------------------------------- tally checks
+def check_tallies(jx, nT, where=""):
+    """every tally value is used exactly once, only to thread it: by an emit (its operand 0), as a while / cond
+    carry, or as a program output (reference _rewrite.py:41-56).  Raises TallyError."""
+    pos = _flow(jx, {v.id for v in jx.invars[:nT]}, where)
+    if pos != set(range(nT)):
+        raise TallyError(f"tallymap: the item function {where} must return its tally (the last t = t.add(...))")
+
+
+def _flow(jx, tin, where, allow_drop=False):
+    """validate the tally use of jx, whose invars with ids in `tin` are tallies -> the indices of jx.outvars that
+    are tallies."""
+    tv, used = set(tin), set()
+
+    def consume(v):
+        if v.id in used:
+            raise TallyError(f"tallymap: a tally is used twice (forked) in the item function {where}")
+        used.add(v.id)
+    for e in jx.eqns:
+        for j, v in enumerate(e.invars):
+            if isinstance(v, C.Var) and v.id in tv:
+                if not ((e.prim == "tallymap_emit" and j == 0) or e.prim in ("while", "cond", "copy")):
+                    raise TallyError(f"tallymap: a tally is read by `{e.prim}` in the item function {where}: "
+                                     "tallies are write-only (t = t.add(...)), used linearly")
+        if e.prim == "tallymap_emit":
+            consume(e.invars[0])
+            tv.add(e.outvars[0].id)
+        elif e.prim == "copy":
+            if isinstance(e.invars[0], C.Var) and e.invars[0].id in tv:
+                consume(e.invars[0])
+                tv.add(e.outvars[0].id)
+        elif e.prim == "while":
+            nc, nb = e.params["cond_nconsts"], e.params["body_nconsts"]
+            if any(isinstance(v, C.Var) and v.id in tv for v in e.invars[:nc + nb]):
+                raise TallyError(f"tallymap: a loop closes over a tally in {where}: thread it as a carry")
+            init = e.invars[nc + nb:]
+            flags = [isinstance(v, C.Var) and v.id in tv for v in init]
+            for v, f in zip(init, flags):
+                if f:
+                    consume(v)
+            bj, cj = e.params["body_jaxpr"], e.params["cond_jaxpr"]
+            got = _flow(bj, {v.id for v, f in zip(bj.invars[nb:], flags) if f}, where)
+            if got != {k for k, f in enumerate(flags) if f}:
+                raise TallyError(f"tallymap: a loop body does not return its tally carries in place in {where}")
+            _flow(cj, {v.id for v, f in zip(cj.invars[nc:], flags) if f}, where, allow_drop=True)
+            for o, f in zip(e.outvars, flags):
+                if f:
+                    tv.add(o.id)
+        elif e.prim == "cond":
+            nco = e.params["nconsts"]
+            if any(isinstance(v, C.Var) and v.id in tv for v in e.invars[1:1 + nco]):
+                raise TallyError(f"tallymap: a cond branch closes over a tally in {where}: pass it as an operand")
+            ops = e.invars[1 + nco:]
+            flags = [isinstance(v, C.Var) and v.id in tv for v in ops]
+            for v, f in zip(ops, flags):
+                if f:
+                    consume(v)
+            outs = None
+            for br in e.params["branches"]:
+                got = _flow(br, {v.id for v, f in zip(br.invars[nco:], flags) if f}, where)
+                if outs is not None and got != outs:
+                    raise TallyError(f"tallymap: the branches of a cond return tallies in different slots in {where}")
+                outs = got
+            if len(outs) != sum(flags):
+                raise TallyError(f"tallymap: a cond branch drops or duplicates a tally in {where}")
+            for k in outs:
+                tv.add(e.outvars[k].id)
+    for o in jx.outvars:
+        if isinstance(o, C.Var) and o.id in tv:
+            consume(o)
+    if not allow_drop and tv - used:
+        raise TallyError(f"tallymap: a tally update is dropped in the item function {where}: return the last "
+                         "tally (t = t.add(...) returns a NEW tally)")
+    return {i for i, o in enumerate(jx.outvars) if isinstance(o, C.Var) and o.id in tv}
+
+
+# -------------------------------------------------------------------------------------------- digests
+def _pval(v):
+    if isinstance(v, C.Jaxpr):
+        return ("J", _jx_key(v))
+    if isinstance(v, (tuple, list)):
+        return tuple(_pval(x) for x in v)
+    if isinstance(v, np.dtype):
+        return v.name
+    return repr(v)
+
+
+def _jx_key(jx):
+    names = {}
+
+    def nm(v):
+        if isinstance(v, C.Lit):
+            return ("L", v.aval.dtype.name, v.aval.shape, v.val.tobytes())
+        return names.setdefault(v.id, ("V", len(names), v.aval.dtype.name, v.aval.shape))
+    key = [tuple(nm(v) for v in jx.invars)]
+    for e in jx.eqns:
+        key.append((e.prim, tuple(nm(v) for v in e.invars), tuple(nm(v) for v in e.outvars),
+                    tuple(sorted((k, _pval(x)) for k, x in e.params.items()))))
+    key.append(tuple(nm(v) for v in jx.outvars))
+    return tuple(key)
+
+
+def digest(jx, tallies=(), extra=()):
+    """structural sha256 of a program (reference _jaxpr.py:301-309): variable names are canonical, literals by
+    their bytes."""
+    h = hashlib.sha256(repr((_jx_key(jx), tuple((s.name, s.shape, s.dtype.name, s.exact, s.kind)
+                                                  for s in tallies), extra)).encode())
+    return h.hexdigest()
+
+
+# ---------------------------------------------------------------------------------------------- vmap
+_PROGS = collections.OrderedDict()
+
+
+def _np_dtype(x):
+    try:
+        import torch
+        if isinstance(x, torch.Tensor):
+            return np.dtype(str(x.dtype).replace("torch.", "").replace("bool", "bool_"))
+    except ImportError:
+        pass
+    return np.asarray(x).dtype if not hasattr(x, "dtype") else np.dtype(x.dtype)
+
+
+def _shape(x):
+    return tuple(int(s) for s in x.shape) if hasattr(x, "shape") else np.shape(x)
+
+
+def item_name(fn):
+    code = getattr(fn, "__code__", None)
+    q = getattr(fn, "__qualname__", repr(fn))
+    return f"{q} ({code.co_filename}:{code.co_firstlineno})" if code else q
+
+
+def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None):
+    """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves)."""
+    names = sorted(outs_spec)
+    tspecs = []
+    for n in names:
+        s = outs_spec[n]
+        shape = (s.shape,) if isinstance(s.shape, int) else tuple(s.shape)
+        dt = np.dtype(s.dtype)
+        exact = bool(s.fixed_point) and dt == C.F32
+        if s.fixed_point and not exact:
+            raise UnsupportedError("tallymap: Sum(fixed_point=True) is supported for float32 (the exact sum) only")
+        if int(np.prod(shape, dtype=np.int64)) > MAX_ITEMS:
+            raise ValueError(f"tallymap: output {n!r} has more than 2^31 - 1 cells")
+        tspecs.append(TSpec(n, shape, dt, exact))
+    where = item_name(fn)
+    tav = [C.AVal((s.S,), s.dtype) for s in tspecs]
+    shapes = {s.name: s.shape for s in tspecs}
+    meta = {}
+    b = C.Builder()
+    C._STACK.append(b)
+    capctx = L._CapCtx(b, max_steps) if max_steps is not None else None
+    if capctx is not None:
+        L._CAP.append(capctx)
+    try:
+        tin = [C.Tracer(b.new_invar(a)) for a in tav]
+        pin = [C.Tracer(b.new_invar(a)) for a in pav]
+        bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
+        t = Tally({n: x for n, x in zip(names, tin)}, shapes)
+        m = unflatten(ptree, pin) if ptree is not None else pin
+        bb = unflatten(btree, bin_) if btree is not None else bin_
+        mi, bi = iter(m), iter(bb)
+        uargs = [next(mi) if x == 0 else next(bi) for x in axes]
+        r = fn(t, *uargs)
+        if isinstance(r, Tally):
+            t2, y = r, None
+        elif isinstance(r, tuple) and len(r) == 2 and isinstance(r[0], Tally):
+            t2, y = r
+        else:
+            raise TypeError("tallymap: the item function must return its Tally or (Tally, per_item_result)")
+        yl, meta["ytree"] = flatten(y)
+        outs = []
+        for n in names:
+            outs.append(b.local(t2._a[n].var))
+        for v in yl:
+            if not C.is_traced(v):
+                v = C.Tracer(C.bind("copy", [C.literal(v)], [C.literal(v).aval.strong()])[0].var)
+            outs.append(b.local(v.var))
+        trunc = None
+        if capctx is not None:
+            tr = capctx.trunc
+            if tr is None:
+                tr = C.Tracer(C.bind("copy", [C.Lit(False, C.AVal((), C.BOOL))], [C.AVal((), C.BOOL)])[0].var)
+            outs.append(b.local(tr.var))
+            trunc = len(outs) - len(names) - 1
+    finally:
+        C._STACK.pop()
+        if capctx is not None:
+            L._CAP.pop()
+    jx = C.Jaxpr(b.invars, outs, b.eqns)
+    if b.captured:
+        raise C.TraceError("tallymap: the item function closes over a traced value of another call")
+    check_tallies(jx, len(tspecs), where)
+    prog = ItemProgram(jx, tuple(tspecs), len(pav), len(bav), trunc, "primal", where)
+    return prog, meta
+
+
+def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts):
+    """Map `fn(tally, *args) -> tally | (tally, y)` over the leading axis of the mapped args (reference
+    _api.py:428-700).
+
+    outputs:   {name: Sum(shape, dtype=float32, fixed_point=False)}
+    in_axes:   0 (mapped) or None (broadcast) per positional argument
+    max_steps: cap on every top-level while loop; an item that hits it is flagged in Result.truncated and makes
+               every float tally of the call NaN
+    backend:   'auto' / 'hip' (the HIP kernel backend; it never falls back)
+    opts:      schedule 'step' (default: a lane refills at loop-step granularity) | 'item'; block (threads per
+               block, default 256); refill (idle lanes a wave waits for before it claims, default 1);
+               rev_checkpoints (reverse mode, C states per checkpoint buffer); cuda_math and min_blocks_per_sm
+               are accepted for drop-in compatibility and have no meaning on ROCm.
+    """
+    if fn is None:
+        return lambda f: vmap(f, outputs=outputs, in_axes=in_axes, max_steps=max_steps, backend=backend, **opts)
+    bad = sorted(set(opts) - set(OPTS))
+    if bad:
+        raise ValueError(f"tallymap: unknown option(s) {bad}; options are " + ", ".join(OPTS))
+    if opts.get("schedule", "step") not in ("item", "step"):
+        raise ValueError(f"tallymap: schedule must be 'item' or 'step', got {opts['schedule']!r}")
+    if backend not in ("auto", "hip", "rocm"):
+        raise ValueError(f"tallymap: unknown backend {backend!r}; this package is the ROCm (HIP) kernel backend")
+    outs_spec = {k: (v if isinstance(v, Sum) else Sum(v)) for k, v in outputs.items()}
+    names = sorted(outs_spec)
+
+    def prepare(args):
+        axes = in_axes if isinstance(in_axes, (tuple, list)) else (in_axes,) * len(args)
+        if len(axes) != len(args) or any(a not in (0, None) for a in axes):
+            raise ValueError("tallymap: in_axes must be 0/None or a tuple of 0/None per positional argument")
+        margs = tuple(a for a, x in zip(args, axes) if x == 0)
+        bargs = tuple(a for a, x in zip(args, axes) if x is None)
+        pi, ptree = flatten(margs)
+        bc, btree = flatten(bargs)
+        if not pi:
+            raise ValueError("tallymap: at least one argument must be mapped (in_axes=0)")
+        Ns = {_shape(x)[0] if len(_shape(x)) else -1 for x in pi}
+        if len(Ns) != 1 or -1 in Ns:
+            raise ValueError(f"tallymap: mapped arguments must share one leading axis length, got {sorted(Ns)}")
+        N = Ns.pop()
+        if N > MAX_ITEMS:
+            raise ValueError(f"tallymap: N={N} items exceeds 2^31-1; split the call")
+        pav = [C.AVal(_shape(x)[1:], _np_dtype(x)) for x in pi]
+        bav = [C.AVal(_shape(x), _np_dtype(x)) for x in bc]
+        key = (tuple(pav), tuple(bav), tuple(axes), str(ptree), str(btree), max_steps,
+               tuple(sorted((n, repr(v)) for n, v in outs_spec.items())))
+        hit = _PROGS.get((id(fn), key))
+        if hit is not None and hit[0] is fn:
+            _PROGS.move_to_end((id(fn), key))
+            prog, meta = hit[1], hit[2]
+        else:
+            prog, meta = build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree, btree)
+            _PROGS[(id(fn), key)] = (fn, prog, meta)
+            while len(_PROGS) > PROG_CACHE:
+                _PROGS.popitem(last=False)
+        return prog, meta, pi, bc, N, axes
+
+    def mapped(*args):
+        from . import backend as B
+        prog, meta, pi, bc, N, _ = prepare(args)
+        o = B.run(prog, pi, bc, N, opts)
+        res_out = {n: o.tallies[i].reshape(prog.tallies[i].shape) for i, n in enumerate(names)}
+        stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
+        ys = list(o.ys)
+        trunc = None
+        if prog.trunc is not None:
+            trunc = ys.pop()
+        stats["n_truncated"] = o.n_truncated
+        per_item = unflatten(meta["ytree"], ys)
+        return Result(res_out, per_item, trunc, stats)
+
+    mapped.__wrapped__ = fn
+    mapped._prepare = prepare
+    mapped._opts = opts
+    mapped._names = names
+    return mapped

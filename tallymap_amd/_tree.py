@@ -1,0 +1,68 @@
+"""Minimal pytrees for item carries and results: tuples, lists, dicts (sorted keys), None, and Tally (a node whose
+leaves are its per-output tally values)."""
+
+
+class TreeDef:
+    __slots__ = ("kind", "meta", "children")
+
+    def __init__(self, kind, meta, children):
+        self.kind, self.meta, self.children = kind, meta, children
+
+    def __eq__(self, o):
+        return (isinstance(o, TreeDef) and self.kind == o.kind and self.meta == o.meta
+                and self.children == o.children)
+
+    def __repr__(self):
+        return f"TreeDef({self.kind}, {self.meta}, {self.children})"
+
+
+def flatten(x):
+    from ._tally import Tally
+    if isinstance(x, Tally):
+        names = tuple(sorted(x._a))
+        return [x._a[n] for n in names], TreeDef("tally", (names, x._shapes_key()), [None] * len(names))
+    if isinstance(x, (tuple, list)):
+        leaves, kids = [], []
+        for c in x:
+            lv, td = flatten(c)
+            leaves += lv
+            kids.append(td)
+        return leaves, TreeDef(type(x).__name__, len(x), kids)
+    if isinstance(x, dict):
+        keys = tuple(sorted(x))
+        leaves, kids = [], []
+        for k in keys:
+            lv, td = flatten(x[k])
+            leaves += lv
+            kids.append(td)
+        return leaves, TreeDef("dict", keys, kids)
+    if x is None:
+        return [], TreeDef("none", None, [])
+    return [x], None
+
+
+def unflatten(td, leaves):
+    it = iter(leaves)
+    out = _build(td, it)
+    rest = list(it)
+    if rest:
+        raise ValueError("too many leaves for this tree")
+    return out
+
+
+def _build(td, it):
+    from ._tally import Tally
+    if td is None:
+        return next(it)
+    if td.kind == "tally":
+        names, shapes = td.meta
+        a = {n: next(it) for n in names}
+        return Tally._from(a, dict(shapes))
+    if td.kind in ("tuple", "list"):
+        xs = [_build(c, it) for c in td.children]
+        return tuple(xs) if td.kind == "tuple" else xs
+    if td.kind == "dict":
+        return {k: _build(c, it) for k, c in zip(td.meta, td.children)}
+    if td.kind == "none":
+        return None
+    raise ValueError(td.kind)

@@ -1,0 +1,157 @@
+"""The HIP kernel backend: run(prog, per-item operands, broadcast operands) on the current device and stream.
+
+The plugin point of the reference is `KB.run(p, pi, bc, target, ...)` (reference backends/kernel/__init__.py:135-185),
+called by `_primitive._run1` for the kernel platforms; this is its ROCm counterpart.  Operands are torch tensors on
+the GPU (numpy arrays are copied there); results are allocated with torch and filled by the kernels, which
+tm_launch queues on torch's current stream.  Device memory and streams come from torch; everything else is
+this package's code.  There is no CPU path: without a GPU or without libtallymap_rocm.so it raises.
+"""
+import collections
+import dataclasses
+import threading
+
+import numpy as np
+
+from . import compile as Cm
+from . import kernel as K
+
+_KERNELS = collections.OrderedDict()
+_LOCK = threading.Lock()
+KERNEL_CACHE = 256
+
+
+@dataclasses.dataclass
+class Compiled:
+    id: int
+    layout: object
+    block: int
+    src: str
+    tag: str
+
+
+@dataclasses.dataclass
+class Outputs:
+    tallies: list          # in prog.out_tallies order
+    stats: object          # int32[5]
+    ys: list               # per-item results (the truncation flag last when the program has a cap)
+    n_truncated: object    # int32 scalar (None: no cap)
+
+
+def torch_dtype(dt):
+    import torch
+    return {"float32": torch.float32, "float64": torch.float64, "int32": torch.int32, "uint32": torch.uint32,
+            "int64": torch.int64, "uint64": torch.uint64, "bool": torch.bool, "uint8": torch.uint8}[np.dtype(dt).name]
+
+
+def device_tensor(x, dtype):
+    """x as a contiguous tensor of `dtype` on the current GPU (a numpy array or scalar is copied there)."""
+    import torch
+    td = torch_dtype(dtype)
+    if not torch.cuda.is_available():
+        raise Cm.BackendError("tallymap_amd: no GPU is visible (torch.cuda.is_available() is False); the HIP backend "
+                              "has no CPU fallback")
+    if isinstance(x, torch.Tensor):
+        if x.device.type != "cuda":
+            x = x.to("cuda")
+        if x.dtype != td:
+            raise TypeError(f"tallymap_amd: operand dtype {x.dtype} != traced {td}")
+        return x.contiguous()
+    a = np.array(x, dtype=dtype, order="C")          # (keeps a 0-d scalar 0-d)
+    return torch.from_numpy(a).to("cuda")
+
+
+def compiled(prog, opts, adjoint=None):
+    """the registered kernel of prog under opts (in-memory LRU, then the disk cache, then hipRTC)."""
+    block = int(opts.get("block", K.BLOCK))
+    schedule = opts.get("schedule", "step")
+    refill = int(opts.get("refill", 1))
+    key = (prog.digest(), block, schedule, refill)
+    with _LOCK:
+        hit = _KERNELS.get(key)
+        if hit is not None:
+            _KERNELS.move_to_end(key)
+            return hit
+    src, L = K.build(prog, block=block, schedule=schedule, refill=refill)
+    img = Cm.code_object(src, name=f"tm_{prog.tag}.hip")
+    kid = int(Cm._key(src)[:15], 16)
+    Cm.check(Cm.lib().tm_register(kid, img, len(img), f"{prog.tag} {prog.where}".encode()))
+    c = Compiled(kid, L, block, src, prog.tag)
+    with _LOCK:
+        _KERNELS[key] = c
+        while len(_KERNELS) > KERNEL_CACHE:
+            _KERNELS.popitem(last=False)
+    return c
+
+
+def launch(c, ins, N, stream=None):
+    """allocate c's results and queue its kernels -> the result tensors (in layout order)."""
+    import ctypes
+
+    import torch
+    L = c.layout
+    outs = []
+    for shape, dt, per_item in L.res:
+        sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
+        outs.append(torch.empty(sh, dtype=torch_dtype(dt), device="cuda"))
+    bufs = [t.data_ptr() for t in ins] + [t.data_ptr() for t in outs]
+    arr = (ctypes.c_void_p * len(bufs))(*bufs)
+    s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), L.n_zero, L.flags, N, c.block))
+    return outs
+
+
+def run(prog, pi, bc, N, opts):
+    """the kernel backend's run(): outputs of prog over N items."""
+    c = compiled(prog, opts)
+    ins = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
+    ins += [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+    for x, a in zip(ins[:prog.nP], prog.p_avals()):
+        if tuple(x.shape) != (N,) + tuple(a.shape):
+            raise ValueError(f"tallymap_amd: per-item operand of shape {tuple(x.shape)}, expected {(N,) + a.shape}")
+    for x, a in zip(ins[prog.nP:], prog.b_avals()):
+        if tuple(x.shape) != tuple(a.shape):
+            raise ValueError(f"tallymap_amd: broadcast operand of shape {tuple(x.shape)}, expected {a.shape}")
+    res = launch(c, ins, N)
+    L = c.layout
+    base = L.n_in
+    tallies = [res[L.r_out[k] - base] for k in prog.out_tallies]
+    stats = res[L.r_stats - base]
+    ys = [res[r - base] for r in L.r_ys]
+    ntr = res[L.r_ctl - base][2:3].view(__import__("torch").int32)[0] if prog.trunc is not None else None
+    return Outputs(tallies, stats, ys, ntr)
+
+
+def kernel_info(c):
+    """tm_kernel_info of a compiled program: registers, private bytes, LDS bytes, blocks per CU, resident threads,
+    CUs, max threads per block, persistent grid."""
+    import ctypes
+    out = (ctypes.c_longlong * 8)()
+    Cm.check(Cm.lib().tm_kernel_info(c.id, c.block, out))
+    keys = ("regs", "private_bytes", "lds_bytes", "blocks_per_cu", "resident_threads", "cus", "max_threads", "grid")
+    return dict(zip(keys, [int(v) for v in out]))
+
+
+def prebuild(configs, n=64):
+    """compile (through hipRTC, no GPU needed) the forward and adjoint modules of each config in `configs`
+    ({name: dict(item, outputs, in_axes, max_steps)}) into the package's code-object cache -> [(name, tag, key)]."""
+    from .. import _core as C
+    from .._api import build_program
+    from .. import configs as CF
+    done = []
+    for name, cfg in configs.items():
+        args = getattr(CF, f"{name}_inputs")(n)
+        axes = cfg["in_axes"]
+        pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
+        bav = [C.AVal(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
+        prog, _ = build_program(cfg["item"], cfg["outputs"], axes, pav, bav, cfg["max_steps"])
+        progs = [prog]
+        try:
+            from . import reverse as R
+            progs.append(R.adjoint_program(prog, R.default_wrt(prog)))
+        except (ImportError, AttributeError):
+            pass
+        for p in progs:
+            src, _ = K.build(p, block=K.BLOCK, schedule="step", refill=1)
+            Cm.code_object(src, name=f"tm_{p.tag}.hip", store_pkg=True)
+            done.append((name, p.tag, Cm._key(src)[:16]))
+    return done

@@ -1,0 +1,591 @@
+"""IR -> HIP C++ statements (the emitter).
+
+Each IR value becomes a list of C expressions, one per element (row-major): values are scalars or small static
+arrays (a PRNG key is uint32[2]), so arrays are unrolled into straight-line code that stays in registers, and
+slice / squeeze / broadcast_in_dim / concatenate cost nothing.  Every computed element is bound once to a `const`
+local; while loops become C loops over mutable carry variables, conds become if / else.
+
+Float semantics (what the reference's CPU target computes, host.py:43-171; op_table.py:84-501):
+  + - * / and sqrt round to nearest, separately: the module is compiled with -ffp-contract=off and correctly
+  rounded f32 division and square root, denormals kept; lax max / min / div / rem / shifts / conversions follow
+  tm_device.h; transcendentals call tm_libm.h (restatements of glibc, checked against it on the host).
+"""
+import numpy as np
+
+from .. import _core as C
+
+
+class CodegenError(NotImplementedError):
+    pass
+
+
+CT = {"float32": "float", "float64": "double", "int32": "i32", "uint32": "u32", "int64": "i64", "uint64": "u64",
+      "bool": "bool", "uint8": "u8", "int8": "i8", "int16": "i16", "uint16": "u16"}
+
+
+def ctype(dt):
+    dt = np.dtype(dt)
+    if dt.name not in CT:
+        raise CodegenError(f"dtype {dt} is not supported by the HIP emitter")
+    return CT[dt.name]
+
+
+def lit(v, dt):
+    """an exact C literal of the scalar `v` as dtype dt."""
+    dt = np.dtype(dt)
+    v = np.asarray(v).astype(dt)[()]
+    if dt == C.BOOL:
+        return "true" if v else "false"
+    if dt in (C.F32, C.F64):
+        suf = "f" if dt == C.F32 else ""
+        ty = "float" if dt == C.F32 else "double"
+        f = float(v)
+        if np.isnan(f):
+            return f"__builtin_nan{'f' if dt == C.F32 else ''}(\"\")"
+        if np.isinf(f):
+            s = "__builtin_inff()" if dt == C.F32 else "__builtin_inf()"
+            return s if f > 0 else f"(-{s})"
+        if f == 0.0:
+            return f"(-0.0{suf})" if np.signbit(f) else f"0.0{suf}"
+        return f"(({ty}){f.hex()}{suf})" if dt == C.F32 else f"({f.hex()})"
+    if dt == C.I32:
+        i = int(v)
+        return "((i32)0x80000000u)" if i == -2 ** 31 else (f"({i})" if i < 0 else str(i))
+    if dt == C.U32:
+        return f"{int(v)}u"
+    if dt == C.I64:
+        i = int(v)
+        return "((i64)0x8000000000000000ull)" if i == -2 ** 63 else f"({i}ll)"
+    if dt == C.U64:
+        return f"{int(v)}ull"
+    return f"(({ctype(dt)}){int(v)})"
+
+
+class Val:
+    """an IR value in the emitter: C expressions per element."""
+    __slots__ = ("el", "shape", "dtype")
+
+    def __init__(self, el, shape, dtype):
+        self.el = list(el)
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+
+
+class VTally:
+    """a tally value: virtual (emits go to the accumulator of slot `slot`)."""
+    __slots__ = ("slot",)
+
+    def __init__(self, slot):
+        self.slot = slot
+
+
+_FLOATS = (C.F32, C.F64)
+
+
+def _isf(dt):
+    return np.dtype(dt) in _FLOATS
+
+
+def _isint(dt):
+    dt = np.dtype(dt)
+    return np.issubdtype(dt, np.integer)
+
+
+_UT = {"i32": "u32", "u32": "u32", "i64": "u64", "u64": "u64", "i8": "u8", "u8": "u8", "i16": "u16", "u16": "u16"}
+
+# f32 / f64 transcendentals with a checked restatement in tm_libm.h
+LIBM = {
+    ("erf_inv", "float"): "tm_erfinvf",
+}
+
+
+class Emitter:
+    """emits the equations of IR programs as C++ statements into self.lines."""
+
+    def __init__(self, hooks=None):
+        self.lines = []
+        self.ind = 1
+        self.n = 0
+        self.hooks = dict(hooks or {})      # prim -> rule(em, eqn, ins) (emit, ...: set by the kernel assembler)
+        self.prims = set()
+
+    # -------------------------------------------------------------------------------- text helpers
+    def fresh(self, p="t"):
+        self.n += 1
+        return f"{p}{self.n}"
+
+    def line(self, s):
+        self.lines.append("  " * self.ind + s)
+
+    def open(self, s):
+        self.line(s + " {")
+        self.ind += 1
+
+    def close(self, s="}"):
+        self.ind -= 1
+        self.line(s)
+
+    def bind(self, expr, dt, p="t"):
+        """const-bind one element expression -> its name."""
+        n = self.fresh(p)
+        self.line(f"const {ctype(dt)} {n} = {expr};")
+        return n
+
+    def declare(self, dt, init=None, p="m"):
+        n = self.fresh(p)
+        self.line(f"{ctype(dt)} {n}{'' if init is None else ' = ' + init};")
+        return n
+
+    # -------------------------------------------------------------------------------- programs
+    def value_of(self, env, v):
+        if isinstance(v, C.Lit):
+            dt = v.aval.dtype
+            return Val([lit(x, dt) for x in v.val.reshape(-1)], v.aval.shape, dt)
+        return env[v.id]
+
+    def run(self, jx, ins):
+        """emit jx with its invars bound to `ins` (Val | VTally) -> outvar Vals."""
+        env = {}
+        for v, x in zip(jx.invars, ins):
+            env[v.id] = x
+        for e in jx.eqns:
+            vals = [self.value_of(env, v) for v in e.invars]
+            outs = self.eqn(e, vals)
+            for o, x in zip(e.outvars, outs):
+                env[o.id] = x
+        return [self.value_of(env, v) for v in jx.outvars]
+
+    def eqn(self, e, ins):
+        self.prims.add(e.prim)
+        if e.prim in self.hooks:
+            r = self.hooks[e.prim](self, e, ins)
+        else:
+            rule = RULES.get(e.prim)
+            if rule is None:
+                if e.prim in EW:
+                    rule = _ew
+                else:
+                    raise CodegenError(f"primitive {e.prim!r} is not supported by the HIP emitter")
+            r = rule(self, e, ins)
+        return r if isinstance(r, list) else [r]
+
+
+# ------------------------------------------------------------------------------------------- rules
+def _bc(x, i, n):
+    """element i of x broadcast to n elements (a scalar repeats)."""
+    return x.el[0] if len(x.el) == 1 else x.el[i]
+
+
+def _iar(t, a, b, op):
+    w = _UT.get(t, t)
+    return f"(({t})(({w})({a}) {op} ({w})({b})))"
+
+
+def b_add(t, a):
+    if t in ("float", "double"):
+        return f"({a[0]} + {a[1]})"
+    if t == "bool":
+        return f"({a[0]} || {a[1]})"
+    return _iar(t, a[0], a[1], "+")
+
+
+def b_sub(t, a):
+    if t in ("float", "double"):
+        return f"({a[0]} - {a[1]})"
+    return _iar(t, a[0], a[1], "-")
+
+
+def b_mul(t, a):
+    if t in ("float", "double"):
+        return f"({a[0]} * {a[1]})"
+    if t == "bool":
+        return f"({a[0]} && {a[1]})"
+    return _iar(t, a[0], a[1], "*")
+
+
+def b_div(t, a):
+    if t in ("float", "double"):
+        return f"({a[0]} / {a[1]})"
+    return f"tm_idiv(({t})({a[0]}), ({t})({a[1]}))"
+
+
+def b_rem(t, a):
+    if t == "float":
+        return f"__builtin_fmodf({a[0]}, {a[1]})"
+    if t == "double":
+        return f"__builtin_fmod({a[0]}, {a[1]})"
+    return f"tm_irem(({t})({a[0]}), ({t})({a[1]}))"
+
+
+def b_max(t, a):
+    if t in ("float", "double"):
+        return f"tm_fmax<{t}>({a[0]}, {a[1]})"
+    if t == "bool":
+        return f"({a[0]} || {a[1]})"
+    return f"tm_imax<{t}>({a[0]}, {a[1]})"
+
+
+def b_min(t, a):
+    if t in ("float", "double"):
+        return f"tm_fmin<{t}>({a[0]}, {a[1]})"
+    if t == "bool":
+        return f"({a[0]} && {a[1]})"
+    return f"tm_imin<{t}>({a[0]}, {a[1]})"
+
+
+def b_neg(t, a):
+    if t in ("float", "double"):
+        return f"(-{a[0]})"
+    return f"(({t})(({_UT[t]})0 - ({_UT[t]})({a[0]})))"
+
+
+def b_abs(t, a):
+    if t == "float":
+        return f"__builtin_fabsf({a[0]})"
+    if t == "double":
+        return f"__builtin_fabs({a[0]})"
+    if t.startswith("u"):
+        return a[0]
+    return f"(({a[0]}) < 0 ? (({t})(({_UT[t]})0 - ({_UT[t]})({a[0]}))) : ({a[0]}))"
+
+
+def b_sign(t, a):
+    if t in ("float", "double"):
+        return f"tm_fsign<{t}>({a[0]})"
+    if t.startswith("u"):
+        return f"(({t})(({a[0]}) != 0))"
+    return f"(({t})((({a[0]}) > 0) - (({a[0]}) < 0)))"
+
+
+def b_floor(t, a):
+    return f"__builtin_floor{'f' if t == 'float' else ''}({a[0]})"
+
+
+def b_ceil(t, a):
+    return f"__builtin_ceil{'f' if t == 'float' else ''}({a[0]})"
+
+
+def b_sqrt(t, a):
+    return f"__builtin_sqrt{'f' if t == 'float' else ''}({a[0]})"
+
+
+def b_rsqrt(t, a):
+    one = "1.0f" if t == "float" else "1.0"
+    return f"({one} / __builtin_sqrt{'f' if t == 'float' else ''}({a[0]}))"
+
+
+def b_isfinite(t, a, ts):
+    return f"__builtin_isfinite({a[0]})"
+
+
+def _cmp(op):
+    return lambda t, a: f"({a[0]} {op} {a[1]})"
+
+
+def b_and(t, a):
+    return f"({a[0]} && {a[1]})" if t == "bool" else f"(({t})({a[0]} & {a[1]}))"
+
+
+def b_or(t, a):
+    return f"({a[0]} || {a[1]})" if t == "bool" else f"(({t})({a[0]} | {a[1]}))"
+
+
+def b_xor(t, a):
+    return f"({a[0]} != {a[1]})" if t == "bool" else f"(({t})({a[0]} ^ {a[1]}))"
+
+
+def b_not(t, a):
+    return f"(!{a[0]})" if t == "bool" else f"(({t})(~{a[0]}))"
+
+
+def b_shl(t, a):
+    return f"tm_shl<{t}, {_UT[t]}>({a[0]}, {a[1]})"
+
+
+def b_shrl(t, a):
+    return f"tm_shrl<{t}, {_UT[t]}>({a[0]}, {a[1]})"
+
+
+def b_shra(t, a):
+    return f"tm_shra<{t}, {_UT[t]}>({a[0]}, {a[1]})"
+
+
+def _lib(prim):
+    def b(t, a):
+        f = LIBM.get((prim, t))
+        if f is None:
+            raise CodegenError(f"{prim} of {t}: no checked implementation in tm_libm.h yet (the parity target is "
+                               "glibc's libm; an unchecked device function would silently break bit-exactness)")
+        return f"{f}({', '.join(a)})"
+    return b
+
+
+EW = {
+    "add": b_add, "sub": b_sub, "mul": b_mul, "div": b_div, "rem": b_rem, "max": b_max, "min": b_min,
+    "neg": b_neg, "abs": b_abs, "sign": b_sign, "floor": b_floor, "ceil": b_ceil, "sqrt": b_sqrt,
+    "rsqrt": b_rsqrt, "and": b_and, "or": b_or, "xor": b_xor, "not": b_not,
+    "eq": _cmp("=="), "ne": _cmp("!="), "lt": _cmp("<"), "le": _cmp("<="), "gt": _cmp(">"), "ge": _cmp(">="),
+    "shift_left": b_shl, "shift_right_logical": b_shrl, "shift_right_arithmetic": b_shra,
+    "erf_inv": _lib("erf_inv"), "exp": _lib("exp"), "log": _lib("log"), "log1p": _lib("log1p"),
+    "expm1": _lib("expm1"), "sin": _lib("sin"), "cos": _lib("cos"), "tan": _lib("tan"), "tanh": _lib("tanh"),
+    "atan2": _lib("atan2"), "pow": _lib("pow"), "logistic": _lib("logistic"),
+}
+
+
+def _ew(em, e, ins):
+    out = e.outvars[0].aval
+    t = ctype(out.dtype)
+    n = max(1, out.size)
+    rule = EW[e.prim]
+    # the operation's type: the operands' (a comparison's result is bool)
+    it = ctype(e.invars[0].aval.dtype)
+    at = it if e.prim in ("eq", "ne", "lt", "le", "gt", "ge") else t
+    res = []
+    for i in range(n):
+        args = [_bc(x, i, n) for x in ins]
+        res.append(em.bind(rule(at, args), out.dtype))
+    return Val(res, out.shape, out.dtype)
+
+
+RULES = {}
+
+
+def rule(*names):
+    def deco(f):
+        for n in names:
+            RULES[n] = f
+        return f
+    return deco
+
+
+@rule("integer_pow")
+def _ipow(em, e, ins):
+    """lax.integer_pow by binary exponentiation, as lax lowers it (acc = x on the first set bit, x squared per
+    bit; a negative exponent divides 1 by the result)."""
+    x = ins[0]
+    y = int(e.params["y"])
+    out = e.outvars[0].aval
+    t = ctype(out.dtype)
+    res = []
+    for i in range(max(1, out.size)):
+        xi = x.el[i] if len(x.el) > 1 else x.el[0]
+        if y == 0:
+            res.append(lit(1, out.dtype))
+            continue
+        neg, yy = y < 0, abs(y)
+        acc, cur = None, xi
+        while yy > 0:
+            if yy & 1:
+                acc = cur if acc is None else em.bind(b_mul(t, [acc, cur]), out.dtype)
+            yy >>= 1
+            if yy > 0:
+                cur = em.bind(b_mul(t, [cur, cur]), out.dtype)
+        if neg:
+            acc = em.bind(b_div(t, [lit(1, out.dtype), acc]), out.dtype)
+        res.append(acc)
+    return Val(res, out.shape, out.dtype)
+
+
+def conv(x, f, t):
+    """convert_element_type of one element from C type f to C type t."""
+    if f == t:
+        return x
+    if t == "bool":
+        return f"(({x}) != 0)"
+    if f == "bool":
+        return f"(({t})(({x}) ? 1 : 0))"
+    fl, tl = f in ("float", "double"), t in ("float", "double")
+    if fl and tl:
+        return f"(({t})({x}))"
+    if fl and not tl:
+        fn = {("float", "i32"): "tm_f2i32", ("float", "u32"): "tm_f2u32", ("double", "i32"): "tm_d2i32",
+              ("double", "u32"): "tm_d2u32", ("float", "i64"): "tm_f2i64", ("double", "i64"): "tm_d2i64"}.get((f, t))
+        if fn is None:
+            raise CodegenError(f"conversion {f} -> {t} is not supported")
+        return f"{fn}({x})"
+    return f"(({t})({x}))"
+
+
+@rule("convert_element_type")
+def _convert(em, e, ins):
+    x = ins[0]
+    out = e.outvars[0].aval
+    f, t = ctype(x.dtype), ctype(out.dtype)
+    if f == t:
+        return Val(x.el, out.shape, out.dtype)
+    return Val([em.bind(conv(a, f, t), out.dtype) for a in x.el], out.shape, out.dtype)
+
+
+@rule("bitcast_convert_type")
+def _bitcast(em, e, ins):
+    x = ins[0]
+    out = e.outvars[0].aval
+    t = ctype(out.dtype)
+    return Val([em.bind(f"__builtin_bit_cast({t}, {a})", out.dtype) for a in x.el], out.shape, out.dtype)
+
+
+@rule("select_n")
+def _select(em, e, ins):
+    p, cases = ins[0], ins[1:]
+    out = e.outvars[0].aval
+    n = max(1, out.size)
+    res = []
+    for i in range(n):
+        w = _bc(p, i, n)
+        cs = [_bc(c, i, n) for c in cases]
+        if p.dtype == C.BOOL:
+            ex = f"({w} ? {cs[1]} : {cs[0]})" if len(cs) == 2 else cs[0]
+        else:
+            ex = cs[-1]
+            for j in range(len(cs) - 2, -1, -1):
+                ex = f"({w} == {j} ? {cs[j]} : {ex})"
+        res.append(em.bind(ex, out.dtype))
+    return Val(res, out.shape, out.dtype)
+
+
+@rule("copy", "stop_gradient")
+def _copy(em, e, ins):
+    x = ins[0]
+    out = e.outvars[0].aval
+    if isinstance(x, VTally):
+        return x
+    return Val(x.el, out.shape, out.dtype)
+
+
+@rule("threefry2x32")
+def _threefry(em, e, ins):
+    a = [x.el[0] for x in ins]
+    o0, o1 = em.fresh("tf"), em.fresh("tf")
+    em.line(f"u32 {o0}, {o1};")
+    em.line(f"tm_threefry({a[0]}, {a[1]}, {a[2]}, {a[3]}, {o0}, {o1});")
+    return [Val([o0], (), C.U32), Val([o1], (), C.U32)]
+
+
+def _strides(shape):
+    st, s = [], 1
+    for d in reversed(shape):
+        st.append(s)
+        s *= d
+    return list(reversed(st))
+
+
+def _unravel(i, shape):
+    idx = []
+    for d in reversed(shape):
+        idx.append(i % d)
+        i //= d
+    return list(reversed(idx))
+
+
+@rule("slice")
+def _slice(em, e, ins):
+    x = ins[0]
+    out = e.outvars[0].aval
+    st = e.params["start_indices"]
+    strides = e.params.get("strides") or (1,) * len(st)
+    xs = _strides(x.shape)
+    res = []
+    for i in range(max(1, out.size)):
+        oi = _unravel(i, out.shape)
+        src = sum((s + o * k) * w for s, o, k, w in zip(st, oi, strides, xs))
+        res.append(x.el[src])
+    return Val(res, out.shape, out.dtype)
+
+
+@rule("squeeze", "reshape")
+def _reshape(em, e, ins):
+    x = ins[0]
+    out = e.outvars[0].aval
+    return Val(x.el, out.shape, out.dtype)
+
+
+@rule("broadcast_in_dim")
+def _bcast(em, e, ins):
+    x = ins[0]
+    out = e.outvars[0].aval
+    dims = e.params["broadcast_dimensions"]
+    xs = _strides(x.shape)
+    res = []
+    for i in range(max(1, out.size)):
+        oi = _unravel(i, out.shape)
+        src = sum((oi[d] if x.shape[k] != 1 else 0) * xs[k] for k, d in enumerate(dims))
+        res.append(x.el[src] if x.el else x.el[0])
+    return Val(res, out.shape, out.dtype)
+
+
+@rule("concatenate")
+def _concat(em, e, ins):
+    out = e.outvars[0].aval
+    if e.params["dimension"] != 0:
+        raise CodegenError("concatenate along a non-leading axis is not supported")
+    res = []
+    for x in ins:
+        res += x.el
+    return Val(res, out.shape, out.dtype)
+
+
+@rule("while")
+def _while(em, e, ins):
+    nc, nb = e.params["cond_nconsts"], e.params["body_nconsts"]
+    cc, bc, init = ins[:nc], ins[nc:nc + nb], ins[nc + nb:]
+    cj, bj = e.params["cond_jaxpr"], e.params["body_jaxpr"]
+    cars = []
+    for x, o in zip(init, e.outvars):
+        if isinstance(x, VTally):
+            cars.append(x)
+            continue
+        names = [em.declare(o.aval.dtype, a, "w") for a in x.el]
+        cars.append(Val(names, o.aval.shape, o.aval.dtype))
+    em.open("while (true)")
+    pred = em.run(cj, cc + cars)[0]
+    em.line(f"if (!({pred.el[0]})) break;")
+    outs = em.run(bj, bc + cars)
+    assign_carries(em, cars, outs)
+    em.close()
+    return cars
+
+
+def assign_carries(em, cars, outs):
+    """cars[j] = outs[j] for every non-tally carry, all at once: an output that reads another carry's variable
+    (a swap) is copied to a temporary first."""
+    names = {n for c in cars if not isinstance(c, VTally) for n in c.el}
+    pairs = []
+    for c, o in zip(cars, outs):
+        if isinstance(c, VTally):
+            continue
+        for n, a in zip(c.el, o.el):
+            if n != a:
+                pairs.append((n, a, c.dtype))
+    fixed = []
+    for n, a, dt in pairs:
+        if a in names:
+            a = em.bind(a, dt, "sw")
+        fixed.append((n, a))
+    for n, a in fixed:
+        em.line(f"{n} = {a};")
+
+
+@rule("cond")
+def _cond(em, e, ins):
+    idx = ins[0]
+    nco = e.params["nconsts"]
+    consts, ops = ins[1:1 + nco], ins[1 + nco:]
+    brs = e.params["branches"]
+    outs = []
+    for o in e.outvars:
+        outs.append(Val([em.declare(o.aval.dtype, None, "c") for _ in range(max(1, o.aval.size))],
+                        o.aval.shape, o.aval.dtype))
+    tally_out = {}
+    for j, br in enumerate(brs):
+        head = f"if ({idx.el[0]} == {j})" if j == 0 else (f"else if ({idx.el[0]} == {j})" if j < len(brs) - 1
+                                                          else "else")
+        em.open(head)
+        r = em.run(br, consts + ops)
+        for k, (ov, x) in enumerate(zip(outs, r)):
+            if isinstance(x, VTally):
+                tally_out[k] = x
+                continue
+            for n, a in zip(ov.el, x.el):
+                em.line(f"{n} = {a};")
+        em.close()
+    return [tally_out.get(k, ov) for k, ov in enumerate(outs)]

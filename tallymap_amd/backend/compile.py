@@ -1,0 +1,150 @@
+"""hipRTC compilation for gfx950 with an on-disk code-object cache, and the binding of libtallymap_rocm.so.
+
+The cache key is sha256(hipRTC library | arch | options | source) (reference backends/kernel/compile.py:30-35,
+160-173 keys NVRTC cubins the same way).  Two directories are searched: $TALLYMAP_CACHE (default
+~/.cache/tallymap_amd) and the package's own _kcache/ (filled by __graft_entry__.build(), so a fresh machine
+with the same toolchain finds the code objects of the benchmark programs without compiling).  New code objects are
+written to the first.
+
+Options: no FMA contraction, correctly rounded f32 division and square root, denormals kept (the reference's
+cuda_math='ieee' / CPU target, kernel.py:48-51, host.py:35); native float atomics; packed FP32 instructions
+disabled (-packed-fp32-ops).
+"""
+import ctypes
+import hashlib
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+CSRC = os.path.join(PKG, "csrc")
+SHIM = os.path.join(PKG, "libtallymap_rocm.so")
+KCACHE = os.path.join(PKG, "_kcache")
+ARCH = "gfx950"
+OPTS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
+        "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero", "-munsafe-fp-atomics",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+_LOCK = threading.Lock()
+_lib = None
+_paths = None
+
+
+class BackendError(RuntimeError):
+    pass
+
+
+def cache_dir():
+    d = os.environ.get("TALLYMAP_CACHE") or os.path.join(os.path.expanduser("~"), ".cache", "tallymap_amd")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def prelude():
+    """the device runtime text every module starts with (tm_device.h, tm_libm.h)."""
+    out = []
+    for f in ("tm_device.h", "tm_libm.h"):
+        with open(os.path.join(CSRC, f)) as fh:
+            out.append(fh.read().replace("#pragma once", ""))
+    return "\n".join(out)
+
+
+def _loaded_lib(name):
+    """the path of an already loaded shared library whose file name starts with `name` (from /proc/self/maps)."""
+    try:
+        with open("/proc/self/maps") as fh:
+            for ln in fh:
+                p = ln.split()[-1] if ln.strip() else ""
+                if os.path.basename(p).startswith(name) and os.path.exists(p):
+                    return p
+    except OSError:
+        pass
+    return None
+
+
+def runtime_paths():
+    """(HIP runtime, hipRTC) to bind: the ones torch loaded when torch is in the process (one HIP runtime per
+    process), else the system's."""
+    global _paths
+    if _paths is None:
+        hip = _loaded_lib("libamdhip64.so")
+        if hip is None:
+            try:
+                import torch  # noqa: F401  (its HIP runtime is the one tensors live in)
+                hip = _loaded_lib("libamdhip64.so")
+            except ImportError:
+                hip = None
+        rtc = None
+        if hip is not None:
+            cand = os.path.join(os.path.dirname(hip), "libhiprtc.so")
+            rtc = cand if os.path.exists(cand) else None
+        _paths = (hip or "/opt/rocm/lib/libamdhip64.so.7", rtc or "/opt/rocm/lib/libhiprtc.so.7")
+    return _paths
+
+
+def lib():
+    """libtallymap_rocm.so, bound to this process's HIP runtime.  Raises BackendError when it is not built: the
+    backend has no fallback."""
+    global _lib
+    with _LOCK:
+        if _lib is None:
+            if not os.path.exists(SHIM):
+                raise BackendError(f"tallymap_amd: {SHIM} is not built (run __graft_entry__.build() or "
+                                   "python -m tallymap_amd.build)")
+            L = ctypes.CDLL(SHIM)
+            vp, i, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
+            L.tm_init.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
+            L.tm_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), i,
+                                     ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp)]
+            L.tm_register.argtypes = [ll, ctypes.c_char_p, sz, ctypes.c_char_p]
+            L.tm_launch.argtypes = [ll, vp, ctypes.POINTER(vp), i, i, i, ll, i]
+            L.tm_kernel_info.argtypes = [ll, i, ctypes.POINTER(ll)]
+            L.tm_last_error.restype = ctypes.c_char_p
+            L.tm_free.argtypes = [vp]
+            hip, rtc = runtime_paths()
+            if L.tm_init(hip.encode(), rtc.encode()):
+                raise BackendError(L.tm_last_error().decode())
+            _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc:
+        raise BackendError(lib().tm_last_error().decode())
+
+
+def _key(src):
+    rtc = runtime_paths()[1]
+    h = hashlib.sha256()
+    h.update(f"{os.path.realpath(rtc)}|{os.path.getsize(rtc) if os.path.exists(rtc) else 0}|{ARCH}|"
+             f"{' '.join(OPTS)}|".encode())
+    h.update(src.encode())
+    return h.hexdigest()
+
+
+def code_object(src, name="tm_program", store_pkg=False):
+    """the gfx950 code object of `src`: from a cache, else compiled with hipRTC and cached."""
+    k = _key(src)
+    for d in (cache_dir(), KCACHE):
+        p = os.path.join(d, k + ".co")
+        if os.path.exists(p):
+            with open(p, "rb") as fh:
+                return fh.read()
+    L = lib()
+    opts = (ctypes.c_char_p * len(OPTS))(*[o.encode() for o in OPTS])
+    img, n, log = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_void_p()
+    rc = L.tm_compile(src.encode(), name.encode(), opts, len(OPTS), ctypes.byref(img), ctypes.byref(n),
+                      ctypes.byref(log))
+    if log.value:
+        L.tm_free(log)
+    if rc:
+        raise BackendError(L.tm_last_error().decode())
+    data = ctypes.string_at(img, n.value)
+    L.tm_free(img)
+    dirs = [cache_dir()] + ([KCACHE] if store_pkg else [])
+    for d in dirs:
+        os.makedirs(d, exist_ok=True)
+        tmp = os.path.join(d, f"{k}.co.tmp{os.getpid()}")
+        with open(tmp, "wb") as fh:
+            fh.write(data)
+        os.replace(tmp, os.path.join(d, k + ".co"))
+    return data

@@ -1,0 +1,411 @@
+"""One HIP module per item program: tm_zero, tm_main (the persistent item loop) and tm_post (readout / poison).
+
+Buffers (one by-value struct of pointers, TmParams; the item count is a kernel argument, so one code object serves
+every N):
+    inputs  [per-item operands][broadcast operands]
+    results [sum tallies][exact scratch of each exact tally][ctl u32[8]][stats i32[5]] | [per-item results]
+The first group of results (up to stats) is zeroed by tm_zero before tm_main runs: the reference's n_zero
+(reference backends/kernel/kernel.py:565-591, shim.cc:215-218).  ctl holds the claim counter (u64, words 0-1) and
+the count of truncated items (word 2).
+
+tm_main is the hand-written CDNA4 loop (reference kernel.py:812-838 is the CUDA one it replaces):
+  * a persistent grid (256 CUs x achieved occupancy), block BLOCK = 256 (4 wave64s);
+  * step-granular refill (the reference's schedule='step', kernel.py:239-295, 469-563): each loop iteration, the
+    lanes of a wave whose item has finished are counted with one ballot, and the wave claims that many
+    consecutive items with ONE atomic (mbcnt gives each idle lane its rank); a lane then runs its item's `pre`,
+    and every live lane runs one (cond, body) step or, when the predicate fails, `post` and writes its per-item
+    results.  A lane never waits for its wave's longest item;
+  * small tallies privatised in LDS (up to LDS_BYTES per block), flushed once at exit with device atomics;
+    larger ones take the global atomic directly;
+  * dropped emits and truncations counted in registers, one atomic per lane at exit.
+Programs without exactly one top-level while loop run the item schedule (a lane runs its whole item per claim).
+"""
+import dataclasses
+
+import numpy as np
+
+from .. import _core as C
+from .codegen import Emitter, Val, VTally, assign_carries, ctype, lit
+
+BLOCK = 256
+LDS_BYTES = 32768          # privatised tallies per block (MI355X: 160 KB LDS per CU)
+XW = 5                     # int64 words per exact bin
+
+
+@dataclasses.dataclass
+class Layout:
+    n_in: int
+    res: list              # (shape, dtype, per_item) per result buffer
+    n_zero: int
+    r_out: dict            # tally slot -> result index (absolute buffer index)
+    r_ctl: int
+    r_stats: int
+    r_ys: list
+    flags: int             # bit1: launch tm_post
+    mode: str
+    priv: list
+    zero_words: list       # (buffer index, u32 words) zeroed by tm_zero
+
+
+def _split(jx):
+    """-> (index of the only top-level while eqn) or None."""
+    ws = [i for i, e in enumerate(jx.eqns) if e.prim == "while"]
+    return ws[0] if len(ws) == 1 else None
+
+
+def _used_vars(eqns, outvars):
+    s = set()
+    for e in eqns:
+        for v in e.invars:
+            if isinstance(v, C.Var):
+                s.add(v.id)
+        for sub in C.subjaxprs(e):
+            s |= _free_vars(sub)
+    for v in outvars:
+        if isinstance(v, C.Var):
+            s.add(v.id)
+    return s
+
+
+def _free_vars(jx):
+    defined = {v.id for v in jx.invars}
+    free = set()
+    for e in jx.eqns:
+        for v in e.invars:
+            if isinstance(v, C.Var) and v.id not in defined:
+                free.add(v.id)
+        for o in e.outvars:
+            defined.add(o.id)
+    return free
+
+
+def exact_words(S):
+    """u32 words of an exact tally's scratch: XW int64 words per bin, then one flag bit per bin."""
+    return 2 * XW * S + (S + 31) // 32
+
+
+def build(prog, block=BLOCK, schedule="step", refill=1, adjoint=None):
+    """-> (HIP source, Layout) of prog's module.  `adjoint`: a backend.reverse.Adjoint (the replay kernel) or
+    None."""
+    jx = prog.jaxpr
+    nT, nP, nB = prog.nT, prog.nP, prog.nB
+    pav, bav = prog.p_avals(), prog.b_avals()
+    yav = prog.y_avals()
+    n_in = nP + nB
+    res = []
+
+    def result(shape, dt, per_item=False):
+        res.append((tuple(shape), np.dtype(dt), per_item))
+        return n_in + len(res) - 1
+    outs = prog.out_tallies
+    r_out = {k: result(prog.tallies[k].shape, prog.tallies[k].dtype) for k in outs}
+    r_scr = {k: result((exact_words(prog.tallies[k].S),), np.uint32) for k in outs if prog.tallies[k].exact}
+    r_ctl = result((8,), np.uint32)
+    r_stats = result((5,), np.int32)
+    n_zero = len(res)
+    r_ys = [result(a.shape, a.dtype, per_item=True) for a in yav]
+    R = n_in + len(res)
+
+    # ------------------------------------------------------------------------------- privatisation plan
+    priv = []
+    budget = LDS_BYTES
+    for k in outs:
+        s = prog.tallies[k]
+        nbytes = s.S * (8 * XW if s.exact else 4)
+        if s.dtype not in (C.F32, C.I32, C.U32) and not s.exact:
+            continue
+        if nbytes <= budget:
+            budget -= nbytes
+            priv.append(k)
+
+    em = Emitter()
+
+    def emit_rule(em_, e, ins):
+        t, idx, val = ins
+        k = t.slot
+        s = prog.tallies[k]
+        if s.kind == "discard":
+            return t
+        ei = em_.bind(idx.el[0], np.int32, "ei")
+        em_.open(f"if ((u32){ei} >= {s.S}u)")
+        em_.line("++tm_drop;")
+        em_.close("} else {")
+        em_.ind += 1
+        v = val.el[0]
+        if s.exact:
+            acc = f"tm_xsh{k}" if k in priv else f"((u64*)P.p[{r_scr[k]}])"
+            fl = f"tm_xfl{k}" if k in priv else f"((u32*)P.p[{r_scr[k]}] + {2 * XW * s.S})"
+            em_.line(f"if (tm_xemit(&{acc}[(i64){ei} * {XW}], {v})) atomicOr(&{fl}[{ei} >> 5], 1u << ({ei} & 31));")
+        elif s.dtype == C.F32:
+            if k in priv:
+                em_.line(f"tm_ladd_f32(&tm_sh{k}[{ei}], {v});")
+            else:
+                em_.line(f"tm_gadd_f32(&((float*)P.p[{r_out[k]}])[{ei}], {v});")
+        elif s.dtype in (C.I32, C.U32):
+            ct = ctype(s.dtype)
+            dst = f"tm_sh{k}" if k in priv else f"(({ct}*)P.p[{r_out[k]}])"
+            em_.line(f"atomicAdd(&{dst}[{ei}], {v});")
+        else:
+            raise NotImplementedError(f"sum output of dtype {s.dtype}")
+        em_.close()
+        return t
+    em.hooks["tallymap_emit"] = emit_rule
+
+    # --------------------------------------------------------------------------------- the item's code
+    w = _split(jx) if schedule == "step" else None
+    mode = "step" if w is not None else "item"
+    tallies = [VTally(k) for k in range(nT)]
+    bvals = []
+    for i, a in enumerate(bav):
+        ct = ctype(a.dtype)
+        bvals.append(Val([f"tm_b{i}_{e}" for e in range(max(1, a.size))], a.shape, a.dtype))
+
+    def load_pi(i, a):
+        ct = ctype(a.dtype)
+        n = max(1, a.size)
+        return Val([f"(({'const ' + ct}*)P.p[{i}])[tm_item * {n} + {e}]" for e in range(n)], a.shape, a.dtype)
+
+    decls, pre_lines, step_lines, post_lines = [], [], [], []
+    ys_write = []
+
+    def write_ys(vals, trunc_idx):
+        lines = []
+        for j, (v, a) in enumerate(zip(vals, yav)):
+            ct = ctype(a.dtype)
+            n = max(1, a.size)
+            for e in range(n):
+                lines.append(f"(({ct}*)P.p[{r_ys[j]}])[tm_item * {n} + {e}] = {v.el[e]};")
+        if trunc_idx is not None:
+            lines.append(f"if ({vals[trunc_idx].el[0]}) ++tm_ntr;")
+        return lines
+
+    if mode == "item":
+        em.lines, em.ind = [], 4
+        pis = []
+        for i, a in enumerate(pav):
+            lv = load_pi(i, a)
+            pis.append(Val([em.bind(x, a.dtype, "x") for x in lv.el], a.shape, a.dtype))
+        outv = em.run(jx, tallies + pis + bvals)
+        for ln in write_ys(outv[nT:], prog.trunc):
+            em.line(ln)
+        pre_lines = em.lines
+    else:
+        we = jx.eqns[w]
+        pre_e, post_e = jx.eqns[:w], jx.eqns[w + 1:]
+        nc, nb = we.params["cond_nconsts"], we.params["body_nconsts"]
+        ops = we.invars
+        cc_v, bc_v, init_v = ops[:nc], ops[nc:nc + nb], ops[nc + nb:]
+        post_used = _used_vars(post_e, jx.outvars)
+        loop_used = {v.id for v in cc_v + bc_v if isinstance(v, C.Var)}
+        bids = {v.id for v in jx.invars[nT + nP:]}
+        # ---- pre: loads + pre eqns -> carries and persistent state
+        em.lines, em.ind = [], 5
+        env = {}
+        for v, t in zip(jx.invars[:nT], tallies):
+            env[v.id] = t
+        for i, (v, a) in enumerate(zip(jx.invars[nT:nT + nP], pav)):
+            lv = load_pi(i, a)
+            env[v.id] = Val([em.bind(x, a.dtype, "x") for x in lv.el], a.shape, a.dtype)
+        for v, bv in zip(jx.invars[nT + nP:], bvals):
+            env[v.id] = bv
+        for e in pre_e:
+            vals = [em.value_of(env, x) for x in e.invars]
+            for o, x in zip(e.outvars, em.eqn(e, vals)):
+                env[o.id] = x
+        # persistent values: defined before the loop (per-item inputs included), read by the loop or post
+        state = {}
+        need = (loop_used | post_used)
+        cand = [v for v in jx.invars[nT:nT + nP]] + [o for e in pre_e for o in e.outvars]
+        for v in cand:
+            if v.id in need and v.id not in bids and not isinstance(env.get(v.id), VTally):
+                x = env[v.id]
+                names = []
+                for j, el in enumerate(x.el):
+                    nm = f"tm_s{len(state)}_{j}"
+                    names.append(nm)
+                    decls.append(f"  {ctype(x.dtype)} {nm};")
+                    em.line(f"{nm} = {el};")
+                state[v.id] = Val(names, x.shape, x.dtype)
+        cars = []
+        for j, (v, o) in enumerate(zip(init_v, we.outvars)):
+            x = em.value_of(env, v)
+            if isinstance(x, VTally):
+                cars.append(x)
+                continue
+            names = []
+            for e_, el in enumerate(x.el):
+                nm = f"tm_c{j}_{e_}"
+                names.append(nm)
+                decls.append(f"  {ctype(o.aval.dtype)} {nm};")
+                em.line(f"{nm} = {el};")
+            cars.append(Val(names, o.aval.shape, o.aval.dtype))
+        pre_lines = em.lines
+
+        def sval(v):
+            if isinstance(v, C.Lit):
+                return em.value_of({}, v)
+            if v.id in bids:
+                return env[v.id]
+            if v.id in state:
+                return state[v.id]
+            x = env.get(v.id)
+            if isinstance(x, VTally):
+                return x
+            raise RuntimeError("internal: a loop operand is neither state nor broadcast")
+        # ---- one step: cond; body or post
+        em.lines, em.ind = [], 3
+        pr = em.run(we.params["cond_jaxpr"], [sval(v) for v in cc_v] + cars)[0]
+        em.open(f"if ({pr.el[0]})")
+        bouts = em.run(we.params["body_jaxpr"], [sval(v) for v in bc_v] + cars)
+        assign_carries(em, cars, bouts)
+        em.close("} else {")
+        em.ind += 1
+        penv = {}
+        for v in jx.invars[:nT]:
+            penv[v.id] = env[v.id]
+        for v in jx.invars[nT + nP:]:
+            penv[v.id] = env[v.id]
+        for vid, x in state.items():
+            penv[vid] = x
+        for o, c in zip(we.outvars, cars):
+            penv[o.id] = c
+        for e in post_e:
+            vals = [em.value_of(penv, x) for x in e.invars]
+            for o, x in zip(e.outvars, em.eqn(e, vals)):
+                penv[o.id] = x
+        outv = [em.value_of(penv, v) for v in jx.outvars]
+        for ln in write_ys(outv[nT:], prog.trunc):
+            em.line(ln)
+        em.line("tm_live = false;")
+        em.close()
+        step_lines = em.lines
+
+    # ------------------------------------------------------------------------------------ assemble
+    from . import compile as Cm
+    src = [Cm.prelude(), f"struct TmParams {{ void* p[{R}]; }};",
+           f"#define TM_STATS ((i32*)P.p[{r_stats}])", f"#define TM_CTL ((u32*)P.p[{r_ctl}])"]
+    zero_words = []
+    for k in outs:
+        s = prog.tallies[k]
+        zero_words.append((r_out[k], s.S * np.dtype(s.dtype).itemsize // 4 if np.dtype(s.dtype).itemsize >= 4
+                           else (s.S * np.dtype(s.dtype).itemsize + 3) // 4))
+        if k in r_scr:
+            zero_words.append((r_scr[k], exact_words(s.S)))
+    zero_words += [(r_ctl, 8), (r_stats, 5)]
+    zl = []
+    for b, nw in zero_words:
+        zl.append(f"  for (i64 i = g; i < {nw}; i += s) ((u32*)P.p[{b}])[i] = 0u;")
+    src.append("extern \"C\" __global__ void tm_zero(const TmParams P, const i64 n_items) {\n"
+               "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, s = (i64)gridDim.x * blockDim.x;\n"
+               + "\n".join(zl) + "\n}")
+    # tm_post: exact readout, then the truncation poison of float tallies
+    post = []
+    flags = 0
+    for k in outs:
+        s = prog.tallies[k]
+        if s.exact:
+            words = f"((const u64*)P.p[{r_scr[k]}])"
+            fl = f"((const u32*)P.p[{r_scr[k]}] + {2 * XW * s.S})"
+            post.append(f"for (i64 i = g; i < {s.S}; i += st) {{ bool bad = false; "
+                        f"const float o = tm_xread(&{words}[i * {XW}], &bad); "
+                        f"const bool f = (({fl}[i >> 5] >> (i & 31)) & 1u) != 0u; "
+                        f"if (f || bad) atomicAdd(&TM_STATS[3], 1); "
+                        f"((float*)P.p[{r_out[k]}])[i] = (f || bad) ? __builtin_nanf(\"\") : o; }}")
+    poison = [k for k in outs if prog.tallies[k].dtype in (C.F32, C.F64)]
+    if prog.trunc is not None and poison:
+        # (the readout and the poison visit a bin from the same thread, in program order)
+        for k in poison:
+            s = prog.tallies[k]
+            ct = ctype(s.dtype)
+            post.append(f"if (TM_CTL[2] != 0u) for (i64 i = g; i < {s.S}; i += st) "
+                        f"(({ct}*)P.p[{r_out[k]}])[i] = __builtin_nanf(\"\");")
+    if post:
+        flags |= 2
+        src.append("extern \"C\" __global__ void tm_post(const TmParams P, const i64 n_items) {\n"
+                   "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, st = (i64)gridDim.x * blockDim.x;\n  "
+                   + "\n  ".join(post) + "\n}")
+
+    # tm_main
+    body = []
+    body.append(f"extern \"C\" __global__ void __launch_bounds__({block}) tm_main(const TmParams P, "
+                "const i64 n_items) {")
+    body.append("  u64* const tm_ctr = (u64*)P.p[%d];" % r_ctl)
+    for k in priv:
+        s = prog.tallies[k]
+        if s.exact:
+            nw = XW * s.S
+            body.append(f"  __shared__ u64 tm_xsh{k}[{nw}];")
+            body.append(f"  __shared__ u32 tm_xfl{k}[{(s.S + 31) // 32}];")
+            body.append(f"  for (int i = threadIdx.x; i < {nw}; i += blockDim.x) tm_xsh{k}[i] = 0ull;")
+            body.append(f"  for (int i = threadIdx.x; i < {(s.S + 31) // 32}; i += blockDim.x) tm_xfl{k}[i] = 0u;")
+        else:
+            ct = ctype(s.dtype)
+            body.append(f"  __shared__ {ct} tm_sh{k}[{s.S}];")
+            body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) tm_sh{k}[i] = ({ct})0;")
+    if priv:
+        body.append("  __syncthreads();")
+    for i, a in enumerate(bav):
+        ct = ctype(a.dtype)
+        for e in range(max(1, a.size)):
+            body.append(f"  const {ct} tm_b{i}_{e} = ((const {ct}*)P.p[{nP + i}])[{e}];")
+    body.append("  bool tm_live = false, tm_more = true;")
+    body.append("  i64 tm_item = 0;")
+    body.append("  i32 tm_drop = 0;")
+    body.append("  u32 tm_ntr = 0;")
+    body += decls
+    body.append("  while (true) {")
+    body.append("    if (tm_more) {")
+    body.append("      const u64 tm_need = tm_ballot(!tm_live);")
+    if mode == "step" and refill > 1:
+        body.append(f"      if (tm_need != 0ull && (__builtin_popcountll(tm_need) >= {int(refill)} || "
+                    "tm_ballot(tm_live) == 0ull)) {")
+    else:
+        body.append("      if (tm_need != 0ull) {")
+    body.append("        const u32 tm_n = (u32)__builtin_popcountll(tm_need);")
+    body.append("        const u64 tm_base = tm_claim(tm_ctr, tm_n);")
+    body.append("        if (tm_base + tm_n >= (u64)n_items) tm_more = false;")
+    body.append("        if (!tm_live) {")
+    body.append("          const u64 tm_t = tm_base + tm_rank(tm_need);")
+    body.append("          if (tm_t < (u64)n_items) {")
+    body.append("            tm_item = (i64)tm_t;")
+    body.append("            tm_live = true;")
+    body += pre_lines
+    if mode == "item":
+        body.append("            tm_live = false;")
+    body.append("          }")
+    body.append("        }")
+    body.append("      }")
+    body.append("    }")
+    body.append("    if (!tm_live) {")
+    body.append("      if (!tm_more) break;")
+    body.append("      continue;")
+    body.append("    }")
+    body += step_lines
+    body.append("  }")
+    body.append("  if (tm_drop) atomicAdd(&TM_STATS[4], tm_drop);")
+    body.append("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")
+    if priv:
+        body.append("  __syncthreads();")
+        for k in priv:
+            s = prog.tallies[k]
+            if s.exact:
+                nw = XW * s.S
+                gw = f"((u64*)P.p[{r_scr[k]}])"
+                gf = f"((u32*)P.p[{r_scr[k]}] + {2 * XW * s.S})"
+                body.append(f"  for (int i = threadIdx.x; i < {nw}; i += blockDim.x) {{ const i64 x = (i64)tm_xsh{k}[i]; "
+                            f"if (x != 0 && tm_xadd(&{gw}[i / {XW} * {XW}], i % {XW}, x)) "
+                            f"atomicOr(&{gf}[(i / {XW}) >> 5], 1u << ((i / {XW}) & 31)); }}")
+                body.append(f"  for (int i = threadIdx.x; i < {(s.S + 31) // 32}; i += blockDim.x) "
+                            f"if (tm_xfl{k}[i]) atomicOr(&{gf}[i], tm_xfl{k}[i]);")
+            elif s.dtype == C.F32:
+                body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const float x = tm_sh{k}[i]; "
+                            f"if (x != 0.0f) tm_gadd_f32(&((float*)P.p[{r_out[k]}])[i], x); }}")
+            else:
+                ct = ctype(s.dtype)
+                body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const {ct} x = tm_sh{k}[i]; "
+                            f"if (x != 0) atomicAdd(&(({ct}*)P.p[{r_out[k]}])[i], x); }}")
+    body.append("}")
+    src.append("\n".join(body))
+    L = Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_out, r_ctl=r_ctl, r_stats=r_stats, r_ys=r_ys,
+               flags=flags, mode=mode, priv=priv, zero_words=zero_words)
+    return "\n".join(src) + "\n", L

@@ -1,0 +1,261 @@
+// tm_device.h -- the CDNA4 device runtime of generated tallymap kernels (gfx950, wave64).
+//
+// Every generated module is this header + tm_libm.h + the program's own code (backend/codegen.py, kernel.py).  The
+// scalar helpers are TM_FN (host + device) so that the same definitions can be compiled for the host and checked
+// there; the wave-level pieces (claims, atomics, LDS) are device-only.
+//
+// Semantics restated from the reference's device prelude (tallymap/backends/kernel/kernel.py:26-188) and its CPU
+// target (host.py:43-171), written for AMD hardware:
+//   - lax max/min: NaN-propagating, a signed-zero tie gives +0 / -0 (kernel.py:78-83);
+//   - lax integer div/rem: x/0 = -1 (unsigned: all ones), INT_MIN/-1 = INT_MIN; x%0 = x, INT_MIN%-1 = 0
+//     (kernel.py:95-103);
+//   - shifts by >= the width give 0 (logical) or the sign fill (arithmetic) (kernel.py:104-109);
+//   - float -> int toward zero, saturating, NaN -> 0 (host.py:133-146; v_cvt_i32_f32 behaves so natively);
+//   - threefry2x32, 20 rounds (kernel.py:137-150; Salmon et al. 2011);
+//   - the subnormal-safe f32 atomic add: |v| >= 2^-102 (or non-finite) takes the native atomic, a smaller
+//     nonzero v a compare-and-swap loop of the IEEE add, +-0 is skipped (kernel.py:112-135);
+//   - the exact f32 sum: a bin is 5 signed int64 words of weight 2^(63 j); an emit adds <= 2 pieces with int64
+//     atomics and carries +-2 into the next word on overflow; the readout rounds once (kernel.py:870-941).
+#pragma once
+
+typedef signed char i8;
+typedef unsigned char u8;
+typedef short i16;
+typedef unsigned short u16;
+typedef int i32;
+typedef unsigned int u32;
+typedef long long i64;
+typedef unsigned long long u64;
+
+#ifdef __HIPCC_RTC__
+#define TM_DEVICE_ONLY 1
+#endif
+#if defined(__HIP__) || defined(__HIPCC_RTC__)
+#define TM_FN __host__ __device__ __forceinline__
+#define TM_DFN __device__ __forceinline__
+#define TM_DNOINLINE __device__ __noinline__
+#else
+#define TM_FN static inline
+#endif
+
+template <class To, class From> TM_FN To tm_bitcast(From x) { return __builtin_bit_cast(To, x); }
+TM_FN float tm_u2f(u32 u) { return __builtin_bit_cast(float, u); }
+TM_FN u32 tm_f2u(float f) { return __builtin_bit_cast(u32, f); }
+TM_FN double tm_u2d(u64 u) { return __builtin_bit_cast(double, u); }
+TM_FN u64 tm_d2u(double d) { return __builtin_bit_cast(u64, d); }
+
+// ------------------------------------------------------------------------------------------- lax helpers
+template <class T> TM_FN T tm_fmax(T a, T b) {
+  return (a > b || a != a) ? a : ((b > a || b != b) ? b : (a == (T)0 ? a + b : a));
+}
+template <class T> TM_FN T tm_fmin(T a, T b) {
+  return (a < b || a != a) ? a : ((b < a || b != b) ? b : (a == (T)0 ? -(-a - b) : a));
+}
+template <class T> TM_FN T tm_imax(T a, T b) { return a > b ? a : b; }
+template <class T> TM_FN T tm_imin(T a, T b) { return a < b ? a : b; }
+template <class T> TM_FN T tm_fsign(T a) { return a > (T)0 ? (T)1 : (a < (T)0 ? (T)-1 : a); }
+
+TM_FN i32 tm_idiv(i32 a, i32 b) { return b == 0 ? -1 : ((b == -1 && a == (i32)0x80000000u) ? a : a / b); }
+TM_FN i32 tm_irem(i32 a, i32 b) { return b == 0 ? a : ((b == -1 && a == (i32)0x80000000u) ? 0 : a % b); }
+TM_FN u32 tm_idiv(u32 a, u32 b) { return b == 0u ? 0xffffffffu : a / b; }
+TM_FN u32 tm_irem(u32 a, u32 b) { return b == 0u ? a : a % b; }
+TM_FN i64 tm_idiv(i64 a, i64 b) {
+  return b == 0 ? -1 : ((b == -1 && a == (i64)0x8000000000000000ull) ? a : a / b);
+}
+TM_FN i64 tm_irem(i64 a, i64 b) {
+  return b == 0 ? a : ((b == -1 && a == (i64)0x8000000000000000ull) ? 0 : a % b);
+}
+
+template <class T, class U> TM_FN T tm_shl(T a, T b) {
+  return ((U)b >= (U)(sizeof(T) * 8)) ? (T)0 : (T)((U)a << (U)b);
+}
+template <class T, class U> TM_FN T tm_shrl(T a, T b) {
+  return ((U)b >= (U)(sizeof(T) * 8)) ? (T)0 : (T)((U)a >> (U)b);
+}
+template <class T, class U> TM_FN T tm_shra(T a, T b) {
+  return ((U)b >= (U)(sizeof(T) * 8)) ? (T)(a < (T)0 ? (T)-1 : (T)0) : (T)(a >> (U)b);
+}
+
+// float -> integer toward zero, saturating, NaN -> 0
+TM_FN i32 tm_f2i32(float x) {
+  return x != x ? 0 : (x <= -2147483648.0f ? (i32)0x80000000u : (x >= 2147483648.0f ? 0x7fffffff : (i32)x));
+}
+TM_FN u32 tm_f2u32(float x) {
+  return x != x ? 0u : (x <= 0.0f ? 0u : (x >= 4294967296.0f ? 0xffffffffu : (u32)x));
+}
+TM_FN i32 tm_d2i32(double x) {
+  return x != x ? 0 : (x <= -2147483648.0 ? (i32)0x80000000u : (x >= 2147483647.0 ? 0x7fffffff : (i32)x));
+}
+TM_FN u32 tm_d2u32(double x) {
+  return x != x ? 0u : (x <= 0.0 ? 0u : (x >= 4294967295.0 ? 0xffffffffu : (u32)x));
+}
+TM_FN i64 tm_f2i64(float x) {
+  return x != x ? 0 : (x <= -9223372036854775808.0f ? (i64)0x8000000000000000ull
+                                                     : (x >= 9223372036854775808.0f ? 0x7fffffffffffffffll : (i64)x));
+}
+TM_FN i64 tm_d2i64(double x) {
+  return x != x ? 0 : (x <= -9223372036854775808.0 ? (i64)0x8000000000000000ull
+                                                    : (x >= 9223372036854775808.0 ? 0x7fffffffffffffffll : (i64)x));
+}
+
+// ----------------------------------------------------------------------------------------- threefry2x32
+TM_FN u32 tm_rotl(u32 x, int d) { return (x << d) | (x >> (32 - d)); }
+
+TM_FN void tm_threefry(u32 k0, u32 k1, u32 c0, u32 c1, u32& o0, u32& o1) {
+  const u32 k2 = k0 ^ k1 ^ 0x1BD11BDAu;
+  u32 x0 = c0 + k0, x1 = c1 + k1;
+#define TM_TFR(r) x0 += x1; x1 = tm_rotl(x1, r); x1 ^= x0;
+  TM_TFR(13) TM_TFR(15) TM_TFR(26) TM_TFR(6)  x0 += k1; x1 += k2 + 1u;
+  TM_TFR(17) TM_TFR(29) TM_TFR(16) TM_TFR(24) x0 += k2; x1 += k0 + 2u;
+  TM_TFR(13) TM_TFR(15) TM_TFR(26) TM_TFR(6)  x0 += k0; x1 += k1 + 3u;
+  TM_TFR(17) TM_TFR(29) TM_TFR(16) TM_TFR(24) x0 += k1; x1 += k2 + 4u;
+  TM_TFR(13) TM_TFR(15) TM_TFR(26) TM_TFR(6)  x0 += k2; x1 += k0 + 5u;
+#undef TM_TFR
+  o0 = x0;
+  o1 = x1;
+}
+
+#if defined(__HIP__) || defined(__HIPCC_RTC__)
+// ============================================================================================ device only
+// lane and wave helpers (wave64)
+TM_DFN int tm_lane() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+TM_DFN u64 tm_ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+TM_DFN u32 tm_rank(u64 mask) {     // set bits of mask below this lane
+  return __builtin_amdgcn_mbcnt_hi((u32)(mask >> 32), __builtin_amdgcn_mbcnt_lo((u32)mask, 0u));
+}
+TM_DFN u32 tm_bcast_first(u32 v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// one claim of `n` consecutive items by the first active lane -> the base, broadcast to the wave
+TM_DFN u64 tm_claim(u64* ctr, u32 n) {
+  u64 base = 0;
+  if (tm_lane() == (int)__builtin_ctzll(tm_ballot(true))) base = atomicAdd((unsigned long long*)ctr, (u64)n);
+  const u32 lo = tm_bcast_first((u32)base);
+  const u32 hi = tm_bcast_first((u32)(base >> 32));
+  return ((u64)hi << 32) | lo;
+}
+
+// f32 atomic adds that keep subnormals (2^-102 = 0x0c800000)
+TM_DFN void tm_cas_addf(float* a, float v) {
+  u32* const u = (u32*)a;
+  u32 o = __hip_atomic_load(u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), w;
+  do {
+    w = o;
+    const float n = tm_u2f(w) + v;
+    o = atomicCAS(u, w, tm_f2u(n));
+  } while (o != w);
+}
+TM_DFN void tm_gadd_f32(float* a, float v) {
+  if (v == 0.0f) return;
+  if (!(__builtin_fabsf(v) < tm_u2f(0x0c800000u))) { unsafeAtomicAdd(a, v); return; }
+  tm_cas_addf(a, v);
+}
+TM_DFN void tm_lds_cas_addf(float* a, float v) {
+  u32* const u = (u32*)a;
+  u32 o = *(volatile u32*)u, w;
+  do {
+    w = o;
+    o = atomicCAS(u, w, tm_f2u(tm_u2f(w) + v));
+  } while (o != w);
+}
+TM_DFN void tm_ladd_f32(float* a, float v) {       // a: LDS
+  if (v == 0.0f) return;
+  if (!(__builtin_fabsf(v) < tm_u2f(0x0c800000u))) { atomicAdd(a, v); return; }
+  tm_lds_cas_addf(a, v);
+}
+TM_DFN void tm_gadd_i32(i32* a, i32 v) { atomicAdd(a, v); }
+
+#endif  // device only
+
+// -------------------------------------------------------------------------- the exact f32 sum (5 words)
+// A finite f32 v = m * 2^(p - 149), m < 2^24, p = max(biased exponent - 1, 0): an integer below 2^277 in units of
+// 2^-149, kept as 5 signed int64 words of weight 2^(63 j).  An emit adds the signed pieces of m << (p % 63) into
+// words p/63 and p/63 + 1; an add that overflows int64 (seen in the old value the add returns) carries +-2 into the
+// next word (2^64 = 2 * 2^63); a carry out of word 4 is lost and flags the bin.  Integer adds commute: the total is
+// bitwise independent of the order of the emits.  `add(a, j, q)` adds q to word j and returns the word's old value
+// (the device passes an int64 atomic; the host checks pass a plain add).
+template <class Add> TM_FN bool tm_xcarry(u64* a, int j, i64 c, Add add) {
+  for (; j < 5; ++j) {
+    const i64 o = add(a, j, c);
+    const i64 r = (i64)((u64)o + (u64)c);
+    if (!((c > 0 && r < o) || (c < 0 && r > o))) return false;
+  }
+  return true;
+}
+template <class Add> TM_FN bool tm_xadd_with(u64* a, int j, i64 q, Add add) {
+  const i64 o = add(a, j, q);
+  const i64 r = (i64)((u64)o + (u64)q);
+  if (q > 0 && r < o) return tm_xcarry(a, j + 1, 2, add);
+  if (q < 0 && r > o) return tm_xcarry(a, j + 1, -2, add);
+  return false;
+}
+// true: flag the bin (a non-finite emit or a lost carry)
+template <class Add> TM_FN bool tm_xemit_with(u64* a, float v, Add add) {
+  const u32 b = tm_f2u(v), e = (b >> 23) & 255u;
+  if (e == 255u) return true;
+  const u64 m = (u64)(b & 0x7fffffu) | (e ? 0x800000ull : 0ull);
+  if (m == 0ull) return false;
+  const u32 p = e ? e - 1u : 0u, j = p / 63u, s = p - 63u * j;
+  const i64 lo = (i64)((m << s) & 0x7fffffffffffffffull), hi = s >= 40u ? (i64)(m >> (63u - s)) : 0ll;
+  const bool neg = (b >> 31) != 0u;
+  bool lost = false;
+  if (lo) lost = tm_xadd_with(a, (int)j, neg ? -lo : lo, add);
+  if (hi) lost = tm_xadd_with(a, (int)j + 1, neg ? -hi : hi, add) || lost;
+  return lost;
+}
+
+#if defined(__HIP__) || defined(__HIPCC_RTC__)
+struct TmAtomicAdd64 {
+  __device__ i64 operator()(u64* a, int j, i64 q) const {
+    return (i64)atomicAdd((unsigned long long*)&a[j], (unsigned long long)q);
+  }
+};
+TM_DFN bool tm_xadd(u64* a, int j, i64 q) { return tm_xadd_with(a, j, q, TmAtomicAdd64()); }
+TM_DFN bool tm_xemit(u64* a, float v) { return tm_xemit_with(a, v, TmAtomicAdd64()); }
+#endif  // device only
+
+// the readout: sum_j word_j 2^(63 j) as a 384-bit two's-complement integer, its magnitude rounded once to f32
+// (nearest, ties to even); *bad when beyond f32 (host + device: the host build checks it against Python integers)
+TM_FN float tm_xread(const u64* a, bool* bad) {
+  u64 d[6] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
+  for (int j = 0; j < 5; ++j) {
+    const i64 w = (i64)a[j];
+    const int sh = 63 * j, l = sh >> 6, b = sh & 63;
+    const u64 ext = w < 0 ? ~0ull : 0ull;
+    const u64 x0 = (u64)w << b, x1 = b ? (u64)(w >> (64 - b)) : ext;
+    u64 c = 0ull;
+    for (int k = l; k < 6; ++k) {
+      const u64 y = k == l ? x0 : (k == l + 1 ? x1 : ext);
+      const u64 t = d[k] + y, u = t + c;
+      c = (t < y ? 1ull : 0ull) + (u < t ? 1ull : 0ull);
+      d[k] = u;
+    }
+  }
+  const bool neg = (i64)d[5] < 0;
+  if (neg) {
+    u64 k = 1ull;
+    for (int j = 0; j < 6; ++j) {
+      d[j] = ~d[j] + k;
+      k = (k && d[j] == 0ull) ? 1ull : 0ull;
+    }
+  }
+  int t = 5;
+  while (t >= 0 && d[t] == 0ull) --t;
+  if (t < 0) return 0.0f;
+  const int s = __builtin_clzll(d[t]);
+  const u64 d1 = t >= 1 ? d[t - 1] : 0ull;
+  const u64 top = s ? (d[t] << s) | (d1 >> (64 - s)) : d[t];
+  bool st = s ? (d1 << s) != 0ull : d1 != 0ull;
+  for (int j = 0; j < t - 1; ++j) st = st || d[j] != 0ull;
+  u64 q = top >> 40;
+  const u64 r = top & 0xffffffffffull, half = 0x8000000000ull;
+  if (r > half || (r == half && (st || (q & 1ull)))) ++q;
+  // q * 2^(64 t + 40 - s - 149): exact in double (q <= 2^24), then to f32 exactly unless out of range
+  const int ex = 64 * t + 40 - s - 149;
+  double o = (double)q;
+  // scale by 2^ex in two exact steps (ex can reach ~250 or fall to ~-149)
+  const int e1 = ex / 2, e2 = ex - e1;
+  o = o * tm_u2d((u64)(1023 + e1) << 52) * tm_u2d((u64)(1023 + e2) << 52);
+  if (!(o <= 3.4028234663852886e38)) *bad = true;
+  const float f = (float)o;
+  return neg ? -f : f;
+}

@@ -1,0 +1,22 @@
+// Compile check of the device runtime for gfx950 (built by __graft_entry__.build(), never launched): one kernel
+// that instantiates every helper of tm_device.h and tm_libm.h.
+#include <hip/hip_runtime.h>
+#include "tm_device.h"
+#include "tm_libm.h"
+
+extern "C" __global__ void tm_device_check(float* f, u64* x, u32* u, u64* ctr, int n) {
+  __shared__ float sh[64];
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  sh[threadIdx.x & 63] = 0.0f;
+  __syncthreads();
+  u32 o0, o1;
+  tm_threefry(u[0], u[1], 0u, (u32)i, o0, o1);
+  const float v = tm_erfinvf(tm_u2f((o0 >> 9) | 0x3f800000u) - 1.5f);
+  tm_ladd_f32(&sh[o1 & 63u], v);
+  tm_gadd_f32(&f[i & 15], tm_fmax<float>(v, 0.0f));
+  if (tm_xemit(&x[(i & 3) * 5], v)) atomicOr(&u[2], 1u);
+  const u64 base = tm_claim(ctr, (u32)__builtin_popcountll(tm_ballot(v > 0.0f)));
+  bool bad = false;
+  if (i < n) f[16 + i] = tm_xread(x, &bad) + (float)base + sh[threadIdx.x & 63] + (float)tm_rank(tm_ballot(true))
+                         + (float)tm_idiv(i, n) + (float)tm_f2i32(v) + (float)tm_log((double)v);
+}

@@ -1,0 +1,295 @@
+// libtallymap_rocm.so -- the C-ABI launch library of the tallymap_amd kernel backend (include/tallymap_rocm.h).
+//
+// Host code only.  The HIP runtime and hipRTC are resolved with dlopen / dlsym at tm_init, so the library binds to
+// the runtime the process already loaded (a framework's bundled libamdhip64) instead of starting a second one; the
+// hip headers are used for types and enum values only.  Every kernel (zeroing, the item loop, the readout) lives in
+// the program's own code object, registered with tm_register and loaded per device on its first launch.
+//
+// Reference: tallymap/backends/kernel/shim.cc (CUDA driver version of the same registry and launch sequence).
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+#include <hip/hiprtc.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/tallymap_rocm.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+  char buf[2048];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return 1;
+}
+
+struct Rt {
+  void* hip = nullptr;
+  void* rtc = nullptr;
+#define TM_SYM(name) decltype(&::name) name = nullptr;
+  TM_SYM(hipModuleLoadData)
+  TM_SYM(hipModuleGetFunction)
+  TM_SYM(hipModuleLaunchKernel)
+  TM_SYM(hipGetDevice)
+  TM_SYM(hipDeviceGetAttribute)
+  TM_SYM(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor)
+  TM_SYM(hipFuncGetAttribute)
+  TM_SYM(hipGetErrorString)
+  TM_SYM(hiprtcCreateProgram)
+  TM_SYM(hiprtcCompileProgram)
+  TM_SYM(hiprtcGetProgramLogSize)
+  TM_SYM(hiprtcGetProgramLog)
+  TM_SYM(hiprtcGetCodeSize)
+  TM_SYM(hiprtcGetCode)
+  TM_SYM(hiprtcDestroyProgram)
+  TM_SYM(hiprtcGetErrorString)
+#undef TM_SYM
+};
+
+std::mutex g_mu;
+Rt g_rt;
+bool g_hip_ok = false, g_rtc_ok = false;
+
+template <class F> bool sym(void* h, const char* name, F& f) {
+  f = reinterpret_cast<F>(dlsym(h, name));
+  return f != nullptr;
+}
+
+struct Program {
+  std::vector<char> image;
+  std::string note;
+};
+
+struct Loaded {
+  hipModule_t mod = nullptr;
+  hipFunction_t zero = nullptr, main = nullptr, post = nullptr;
+  int cus = 0;
+  std::map<int, int> occ;       // block size -> blocks per CU of tm_main
+};
+
+std::map<long long, std::shared_ptr<Program>>& registry() {
+  static std::map<long long, std::shared_ptr<Program>> r;
+  return r;
+}
+std::map<std::pair<long long, int>, std::shared_ptr<Loaded>>& modules() {
+  static std::map<std::pair<long long, int>, std::shared_ptr<Loaded>> m;
+  return m;
+}
+
+const char* herr(hipError_t e) { return g_rt.hipGetErrorString ? g_rt.hipGetErrorString(e) : "hip error"; }
+
+int bind_hip(const char* path) {
+  if (g_hip_ok) return 0;
+  void* h = dlopen(path ? path : "libamdhip64.so.7", RTLD_NOW | RTLD_LOCAL);
+  if (!h) return fail("tallymap_rocm: cannot load the HIP runtime %s: %s", path ? path : "libamdhip64.so.7",
+                      dlerror());
+  Rt& r = g_rt;
+  bool ok = sym(h, "hipModuleLoadData", r.hipModuleLoadData) && sym(h, "hipModuleGetFunction", r.hipModuleGetFunction) &&
+            sym(h, "hipModuleLaunchKernel", r.hipModuleLaunchKernel) && sym(h, "hipGetDevice", r.hipGetDevice) &&
+            sym(h, "hipDeviceGetAttribute", r.hipDeviceGetAttribute) &&
+            sym(h, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor",
+                r.hipModuleOccupancyMaxActiveBlocksPerMultiprocessor) &&
+            sym(h, "hipFuncGetAttribute", r.hipFuncGetAttribute) && sym(h, "hipGetErrorString", r.hipGetErrorString);
+  if (!ok) return fail("tallymap_rocm: %s lacks a HIP module API symbol", path ? path : "libamdhip64.so.7");
+  r.hip = h;
+  g_hip_ok = true;
+  return 0;
+}
+
+int bind_rtc(const char* path) {
+  if (g_rtc_ok) return 0;
+  void* h = dlopen(path ? path : "libhiprtc.so.7", RTLD_NOW | RTLD_LOCAL);
+  if (!h) return fail("tallymap_rocm: cannot load hipRTC %s: %s", path ? path : "libhiprtc.so.7", dlerror());
+  Rt& r = g_rt;
+  bool ok = sym(h, "hiprtcCreateProgram", r.hiprtcCreateProgram) && sym(h, "hiprtcCompileProgram", r.hiprtcCompileProgram) &&
+            sym(h, "hiprtcGetProgramLogSize", r.hiprtcGetProgramLogSize) &&
+            sym(h, "hiprtcGetProgramLog", r.hiprtcGetProgramLog) && sym(h, "hiprtcGetCodeSize", r.hiprtcGetCodeSize) &&
+            sym(h, "hiprtcGetCode", r.hiprtcGetCode) && sym(h, "hiprtcDestroyProgram", r.hiprtcDestroyProgram) &&
+            sym(h, "hiprtcGetErrorString", r.hiprtcGetErrorString);
+  if (!ok) return fail("tallymap_rocm: %s lacks a hipRTC symbol", path ? path : "libhiprtc.so.7");
+  r.rtc = h;
+  g_rtc_ok = true;
+  return 0;
+}
+
+// the module of program `id` on the current device (loaded on first use)
+int loaded(long long id, std::shared_ptr<Loaded>* out) {
+  int dev = 0;
+  hipError_t e = g_rt.hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("tallymap_rocm: hipGetDevice: %s", herr(e));
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = modules().find({id, dev});
+  if (it != modules().end()) {
+    *out = it->second;
+    return 0;
+  }
+  auto pr = registry().find(id);
+  if (pr == registry().end()) return fail("tallymap_rocm: program %lld is not registered", id);
+  auto L = std::make_shared<Loaded>();
+  e = g_rt.hipModuleLoadData(&L->mod, pr->second->image.data());
+  if (e != hipSuccess) return fail("tallymap_rocm: loading %s on device %d: %s", pr->second->note.c_str(), dev, herr(e));
+  if ((e = g_rt.hipModuleGetFunction(&L->main, L->mod, "tm_main")) != hipSuccess)
+    return fail("tallymap_rocm: %s has no tm_main: %s", pr->second->note.c_str(), herr(e));
+  if (g_rt.hipModuleGetFunction(&L->zero, L->mod, "tm_zero") != hipSuccess) L->zero = nullptr;
+  if (g_rt.hipModuleGetFunction(&L->post, L->mod, "tm_post") != hipSuccess) L->post = nullptr;
+  if ((e = g_rt.hipDeviceGetAttribute(&L->cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess)
+    return fail("tallymap_rocm: device attribute: %s", herr(e));
+  modules()[{id, dev}] = L;
+  *out = L;
+  return 0;
+}
+
+int occupancy(Loaded& L, int block, int* occ) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = L.occ.find(block);
+  if (it != L.occ.end()) {
+    *occ = it->second;
+    return 0;
+  }
+  int o = 0;
+  hipError_t e = g_rt.hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&o, L.main, block, 0);
+  if (e != hipSuccess) return fail("tallymap_rocm: occupancy query: %s", herr(e));
+  if (o < 1) o = 1;
+  L.occ[block] = o;
+  *occ = o;
+  return 0;
+}
+
+int launch1(hipFunction_t f, unsigned grid, unsigned block, hipStream_t s, const std::vector<char>& args,
+            const char* what) {
+  size_t sz = args.size();
+  void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<char*>(args.data()), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                 HIP_LAUNCH_PARAM_END};
+  hipError_t e = g_rt.hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, s, nullptr, cfg);
+  if (e != hipSuccess) return fail("tallymap_rocm: launching %s (grid %u x %u): %s", what, grid, block, herr(e));
+  return 0;
+}
+
+constexpr long long MAX_PRIVATE = 64 << 10;      // private (scratch) bytes per lane a launch accepts
+
+}  // namespace
+
+extern "C" {
+
+int tm_init(const char* hip_path, const char* hiprtc_path) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (bind_hip(hip_path)) return 1;
+  if (bind_rtc(hiprtc_path)) return 1;
+  return 0;
+}
+
+int tm_compile(const char* src, const char* name, const char* const* opts, int nopts, void** image, size_t* n,
+               char** log) {
+  if (!g_rtc_ok) return fail("tallymap_rocm: tm_init was not called");
+  *image = nullptr;
+  *n = 0;
+  if (log) *log = nullptr;
+  hiprtcProgram p;
+  hiprtcResult r = g_rt.hiprtcCreateProgram(&p, src, name, 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS) return fail("tallymap_rocm: hiprtcCreateProgram: %s", g_rt.hiprtcGetErrorString(r));
+  r = g_rt.hiprtcCompileProgram(p, nopts, const_cast<const char**>(opts));
+  size_t ls = 0;
+  g_rt.hiprtcGetProgramLogSize(p, &ls);
+  std::string lg(ls, '\0');
+  if (ls) g_rt.hiprtcGetProgramLog(p, &lg[0]);
+  if (log && ls) {
+    *log = static_cast<char*>(malloc(ls + 1));
+    memcpy(*log, lg.c_str(), ls);
+    (*log)[ls] = 0;
+  }
+  if (r != HIPRTC_SUCCESS) {
+    g_rt.hiprtcDestroyProgram(&p);
+    return fail("tallymap_rocm: hipRTC failed (%s) for %s:\n%.1800s", g_rt.hiprtcGetErrorString(r), name, lg.c_str());
+  }
+  size_t cs = 0;
+  g_rt.hiprtcGetCodeSize(p, &cs);
+  void* buf = malloc(cs);
+  g_rt.hiprtcGetCode(p, static_cast<char*>(buf));
+  g_rt.hiprtcDestroyProgram(&p);
+  *image = buf;
+  *n = cs;
+  return 0;
+}
+
+int tm_register(long long id, const void* image, size_t n, const char* note) {
+  if (!image || !n) return fail("tallymap_rocm: tm_register(%lld): empty image", id);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (registry().count(id)) return 0;
+  auto p = std::make_shared<Program>();
+  p->image.assign(static_cast<const char*>(image), static_cast<const char*>(image) + n);
+  p->note = note ? note : "";
+  registry()[id] = p;
+  return 0;
+}
+
+int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, int flags, long long n_items,
+              int block) {
+  if (!g_hip_ok) return fail("tallymap_rocm: tm_init was not called");
+  if (n < 1 || block < 64 || block > 1024 || block % 64) return fail("tallymap_rocm: bad launch shape");
+  if (n_items < 0) return fail("tallymap_rocm: negative item count");
+  std::shared_ptr<Loaded> L;
+  if (loaded(id, &L)) return 1;
+  int priv = 0;
+  if (g_rt.hipFuncGetAttribute(&priv, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES, L->main) != hipSuccess) priv = 0;
+  if (priv > MAX_PRIVATE)
+    return fail("tallymap_rocm: program %lld needs %d private bytes per lane (limit %lld): refusing to launch", id,
+                priv, MAX_PRIVATE);
+  int occ = 1;
+  if (occupancy(*L, block, &occ)) return 1;
+  std::vector<char> args(sizeof(void*) * n + sizeof(long long));
+  memcpy(args.data(), bufs, sizeof(void*) * n);
+  memcpy(args.data() + sizeof(void*) * n, &n_items, sizeof(long long));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_zero > 0 && L->zero && launch1(L->zero, 64, 256, s, args, "tm_zero")) return 1;
+  if (n_items > 0) {
+    const long long want = (n_items + block - 1) / block;
+    const long long cap = (long long)L->cus * occ;
+    const unsigned grid = (unsigned)(want < cap ? want : cap);
+    if (launch1(L->main, grid, block, s, args, "tm_main")) return 1;
+  }
+  if ((flags & 2) && L->post && launch1(L->post, 64, 256, s, args, "tm_post")) return 1;
+  return 0;
+}
+
+int tm_kernel_info(long long id, int block, long long out[8]) {
+  if (!g_hip_ok) return fail("tallymap_rocm: tm_init was not called");
+  std::shared_ptr<Loaded> L;
+  if (loaded(id, &L)) return 1;
+  int regs = 0, priv = 0, lds = 0, maxt = 0, occ = 1;
+  const hipFunction_attribute at[4] = {HIP_FUNC_ATTRIBUTE_NUM_REGS, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES,
+                                       HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK};
+  int* dst[4] = {&regs, &priv, &lds, &maxt};
+  for (int i = 0; i < 4; ++i) {
+    hipError_t e = g_rt.hipFuncGetAttribute(dst[i], at[i], L->main);
+    if (e != hipSuccess) return fail("tallymap_rocm: hipFuncGetAttribute: %s", herr(e));
+  }
+  if (occupancy(*L, block, &occ)) return 1;
+  out[0] = regs;
+  out[1] = priv;
+  out[2] = lds;
+  out[3] = occ;
+  out[4] = (long long)occ * block * L->cus;
+  out[5] = L->cus;
+  out[6] = maxt;
+  out[7] = (long long)L->cus * occ;
+  return 0;
+}
+
+const char* tm_last_error(void) { return g_err.c_str(); }
+
+void tm_free(void* p) { free(p); }
+
+}  // extern "C"

@@ -1,0 +1,324 @@
+"""lax for item code: while_loop, fori_loop, cond, select, stop_gradient and the elementwise primitives.
+
+While loops carry pytrees (tuples, lists, dicts, Tally).  At the item's top level, when the call has
+`max_steps=M`, every while loop is capped as the reference's re-tracer caps it (reference _rewrite.py:517-527): a
+step counter k is prepended to the carries, the loop runs while (k < M) & cond(carries), and the item's
+`truncated` flag ORs (k >= M) & cond(final carries) over its top-level loops.
+"""
+import numpy as np
+
+from . import _core as C
+from ._tree import flatten, unflatten
+
+# the capping context of the item being traced (set by tallymap_amd._api while tracing an item)
+_CAP = []
+
+
+class _CapCtx:
+    def __init__(self, builder, M):
+        self.builder, self.M, self.trunc = builder, M, None
+
+
+def _leaf_var(x, aval=None):
+    """a carry leaf -> (Var | Lit, aval)."""
+    if C.is_traced(x):
+        return C.current().local(x.var), x.aval
+    lit = C.literal(x) if aval is None else C.literal(np.asarray(x).astype(aval.dtype), aval.dtype,
+                                                       weak=aval.weak)
+    return lit, lit.aval
+
+
+def _finish_sub(b, ins, outs, out_avals):
+    """the closed sub-program of builder b: invars = [captured locals] + ins; outputs coerced to out_avals."""
+    ov = []
+    C._STACK.append(b)
+    try:
+        for x, a in zip(outs, out_avals):
+            if C.is_traced(x):
+                if x.shape != a.shape:
+                    raise C.TraceError(f"loop/branch output shape {x.shape} != carry shape {a.shape}")
+                if x.dtype != a.dtype:
+                    if x.aval.weak or C._kind(x.dtype) <= C._kind(a.dtype):
+                        x = C.convert(x, a.dtype, weak=a.weak)
+                    else:
+                        raise C.TraceError(f"loop/branch output dtype {x.dtype} != carry dtype {a.dtype}")
+                ov.append(b.local(x.var))
+            else:
+                ov.append(C.literal(np.asarray(x).astype(a.dtype), a.dtype, weak=a.weak))
+    finally:
+        C._STACK.pop()
+    cap_locals = [b.env[o.id] for o in b.captured]
+    return C.Jaxpr(cap_locals + [t.var for t in ins], ov, b.eqns)
+
+
+def _unify(avals_init, outs):
+    """carry avals: the init's, widened where the init is weak and the body output is strong."""
+    res = []
+    for a, x in zip(avals_init, outs):
+        if a.weak and C.is_traced(x) and not x.aval.weak and x.shape == a.shape and x.dtype != a.dtype \
+                and C._kind(x.dtype) >= C._kind(a.dtype):
+            res.append(C.AVal(a.shape, x.dtype, False))
+        elif a.weak and C.is_traced(x) and not x.aval.weak and x.dtype == a.dtype:
+            res.append(C.AVal(a.shape, a.dtype, False))
+        else:
+            res.append(a)
+    return res
+
+
+def while_loop(cond_fun, body_fun, init_val):
+    """lax.while_loop: carries a pytree; captured outer values become the loop's constants."""
+    leaves, td = flatten(init_val)
+    cur = C.current()
+    cap = _CAP[-1] if _CAP and _CAP[-1].builder is cur else None
+    avals = [_leaf_var(x)[1] for x in leaves]
+    # trace the body once to learn the carry types (a weak init widened by a strong update), then for real
+    for attempt in range(2):
+        bb, bins, bout = C.trace_fn(lambda *ls: flatten(body_fun(unflatten(td, list(ls))))[0], avals, parent=cur)
+        new = _unify(avals, bout)
+        if new == avals and all(a.weak == n.weak for a, n in zip(avals, new)):
+            break
+        avals = new
+    bjx = _finish_sub(bb, bins, bout, avals)
+    cb, cins, cout = C.trace_fn(lambda *ls: [cond_fun(unflatten(td, list(ls)))], avals, parent=cur)
+    pred = cout[0]
+    if not C.is_traced(pred) or pred.dtype != C.BOOL or pred.shape != ():
+        raise C.TraceError("while_loop: cond_fun must return a traced scalar bool")
+    cjx = _finish_sub(cb, cins, cout, [C.AVal((), C.BOOL)])
+    init_vars = []
+    for x, a in zip(leaves, avals):
+        v, _ = _leaf_var(x, a)
+        if isinstance(v, C.Var) and v.aval.dtype != a.dtype:
+            v = C.convert(C.Tracer(v), a.dtype, weak=a.weak).var
+        init_vars.append(v)
+    if cap is not None:
+        return _capped(cap, cjx, bjx, cb, bb, init_vars, avals, td)
+    outs = C.bind("while", list(cb.captured) + list(bb.captured) + init_vars, avals,
+                  cond_jaxpr=cjx, body_jaxpr=bjx, cond_nconsts=len(cb.captured), body_nconsts=len(bb.captured))
+    return unflatten(td, outs)
+
+
+def _capped(cap, cjx, bjx, cb, bb, init_vars, avals, td):
+    """the capped top-level loop: carries [k] + carries; cond (k < M) & cond; body (k + 1, body)."""
+    M = int(cap.M)
+    kav = C.AVal((), C.I32)
+    ncc, nbc = len(cb.captured), len(bb.captured)
+    # cond': invars [cond consts] + [k] + carries
+    cc_vars = [C.Var(v.aval) for v in cjx.invars[:ncc]]
+    k_c = C.Var(kav)
+    cr_vars = [C.Var(a) for a in avals]
+    p_inner = C.Var(C.AVal((), C.BOOL))
+    ltv = C.Var(C.AVal((), C.BOOL))
+    andv = C.Var(C.AVal((), C.BOOL))
+    ceqns = [C.Eqn("lt", [k_c, C.Lit(M, kav)], [ltv], {}),
+             _inline(cjx, cc_vars + cr_vars, [p_inner]),
+             C.Eqn("and", [ltv, p_inner], [andv], {})]
+    cjx2 = C.Jaxpr(cc_vars + [k_c] + cr_vars, [andv], _flat_eqns(ceqns))
+    # body': invars [body consts] + [k] + carries
+    bc_vars = [C.Var(v.aval) for v in bjx.invars[:nbc]]
+    k_b = C.Var(kav)
+    br_vars = [C.Var(a) for a in avals]
+    k1 = C.Var(kav)
+    bouts = [C.Var(a) for a in avals]
+    beqns = [C.Eqn("add", [k_b, C.Lit(1, kav)], [k1], {}), _inline(bjx, bc_vars + br_vars, bouts)]
+    bjx2 = C.Jaxpr(bc_vars + [k_b] + br_vars, [k1] + bouts, _flat_eqns(beqns))
+    outs = C.bind("while", list(cb.captured) + list(bb.captured) + [C.Lit(0, kav)] + init_vars, [kav] + avals,
+                  cond_jaxpr=cjx2, body_jaxpr=bjx2, cond_nconsts=ncc, body_nconsts=nbc)
+    kout, rest = outs[0], outs[1:]
+    # truncated = (k >= M) & cond(final carries): the cond program once more, inline, on the loop's results
+    still = C.Var(C.AVal((), C.BOOL))
+    b = C.current()
+    consts = [b.local(v) for v in cb.captured]
+    b.eqns.extend(inline_eqns(cjx, consts + [t.var for t in rest], [still]))
+    b.owned.add(still.id)
+    tr = (kout >= M) & C.Tracer(still)
+    cap.trunc = tr if cap.trunc is None else (cap.trunc | tr)
+    return unflatten(td, rest)
+
+
+class _Inline:
+    """marker: the equations of a sub-program, renamed onto given in/out vars (expanded by _flat_eqns)."""
+
+    def __init__(self, jx, ins, outs):
+        self.jx, self.ins, self.outs = jx, ins, outs
+
+
+def _inline(jx, ins, outs):
+    return _Inline(jx, ins, outs)
+
+
+def _flat_eqns(items):
+    out = []
+    for it in items:
+        if isinstance(it, _Inline):
+            out += inline_eqns(it.jx, it.ins, it.outs)
+        else:
+            out.append(it)
+    return out
+
+
+def inline_eqns(jx, ins, outs):
+    """jx's equations with its invars renamed to `ins` and its outvars to `outs` (fresh vars inside; an output that
+    is an input or a literal gets a copy equation)."""
+    ren = {v.id: w for v, w in zip(jx.invars, ins)}
+
+    def rv(v):
+        if isinstance(v, C.Lit):
+            return v
+        return ren.get(v.id, v)
+    eqns = []
+    outmap = {}
+    for o, w in zip(jx.outvars, outs):
+        if isinstance(o, C.Var) and o.id not in ren and o.id not in outmap:
+            outmap[o.id] = w
+    for e in jx.eqns:
+        new_outs = []
+        for o in e.outvars:
+            if o.id in outmap:
+                w = outmap.pop(o.id)
+                ren[o.id] = w
+                new_outs.append(w)
+            else:
+                w = C.Var(o.aval)
+                ren[o.id] = w
+                new_outs.append(w)
+        eqns.append(C.Eqn(e.prim, [rv(v) for v in e.invars], new_outs, e.params))
+    for o, w in zip(jx.outvars, outs):
+        src = rv(o)
+        if src is not w:
+            eqns.append(C.Eqn("copy", [src], [w], {}))
+    return eqns
+
+
+def fori_loop(lower, upper, body_fun, init_val):
+    """lax.fori_loop as a while loop over (i, carry)."""
+    def cond(c):
+        return c[0] < upper
+
+    def body(c):
+        return (c[0] + 1, body_fun(c[0], c[1]))
+    return while_loop(cond, body, (lower, init_val))[1]
+
+
+def cond(pred, true_fun, false_fun, *operands):
+    """lax.cond(pred, true_fun, false_fun, *operands): one `cond` equation, branches (false, true) as JAX orders
+    them, selected by int32(pred)."""
+    if not C.is_traced(pred):
+        return true_fun(*operands) if pred else false_fun(*operands)
+    if pred.dtype != C.BOOL:
+        pred = pred != 0
+    leaves, td = flatten(list(operands))
+    cur = C.current()
+    avals = [_leaf_var(x)[1] for x in leaves]
+    trees = []
+
+    def run(f):
+        def g(*ls):
+            lv, t = flatten(f(*unflatten(td, list(ls))))
+            trees.append(t)
+            return lv
+        return g
+    fb, fins, fout = C.trace_fn(run(false_fun), avals, parent=cur)
+    tb, tins, tout = C.trace_fn(run(true_fun), avals, parent=cur)
+    otd = trees[1]
+    if trees[0] != trees[1]:
+        raise C.TraceError("cond: branches return different structures")
+    if len(fout) != len(tout):
+        raise C.TraceError("cond: branches return different structures")
+    oav = []
+    for a, b in zip(tout, fout):
+        aa, ab = C._aval(a), C._aval(b)
+        dt, weak = C.result_type(aa, ab)
+        if aa.shape != ab.shape:
+            raise C.TraceError("cond: branch outputs have different shapes")
+        oav.append(C.AVal(aa.shape, dt, weak))
+    union = []
+    for o in list(fb.captured) + list(tb.captured):
+        if all(o is not u for u in union):
+            union.append(o)
+    branches = []
+    for b, ins, out in ((fb, fins, fout), (tb, tins, tout)):
+        jx = _finish_sub(b, ins, out, oav)
+        ncap = len(b.captured)
+        loc = {o.id: l for o, l in zip(b.captured, jx.invars[:ncap])}
+        cap_vars = [loc.get(u.id) or C.Var(u.aval) for u in union]
+        branches.append(C.Jaxpr(cap_vars + jx.invars[ncap:], jx.outvars, jx.eqns))
+    ops = []
+    for x, a in zip(leaves, avals):
+        ops.append(_leaf_var(x, a)[0])
+    idx = C.convert(pred, C.I32)
+    outs = C.bind("cond", [idx.var] + list(union) + ops, oav, branches=tuple(branches), nconsts=len(union))
+    return unflatten(otd, outs)
+
+
+def select(pred, on_true, on_false):
+    return C.select(pred, on_true, on_false)
+
+
+def stop_gradient(x):
+    """the value, with a zero derivative (reverse mode sends no cotangent through it)."""
+    if not C.is_traced(x):
+        return x
+    return C.bind("stop_gradient", [x.var], [x.aval])[0]
+
+
+def _u(prim):
+    def f(x):
+        x = C._float_of(x)
+        return C.unop(prim, x, float_only=True)
+    f.__name__ = prim
+    return f
+
+
+exp = _u("exp")
+log = _u("log")
+log1p = _u("log1p")
+expm1 = _u("expm1")
+sin = _u("sin")
+cos = _u("cos")
+tan = _u("tan")
+tanh = _u("tanh")
+sqrt = _u("sqrt")
+rsqrt = _u("rsqrt")
+erf_inv = _u("erf_inv")
+floor = _u("floor")
+ceil = _u("ceil")
+logistic = _u("logistic")
+
+
+def atan2(y, x):
+    return C.binop("atan2", C._float_of(y), C._float_of(x))
+
+
+def max(a, b):          # noqa: A001 (lax.max)
+    return C.binop("max", a, b)
+
+
+def min(a, b):          # noqa: A001 (lax.min)
+    return C.binop("min", a, b)
+
+
+def pow(a, b):          # noqa: A001 (lax.pow)
+    return C.binop("pow", C._float_of(a), C._float_of(b))
+
+
+def integer_pow(x, y):
+    return C.bind("integer_pow", [x.var], [x.aval], y=int(y))[0]
+
+
+def convert_element_type(x, dtype):
+    return C.convert(x, dtype)
+
+
+def bitcast_convert_type(x, dtype):
+    dtype = np.dtype(dtype)
+    if dtype.itemsize != x.dtype.itemsize:
+        raise C.TraceError("bitcast between different widths is not supported")
+    return C.bind("bitcast_convert_type", [x.var], [C.AVal(x.shape, dtype)], new_dtype=dtype)[0]
+
+
+def shift_right_logical(x, n):
+    return C.binop("shift_right_logical", x, n)
+
+
+def shift_left(x, n):
+    return C.binop("shift_left", x, n)

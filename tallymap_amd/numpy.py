@@ -1,0 +1,106 @@
+"""jax.numpy for item code: the subset the item programs use, with jax.numpy's semantics (ufuncs lower to the lax
+primitives of the same name; jnp.where is lax.select_n; jnp.clip is maximum then minimum, as jax.numpy.clip)."""
+import numpy as _np
+
+from . import _core as C
+from . import lax as _lax
+
+float32, float64, int32, uint32, int64, uint32, bool_, uint8 = (_np.float32, _np.float64, _np.int32, _np.uint32,
+                                                              _np.int64, _np.uint32, _np.bool_, _np.uint8)
+pi = _np.pi
+e = _np.e
+inf = _np.inf
+nan = _np.nan
+
+exp, log, log1p, expm1 = _lax.exp, _lax.log, _lax.log1p, _lax.expm1
+sin, cos, tan, tanh = _lax.sin, _lax.cos, _lax.tan, _lax.tanh
+sqrt, floor, ceil = _lax.sqrt, _lax.floor, _lax.ceil
+arctan2 = _lax.atan2
+
+
+def asarray(x, dtype=None):
+    if C.is_traced(x):
+        return x if dtype is None else C.convert(x, dtype)
+    return _np.asarray(x, dtype)
+
+
+def where(cond, x, y):
+    return C.select(cond, x, y)
+
+
+def maximum(a, b):
+    return C.binop("max", a, b)
+
+
+def minimum(a, b):
+    return C.binop("min", a, b)
+
+
+def abs(x):             # noqa: A001
+    return C.unop("abs", x)
+
+
+absolute = abs
+
+
+def sign(x):
+    return C.unop("sign", x)
+
+
+def clip(x, a_min=None, a_max=None):
+    if a_min is not None:
+        x = maximum(a_min, x)
+    if a_max is not None:
+        x = minimum(a_max, x)
+    return x
+
+
+def square(x):
+    return C.bind("integer_pow", [x.var], [x.aval], y=2)[0]
+
+
+def power(a, b):
+    return C.power(a, b)
+
+
+def logical_and(a, b):
+    return C.binop("and", a, b)
+
+
+def logical_or(a, b):
+    return C.binop("or", a, b)
+
+
+def logical_not(a):
+    return C.unop("not", a)
+
+
+def stack(xs):
+    return C.stack(xs)
+
+
+def array(xs, dtype=None):
+    if any(C.is_traced(x) for x in xs):
+        r = C.stack(xs)
+        return r if dtype is None else C.convert(r, dtype)
+    return _np.array(xs, dtype)
+
+
+def sum(x):             # noqa: A001
+    return C.reduce_sum(x) if C.is_traced(x) else _np.sum(x)
+
+
+def dot(a, b):
+    """the dot product of two small vectors: (a0 b0 + a1 b1) + ..., left to right."""
+    acc = a[0] * b[0]
+    for i in range(1, a.shape[0]):
+        acc = acc + a[i] * b[i]
+    return acc
+
+
+def zeros_like(x):
+    return x * 0
+
+
+def int32_(x):
+    return C.convert(x, C.I32)

@@ -1,0 +1,60 @@
+// Host checks of tallymap_amd/csrc/tm_libm.h against glibc (test infrastructure).
+//   libm_check erfinv_normal   every f32 argument jax.random.normal passes to erf_inv (2^23 uniform values):
+//                              tm_erfinvf vs the reference CPU target's formula with glibc log / sqrt
+//   libm_check log <n> <seed>  n random positive doubles: tm_log vs glibc log (ulp histogram)
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <cstdint>
+#include "../../tallymap_amd/csrc/tm_device.h"
+#include "../../tallymap_amd/csrc/tm_libm.h"
+
+static double ref_giles(double y) {        // reference host.py:107-118 with glibc's log / sqrt
+  const double a = fabs(y);
+  double w = -log((1.0 - a) * (1.0 + a)), p;
+  if (w < 5.0) { w -= 2.5; p = 2.81022636e-08; p = 3.43273939e-07 + p * w; p = -3.5233877e-06 + p * w;
+    p = -4.39150654e-06 + p * w; p = 0.00021858087 + p * w; p = -0.00125372503 + p * w; p = -0.00417768164 + p * w;
+    p = 0.246640727 + p * w; p = 1.50140941 + p * w; }
+  else { w = sqrt(w) - 3.0; p = -0.000200214257; p = 0.000100950558 + p * w; p = 0.00134934322 + p * w;
+    p = -0.00367342844 + p * w; p = 0.00573950773 + p * w; p = -0.0076224613 + p * w; p = 0.00943887047 + p * w;
+    p = 1.00167406 + p * w; p = 2.83297682 + p * w; }
+  return p * a; }
+static float ref_erfinvf(float y) {
+  if (!(y > -1.0f && y < 1.0f)) return y == 1.0f ? INFINITY : (y == -1.0f ? -INFINITY : NAN);
+  return y == 0.0f ? y : (float)copysign(ref_giles(y), (double)y); }
+
+int main(int argc, char** argv) {
+  if (argc > 1 && !strcmp(argv[1], "erfinv_normal")) {
+    const float lo = tm_u2f(0xbf7fffffu), span = 1.0f - lo;
+    long n = 0, bad = 0, logdiff = 0;
+    for (uint32_t m = 0; m < (1u << 23); ++m) {
+      const float f = tm_u2f(m | 0x3f800000u) - 1.0f;
+      const float r = f * span;
+      const float s = r + lo;
+      const float u = tm_fmax(lo, s);
+      const float a = tm_erfinvf(u), b = ref_erfinvf(u);
+      const double ad = fabs((double)u);
+      if (tm_log((1.0 - ad) * (1.0 + ad)) != log((1.0 - ad) * (1.0 + ad))) ++logdiff;
+      ++n;
+      if (tm_f2u(a) != tm_f2u(b)) { if (++bad < 10) printf("  u=%a tm=%a ref=%a\n", u, a, b); }
+    }
+    printf("erfinv_normal: %ld arguments, %ld f32 mismatches (double log differs on %ld)\n", n, bad, logdiff);
+    return bad != 0;
+  }
+  if (argc > 3 && !strcmp(argv[1], "log")) {
+    long n = atol(argv[2]);
+    srand48(atol(argv[3]));
+    long diff = 0, big = 0;
+    for (long i = 0; i < n; ++i) {
+      uint64_t b = ((uint64_t)(mrand48() & 0x7fefffff) << 32) | (uint32_t)mrand48();
+      double x = tm_u2d(b);
+      double a = tm_log(x), r = log(x);
+      if (a != r) { ++diff; int64_t d = (int64_t)tm_d2u(a) - (int64_t)tm_d2u(r); if (d > 1 || d < -1) ++big; }
+    }
+    printf("log: %ld random doubles, %ld differ from glibc, %ld by more than 1 ulp\n", n, diff, big);
+    return big != 0;
+  }
+  fprintf(stderr, "usage: libm_check erfinv_normal | log <n> <seed>\n");
+  return 2;
+}

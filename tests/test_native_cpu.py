@@ -1,0 +1,115 @@
+"""CPU checks of the native pieces: the C-ABI library exports what include/tallymap_rocm.h declares, the device
+runtime's exact accumulator and tm_libm.h agree with Python integers / glibc on the host, generated kernels compile
+for gfx950 through the product's hipRTC path."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import exact as X
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _build(src, out):
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-o", out, os.path.join(ROOT, src), "-lm"],
+                   check=True)
+    return out
+
+
+def test_cabi_exports_every_declared_symbol():
+    hdr = open(os.path.join(ROOT, "include", "tallymap_rocm.h")).read()
+    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)          # declarations only, not the comments
+    names = sorted(set(re.findall(r"^[a-z][\w \*]*?\b(tm_[a-z_]+)\(", hdr, flags=re.M)))
+    assert {"tm_init", "tm_compile", "tm_register", "tm_launch", "tm_kernel_info", "tm_last_error",
+            "tm_free"} <= set(names)
+    from tallymap_amd.backend import compile as Cm
+    lib = ctypes.CDLL(Cm.SHIM)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_cabi_errors_without_init():
+    from tallymap_amd.backend import compile as Cm
+    lib = ctypes.CDLL(Cm.SHIM)
+    lib.tm_last_error.restype = ctypes.c_char_p
+    # tm_register copies; an empty image is refused with a message
+    lib.tm_register.argtypes = [ctypes.c_longlong, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]
+    assert lib.tm_register(1, b"", 0, b"x") != 0
+    assert b"empty image" in lib.tm_last_error()
+
+
+@pytest.fixture(scope="module")
+def xsum(tmp_path_factory):
+    return _build("tests/native/xsum_check.cc", str(tmp_path_factory.mktemp("n") / "xsum_check"))
+
+
+def _xrun(exe, v):
+    inp = "\n".join("%08x" % x for x in np.asarray(v, np.float32).view(np.uint32))
+    out = subprocess.run([exe], input=inp, capture_output=True, text=True, check=True).stdout.split()
+    return np.uint32(int(out[0], 16)).view(np.float32), out[1] == "1"
+
+
+def test_exact_accumulator_matches_python_integers(xsum):
+    rng = np.random.default_rng(11)
+    cases = [rng.standard_normal(3000).astype(np.float32),
+             (rng.standard_normal(300) * 1e37).astype(np.float32),
+             np.concatenate([np.full(5000, 3.4e38), np.full(5000, -3.4e38), [1.0]]).astype(np.float32),
+             np.array([1e-45] * 1000 + [-3e-45] * 10, np.float32),
+             np.array([1.0, 2 ** -24, 2 ** -24], np.float32),
+             np.array([2.0 ** 100, 1.0, -2.0 ** 100], np.float32),
+             rng.permutation(np.concatenate([rng.standard_normal(500) * 10.0 ** rng.integers(-40, 38, 500),
+                                             -rng.standard_normal(500)])).astype(np.float32)]
+    for v in cases:
+        g, bad = _xrun(xsum, v)
+        w, wbad = X.exact_sum(v)
+        assert bad == wbad
+        if not bad:
+            assert g.view(np.uint32) == w.view(np.uint32)
+    # order independence: a permutation gives the same bits
+    v = cases[-1]
+    assert _xrun(xsum, v)[0].view(np.uint32) == _xrun(xsum, v[::-1].copy())[0].view(np.uint32)
+    # a non-finite emit or a total beyond f32 flags the bin
+    assert _xrun(xsum, np.array([1.0, np.inf], np.float32))[1]
+    assert _xrun(xsum, np.full(5000, 3.4e38, np.float32))[1]
+
+
+@pytest.fixture(scope="module")
+def libm(tmp_path_factory):
+    return _build("tests/native/libm_check.cc", str(tmp_path_factory.mktemp("n") / "libm_check"))
+
+
+def test_erfinv_matches_glibc_reference_on_every_normal_argument(libm):
+    """tm_erfinvf (device) vs the reference CPU target's formula with glibc's log, over all 2^23 arguments that
+    jax.random.normal passes to erf_inv: bitwise."""
+    r = subprocess.run([libm, "erfinv_normal"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+    assert ", 0 f32 mismatches" in r.stdout
+
+
+def test_log_within_one_ulp_of_glibc(libm):
+    r = subprocess.run([libm, "log", "2000000", "5"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+
+
+def test_generated_modules_compile_for_gfx950():
+    """the forward modules of configs 1 and 2 compile through the product's hipRTC path (no GPU needed)."""
+    from tallymap_amd import _core as C
+    from tallymap_amd import configs
+    from tallymap_amd._api import build_program
+    from tallymap_amd.backend import compile as Cm
+    from tallymap_amd.backend import kernel as K
+    for name in ("c1", "c2"):
+        cfg = configs.CONFIGS[name]
+        args = getattr(configs, f"{name}_inputs")(8)
+        axes = cfg["in_axes"]
+        pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
+        bav = [C.AVal(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
+        prog, _ = build_program(cfg["item"], cfg["outputs"], axes, pav, bav, cfg["max_steps"])
+        src, L = K.build(prog)
+        assert L.mode == "step"
+        img = Cm.code_object(src)
+        assert img[:4] == b"\x7fELF" or len(img) > 1000
