@@ -48,7 +48,7 @@ def lib():
         L.tmref_exact_sum.restype = _f
         L.tmref_exact_sum.argtypes = [_p, _i64, _p]
         L.tmref_c1_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
-        L.tmref_c1_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p]
+        L.tmref_c1_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
         L.tmref_c2_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p]
         L.tmref_c2_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
         L.tmref_c2_x0.argtypes = [_p, _i64, _p]
@@ -133,14 +133,18 @@ def c1_fwd(xs, keys, theta, max_steps=100, nthreads=0, shadow=True):
     return Fwd({"hist": hist}, {"hist": h64}, ks, tr.astype(bool), st)
 
 
-def c1_grad(xs, keys, theta, ct, max_steps=100, nthreads=0):
+def c1_grad(xs, keys, theta, ct, max_steps=100, nthreads=0, per_item=False):
+    """forward-mode gradient of sum_b ct[b] hist[b]: (d/d theta exact-summed, [d/d xs per item], n_truncated)."""
     xs = np.ascontiguousarray(xs, np.float32)
     keys = np.ascontiguousarray(keys, np.uint32)
     ct = np.ascontiguousarray(ct, np.float32)
     out = np.zeros(1, np.float32)
+    dxs = np.zeros(xs.shape[0], np.float32) if per_item else None
     ntr = np.zeros(1, np.int32)
     lib().tmref_c1_grad(_ptr(xs), _ptr(keys), float(np.float32(theta)), xs.shape[0], max_steps, nthreads, _ptr(ct),
-                        _ptr(out), _ptr(ntr))
+                        _ptr(out), _ptr(dxs), _ptr(ntr))
+    if per_item:
+        return out[0], dxs, int(ntr[0])
     return out[0], int(ntr[0])
 
 

@@ -308,27 +308,33 @@ static int team_size(int nthreads) {
 /* reference examples/quickstart.py:19-28: per step k, u = uniform(fold_in(key, k)); add
  * theta * (1 - x) to hist[int32(x * 16)]; x *= 0.5 + 0.5 u; while x > 0.05.  Gradient: d(sum_b ct[b] hist[b]) /
  * d theta in forward mode, tangent of theta = 1. */
-typedef struct { i32 k; u32 trunc; float g; } c1_res;
+typedef struct { i32 k; u32 trunc; float g, gx; } c1_res;
 
 static inline c1_res c1_item(const float* xs, const u32* keys, float theta, i64 i, int M, tm_thr* t,
                              const float* ct) {
   const u32* key = keys + 2 * i;
   float x = xs[i];
+  float dx = 1.0f;          /* tangent of x w.r.t. its own start value x0 */
   i32 k = 0, cap = 0;
-  float g = 0.0f;
+  float g = 0.0f, gx = 0.0f;
   while (cap < M && x > 0.05f) {
     u32 fk[2];
     fold_in(key, (u32)k, fk);
     const float u = uniform_f32(fk, 0.0f, 1.0f);
     const i32 idx = f2i(x * 16.0f);
     const float omx = 1.0f - x;
+    const float f = 0.5f + 0.5f * u;
     if (t) emit(t, 0, idx, theta * omx);
-    if (ct && (u32)idx < 16u) g = g + ct[idx] * omx;     /* tangent of theta * (1 - x) is 1 * (1 - x) */
+    if (ct && (u32)idx < 16u) {
+      g = g + ct[idx] * omx;               /* d(theta * (1 - x)) / d theta = 1 - x */
+      gx = gx + ct[idx] * (-theta * dx);   /* d(theta * (1 - x)) / d x0 = -theta dx */
+    }
     k = k + 1;
-    x = x * (0.5f + 0.5f * u);
+    x = x * f;
+    dx = dx * f;
     ++cap;
   }
-  c1_res r = {k, (u32)(cap >= M && x > 0.05f), g};
+  c1_res r = {k, (u32)(cap >= M && x > 0.05f), g, gx};
   return r;
 }
 
@@ -362,7 +368,7 @@ int tmref_c1_fwd(const float* xs, const u32* keys, float theta, i64 n, int M, in
 /* gradient: exact sum over items of each item's f32 forward-mode cotangent; out[0] = d/d theta; per-item trip
  * counts and truncation flags as in the forward pass (the adjoint's own replay flags) */
 int tmref_c1_grad(const float* xs, const u32* keys, float theta, i64 n, int M, int nthreads, const float* ct,
-                  float* dtheta, i32* ntrunc) {
+                  float* dtheta, float* dxs, i32* ntrunc) {
   exsum tot;
   memset(&tot, 0, sizeof(tot));
   i64 ctr = 0;
@@ -380,6 +386,7 @@ int tmref_c1_grad(const float* xs, const u32* keys, float theta, i64 n, int M, i
       if (i >= n) break;
       const c1_res r = c1_item(xs, keys, theta, i, M, NULL, ct);
       ex_add(&e, r.g);
+      if (dxs) dxs[i] = r.gx;
       mytr += (i32)r.trunc;
     }
 #pragma omp critical

@@ -6,8 +6,8 @@ one persistent wave64 kernel through the C-ABI library libtallymap_rocm.so.  Rev
 checkpointed replay adjoint through the same path.
 """
 from . import lax, numpy, random
-from ._api import STATS, Result, Sum, TallyError, UnsupportedError, vmap
+from ._api import STATS, Result, Sum, TallyError, UnsupportedError, grad, vjp, vmap
 from ._tally import Tally
 
 __version__ = "0.1.0"
-__all__ = ["vmap", "Sum", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]
+__all__ = ["vmap", "vjp", "grad", "Sum", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]

@@ -1,0 +1,325 @@
+"""Reverse-mode differentiation of straight-line item programs (the step VJPs of the replay adjoint).
+
+vjp_jaxpr(jx, active) builds a program that takes jx's inputs and the cotangents of jx's active float outputs and
+returns the cotangents of its active inputs: the forward equations are replayed (the emitter keeps what the
+reverse sweep reads; the compiler drops the rest), then every equation with an active float result is transposed,
+newest first.  The rules are the derivatives JAX's own rules state (jax/_src/lax/lax.py jvp rules, transposed);
+operation order inside them fixes the last bits of a per-item cotangent, which the reference tolerates (gradients
+are judged at 1e-4, reference tests/reverse.py).
+
+An emit `t.add(name, i, v)` contributes ct_tally[name][i] to v's cotangent (0 when i is out of range, like the
+dropped emit: reference _tally.py:72-82), read through the `tm_ct_read` primitive.
+Activity: an input is active when the caller perturbs it; a float result is active when an operand is active and
+the primitive is differentiable (comparisons, conversions to integers, floor / ceil / round / sign, threefry,
+stop_gradient and integer arithmetic end activity).
+"""
+import numpy as np
+
+from . import _core as C
+from . import lax as L
+
+ZERO_D = {"floor", "ceil", "round", "sign", "stop_gradient", "eq", "ne", "lt", "le", "gt", "ge", "and", "or",
+          "not", "xor", "threefry2x32", "shift_left", "shift_right_logical", "shift_right_arithmetic",
+          "bitcast_convert_type"}
+
+
+class ADError(NotImplementedError):
+    pass
+
+
+def _isf(aval):
+    return aval.dtype in (C.F32, C.F64)
+
+
+def activity(jx, active_in):
+    """ids of jx's active vars (inputs flagged in active_in, and float results of differentiable equations on
+    active operands)."""
+    act = {v.id for v, a in zip(jx.invars, active_in) if a and _isf(v.aval)}
+    for e in jx.eqns:
+        if e.prim in ZERO_D:
+            continue
+        if e.prim == "tallymap_emit":
+            continue
+        if e.prim in ("while", "cond"):
+            if any(isinstance(v, C.Var) and v.id in act for v in e.invars):
+                raise ADError(f"reverse mode through a nested `{e.prim}` with active operands is not supported yet "
+                              "(only the item's top-level loop is differentiated)")
+            continue
+        if any(isinstance(v, C.Var) and v.id in act for v in e.invars):
+            for o in e.outvars:
+                if _isf(o.aval):
+                    act.add(o.id)
+    return act
+
+
+def _t(v, env):
+    if isinstance(v, C.Lit):
+        return v.val.reshape(()).astype(v.aval.dtype)[()] if v.aval.shape == () else v.val
+    return env[v.id]
+
+
+def _replay(e, ins):
+    """re-bind equation e on new operands (Tracers / numpy scalars) -> output Tracers."""
+    vs = []
+    for x in ins:
+        if C.is_traced(x):
+            vs.append(x.var)
+        else:
+            a = np.asarray(x)
+            vs.append(C.Lit(a, C.AVal(a.shape, a.dtype)))
+    return C.bind(e.prim, vs, [o.aval for o in e.outvars], **e.params)
+
+
+def _f(x, dt):
+    return np.asarray(x, dt)[()]
+
+
+def _zeros_like(aval):
+    return _f(0, aval.dtype)
+
+
+def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True):
+    """-> (Jaxpr, ct_out_mask, ct_in_mask).
+    The Jaxpr's invars: jx.invars + [cotangent of each output in ct_out_mask]; outvars: [cotangent of each input
+    in ct_in_mask].  ct_out_mask: jx's active float outputs; ct_in_mask: jx's active inputs.
+    ct_read(slot, idx) -> the cotangent tally value (a Tracer) for an emit into tally `slot` at index idx; slots:
+    {invar index of a tally input: its slot}."""
+    tslot = {jx.invars[i].id: s for i, s in (slots or {}).items()}
+    act = activity(jx, active_in)
+    ct_out_mask = [isinstance(v, C.Var) and v.id in act for v in jx.outvars]
+    ct_in_mask = [v.id in act for v in jx.invars]
+    b = C.Builder()
+    C._STACK.append(b)
+    try:
+        prim = [C.Tracer(b.new_invar(v.aval)) for v in jx.invars]
+        cts_in = [C.Tracer(b.new_invar(v.aval)) for v, m in zip(jx.outvars, ct_out_mask) if m]
+        env = {v.id: t for v, t in zip(jx.invars, prim)}
+        recs = []
+        for e in jx.eqns:
+            ins = [_t(v, env) for v in e.invars]
+            if e.prim in ("tallymap_emit", "copy") and isinstance(e.invars[0], C.Var) and e.invars[0].id in tslot:
+                tslot[e.outvars[0].id] = tslot[e.invars[0].id]
+            if e.prim == "tallymap_emit":
+                outs = [ins[0]]
+            else:
+                outs = _replay(e, ins)
+            for o, x in zip(e.outvars, outs):
+                env[o.id] = x
+            recs.append((e, ins, outs))
+        ct = {}
+
+        def add(v, c):
+            if not isinstance(v, C.Var) or v.id not in act or c is None:
+                return
+            if v.id in ct:
+                ct[v.id] = ct[v.id] + c
+            else:
+                ct[v.id] = c
+        k = 0
+        for v, m in zip(jx.outvars, ct_out_mask):
+            if m:
+                add(v, cts_in[k])
+                k += 1
+        for e, ins, outs in reversed(recs):
+            if e.prim == "tallymap_emit":
+                val = e.invars[2]
+                if emits_active and isinstance(val, C.Var) and val.id in act:
+                    tv = e.invars[0]
+                    if not isinstance(tv, C.Var) or tv.id not in tslot:
+                        raise ADError("internal: an emit whose tally slot is unknown")
+                    add(val, ct_read(tslot[tv.id], ins[1]))
+                continue
+            if not any(o.id in ct for o in e.outvars):
+                continue
+            gs = [ct.get(o.id) for o in e.outvars]
+            rule = RULES.get(e.prim)
+            if rule is None:
+                raise ADError(f"no reverse-mode rule for `{e.prim}`")
+            cin = rule(gs, ins, outs, e)
+            for v, c in zip(e.invars, cin):
+                add(v, c)
+        res = []
+        for v, m in zip(jx.invars, ct_in_mask):
+            if m:
+                c = ct.get(v.id)
+                if c is None:
+                    c = C.Tracer(C.bind("copy", [C.Lit(0, v.aval.strong())], [v.aval.strong()])[0].var)
+                elif c.dtype != v.aval.dtype:
+                    c = C.convert(c, v.aval.dtype)
+                res.append(b.local(c.var) if C.is_traced(c) else c)
+    finally:
+        C._STACK.pop()
+    outv = []
+    for r in res:
+        outv.append(r if isinstance(r, C.Var) else C.Lit(r, C.AVal((), np.asarray(r).dtype)))
+    return C.Jaxpr(b.invars, outv, b.eqns), ct_out_mask, ct_in_mask
+
+
+# --------------------------------------------------------------------------------------------- the rules
+def _neg(x):
+    return -x
+
+
+def r_add(g, ins, outs, e):
+    return [g[0], g[0]]
+
+
+def r_sub(g, ins, outs, e):
+    return [g[0], -g[0]]
+
+
+def r_mul(g, ins, outs, e):
+    x, y = ins
+    return [g[0] * y, x * g[0]]
+
+
+def r_div(g, ins, outs, e):
+    x, y = ins
+    # jvp: g_x / y  and  -(g_y * x) * y^-2   (lax.div_p)
+    inv2 = C.bind("integer_pow", [_v(y)], [_av(y)], y=-2)[0] if C.is_traced(y) else _f(np.asarray(y) ** -2, _dt(x, y))
+    return [g[0] / y, -((g[0] * x) * inv2)]
+
+
+def _v(x):
+    return x.var if C.is_traced(x) else C.literal(x)
+
+
+def _av(x):
+    return x.aval if C.is_traced(x) else C.literal(x).aval
+
+
+def _dt(*xs):
+    for x in xs:
+        if C.is_traced(x):
+            return x.dtype
+    return np.asarray(xs[0]).dtype
+
+
+def r_neg(g, ins, outs, e):
+    return [-g[0]]
+
+
+def _balanced(x, ans, y):
+    """1 where x alone is the result, 0.5 on a tie, 0 otherwise (lax._balanced_eq)."""
+    from . import numpy as jnp
+    one = _f(1, _dt(x, y))
+    half = _f(0.5, _dt(x, y))
+    zero = _f(0, _dt(x, y))
+    return jnp.where(x == ans, jnp.where(y == ans, half, one), zero)
+
+
+def r_max(g, ins, outs, e):
+    x, y = ins
+    ans = outs[0]
+    return [g[0] * _balanced(x, ans, y), g[0] * _balanced(y, ans, x)]
+
+
+r_min = r_max
+
+
+def r_abs(g, ins, outs, e):
+    from . import numpy as jnp
+    x = ins[0]
+    return [g[0] * jnp.where(x >= 0, _f(1, x.dtype), _f(-1, x.dtype))]
+
+
+def r_sqrt(g, ins, outs, e):
+    return [g[0] * (_f(0.5, outs[0].dtype) / outs[0])]
+
+
+def r_rsqrt(g, ins, outs, e):
+    x, ans = ins[0], outs[0]
+    return [g[0] * ((ans / x) * _f(-0.5, x.dtype))]
+
+
+def r_exp(g, ins, outs, e):
+    return [g[0] * outs[0]]
+
+
+def r_log(g, ins, outs, e):
+    return [g[0] / ins[0]]
+
+
+def r_log1p(g, ins, outs, e):
+    return [g[0] / (ins[0] + _f(1, ins[0].dtype))]
+
+
+def r_expm1(g, ins, outs, e):
+    return [g[0] * (outs[0] + _f(1, outs[0].dtype))]
+
+
+def r_sin(g, ins, outs, e):
+    return [g[0] * L.cos(ins[0])]
+
+
+def r_cos(g, ins, outs, e):
+    return [g[0] * -L.sin(ins[0])]
+
+
+def r_tanh(g, ins, outs, e):
+    a = outs[0]
+    return [g[0] * (_f(1, a.dtype) - a * a)]
+
+
+def r_logistic(g, ins, outs, e):
+    a = outs[0]
+    return [g[0] * (a * (_f(1, a.dtype) - a))]
+
+
+def r_atan2(g, ins, outs, e):
+    y, x = ins
+    den = x * x + y * y
+    return [g[0] * (x / den), g[0] * (-y / den)]
+
+
+def r_pow(g, ins, outs, e):
+    x, y = ins
+    dt = _dt(x, y)
+    gx = g[0] * (y * C.binop("pow", x, y - _f(1, dt))) if C.is_traced(x) else None
+    gy = None
+    if C.is_traced(y):
+        from . import numpy as jnp
+        gy = g[0] * (outs[0] * L.log(jnp.where(x == 0, _f(1, dt), x)))
+    return [gx, gy]
+
+
+def r_integer_pow(g, ins, outs, e):
+    x = ins[0]
+    n = int(e.params["y"])
+    if n == 0:
+        return [None]
+    d = _f(n, x.dtype) if n - 1 == 0 else _f(n, x.dtype) * C.bind("integer_pow", [x.var], [x.aval], y=n - 1)[0]
+    return [g[0] * d]
+
+
+def r_erf_inv(g, ins, outs, e):
+    a = outs[0]
+    return [g[0] * (_f(np.sqrt(np.pi) / 2, a.dtype) * L.exp(a * a))]
+
+
+def r_select(g, ins, outs, e):
+    from . import numpy as jnp
+    p = ins[0]
+    z = _f(0, outs[0].dtype)
+    n = len(ins) - 1
+    if n != 2:
+        raise ADError("select_n with more than two cases")
+    return [None, jnp.where(p, z, g[0]), jnp.where(p, g[0], z)]
+
+
+def r_convert(g, ins, outs, e):
+    x = ins[0]
+    if C.is_traced(x) and _isf(x.aval):
+        return [C.convert(g[0], x.dtype)]
+    return [None]
+
+
+def r_copy(g, ins, outs, e):
+    return [g[0]]
+
+
+RULES = {"add": r_add, "sub": r_sub, "mul": r_mul, "div": r_div, "neg": r_neg, "max": r_max, "min": r_min,
+         "abs": r_abs, "sqrt": r_sqrt, "rsqrt": r_rsqrt, "exp": r_exp, "log": r_log, "log1p": r_log1p,
+         "expm1": r_expm1, "sin": r_sin, "cos": r_cos, "tanh": r_tanh, "logistic": r_logistic, "atan2": r_atan2,
+         "pow": r_pow, "integer_pow": r_integer_pow, "erf_inv": r_erf_inv, "select_n": r_select,
+         "convert_element_type": r_convert, "copy": r_copy}

@@ -369,3 +369,79 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
     mapped._opts = opts
     mapped._names = names
     return mapped
+
+
+# ----------------------------------------------------------------------------------------- reverse mode
+def _float_args(prog, axes, argnums):
+    """map positional argnums to (per-item operand indices, broadcast operand indices) (leaves of float32)."""
+    pi_idx, bc_idx = [], []
+    p = b = 0
+    for pos, x in enumerate(axes):
+        if x == 0:
+            if pos in argnums:
+                pi_idx.append(p)
+            p += 1
+        else:
+            if pos in argnums:
+                bc_idx.append(b)
+            b += 1
+    return tuple(pi_idx), tuple(bc_idx)
+
+
+def _argnums(argnums, nargs):
+    if argnums is None:
+        return tuple(range(nargs))
+    return (argnums,) if isinstance(argnums, int) else tuple(argnums)
+
+
+def vjp(mapped, *args, argnums=None):
+    """(Result, pullback): the forward call, and pullback(ct_outputs, ct_per_item=None) -> the cotangents of the
+    positional arguments in `argnums` (float32 ones; broadcast arguments' cotangents are exact float32 sums).
+    ct_outputs: {name: array or scalar (broadcast to the output)}.  The pullback launches the replay adjoint: the
+    reference's jax.vjp through tallymap_call (_primitive.py:565-667, _reverse.py:1079-1180)."""
+    res = mapped(*args)
+    return res, _pullback(mapped, args, argnums)
+
+
+def _pullback(mapped, args, argnums):
+    from . import backend as B
+    prog, meta, pi, bc, N, axes = mapped._prepare(args)
+    an = _argnums(argnums, len(args))
+    wrt = _float_args(prog, axes, an)
+
+    def pullback(ct_outputs=None, ct_per_item=None):
+        cts = {}
+        for k, s in enumerate(prog.tallies):
+            if ct_outputs and s.name in ct_outputs:
+                cts[k] = ct_outputs[s.name]
+        cys = {}
+        if ct_per_item is not None:
+            yl, _ = flatten(ct_per_item)
+            for j, x in enumerate(yl):
+                if x is not None:
+                    cys[j] = x
+        g_pi, g_bc, ntr = B.run_vjp(prog, wrt, pi, bc, N, cts, cys, mapped._opts)
+        out = []
+        gp, gb = iter(g_pi), iter(g_bc)
+        p = b = 0
+        for pos, x in enumerate(axes):
+            if pos in an:
+                if x == 0:
+                    out.append(next(gp) if p in wrt[0] else None)
+                else:
+                    g = next(gb) if b in wrt[1] else None
+                    out.append(g.reshape(np.shape(args[pos])) if g is not None else None)
+            p += x == 0
+            b += x is None
+        return tuple(out) if len(out) != 1 else out[0]
+    return pullback
+
+
+def grad(mapped, weights=None, argnums=None):
+    """the gradient of sum_name <weights[name], outputs[name]> (weights: a scalar or an array per output; default
+    1 for every float output, i.e. the gradient of the sum of all float tallies) w.r.t. the arguments in
+    argnums.  ONE launch of the replay adjoint, no forward launch (as jax.grad of a tallymap call under jit)."""
+    def g(*args):
+        return _pullback(mapped, args, argnums)(
+            weights if weights is not None else {n: 1.0 for n in mapped._names})
+    return g

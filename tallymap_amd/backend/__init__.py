@@ -155,3 +155,60 @@ def prebuild(configs, n=64):
             Cm.code_object(src, name=f"tm_{p.tag}.hip", store_pkg=True)
             done.append((name, p.tag, Cm._key(src)[:16]))
     return done
+
+
+def compiled_adjoint(adj, opts):
+    """the registered adjoint kernel of `adj` (a reverse.Adjoint) under opts."""
+    from . import reverse as R
+    block = int(opts.get("block", K.BLOCK))
+    ck = int(opts.get("rev_checkpoints", R.C_DEFAULT) or R.C_DEFAULT)
+    key = (adj.digest(), block, "adjoint", ck)
+    with _LOCK:
+        hit = _KERNELS.get(key)
+        if hit is not None:
+            _KERNELS.move_to_end(key)
+            return hit
+    src, L = R.build(adj, block=block, ckpt=ck)
+    img = Cm.code_object(src, name=f"tm_{adj.tag}.hip")
+    kid = int(Cm._key(src)[:15], 16)
+    Cm.check(Cm.lib().tm_register(kid, img, len(img), f"{adj.tag} {adj.where}".encode()))
+    c = Compiled(kid, L, block, src, adj.tag)
+    with _LOCK:
+        _KERNELS[key] = c
+        while len(_KERNELS) > KERNEL_CACHE:
+            _KERNELS.popitem(last=False)
+    return c
+
+
+def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
+    """the replay adjoint of prog: cotangents of the per-item operands wrt[0] ([N, ...] each) and the broadcast
+    operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
+    0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated)."""
+    import torch
+
+    from . import reverse as R
+    adj = R.adjoint_program(prog, wrt)
+    c = compiled_adjoint(adj, opts)
+    L = c.layout
+    ins = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
+    yav = prog.y_avals()
+    for j in L.fy:
+        x = ct_ys.get(j) if ct_ys else None
+        a = yav[j]
+        ins.append(device_tensor(x, a.dtype) if x is not None
+                   else torch.zeros((N,) + tuple(a.shape), dtype=torch.float32, device="cuda"))
+    ins += [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+    for k in L.ft:
+        s = prog.tallies[k]
+        x = ct_tallies.get(k) if ct_tallies else None
+        if x is None:
+            ins.append(torch.zeros(s.shape, dtype=torch.float32, device="cuda").reshape(-1))
+        else:
+            ins.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
+                                     else x, np.float32).reshape(-1))
+    res = launch(c, ins, N)
+    base = L.n_in
+    g_bc = [res[L.r_out[j] - base] for j in adj.wrt_bc]
+    g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
+    ntr = res[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
+    return g_pi, g_bc, ntr

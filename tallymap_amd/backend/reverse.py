@@ -1,0 +1,590 @@
+"""The replay adjoint: one HIP kernel computing reverse-mode cotangents of an item program (reference
+tallymap/_reverse.py: vjp_prog 1079-1180, checkpointed_while 324-444).
+
+The item is split at its top-level while loop into PRE (operands -> loop carries and the values P the loop's
+constants and the tail read), BODY / COND (one step), POST (final carries -> per-item results, emits).  The adjoint
+of one item, run by one lane:
+
+  1. PRE, then the COUNT pass: the (capped) loop runs to its end, K steps, storing the states before steps
+     0..C-1 in the HEAD buffer H.
+  2. POST's VJP seeds the carries' cotangent lambda from the per-item result cotangents and the tally cotangents
+     of POST's emits (an emit's value gets ct_tally[index]).
+  3. The reverse sweep applies BODY's VJP newest step first.  K <= C: straight from H.  K > C: one replay stores a
+     checkpoint every m = max(C, ceil(K/C)) steps (CK), then each segment, last first, is refilled into the tape T
+     in chunks of at most C states (a chunk's start is re-advanced from the segment's checkpoint) and swept.
+     Work: ~3K steps + K step-VJPs for K <= C^2, plus K^2/(2C^2) beyond; per-lane memory 3C states (private
+     arrays).  The per-item cotangents do not depend on C (replays are bit-exact).
+     When no loop carry is active (a parameter reaches the tallies only through emitted values, not through the
+     state), lambda is identically zero: the step VJPs run inside the count pass, in forward order, and nothing is
+     stored or replayed.
+  4. PRE's VJP maps the carries' and the loop constants' cotangents onto the operands.  A broadcast operand's
+     cotangent is added into the exact accumulator (one emit per item and element, LDS-privatised 5-word bins, read
+     out once: reference _reverse.py:1172-1177); a per-item operand's cotangent is written per item.
+
+A truncated item (max_steps) is replayed with the same cap; any truncation makes every float cotangent NaN
+(reference _primitive.py:586-594), applied by tm_post.
+"""
+import dataclasses
+
+import numpy as np
+
+from .. import _ad as AD
+from .. import _core as C
+from .._api import ItemProgram, TSpec
+from . import kernel as K
+from .codegen import Emitter, Val, VTally, assign_carries, ctype
+
+C_DEFAULT = 16
+
+
+class ReverseError(NotImplementedError):
+    pass
+
+
+@dataclasses.dataclass
+class Adjoint:
+    prog: object            # the forward ItemProgram
+    wrt_pi: tuple           # per-item operand indices differentiated
+    wrt_bc: tuple           # broadcast operand indices differentiated
+    tag: str
+    where: str
+
+    def digest(self):
+        return self.prog.digest() + f"|vjp|{self.wrt_pi}|{self.wrt_bc}"
+
+
+def default_wrt(prog):
+    """every float operand."""
+    wp = tuple(i for i, a in enumerate(prog.p_avals()) if a.dtype == C.F32)
+    wb = tuple(i for i, a in enumerate(prog.b_avals()) if a.dtype == C.F32)
+    return wp, wb
+
+
+def adjoint_program(prog, wrt):
+    wp, wb = wrt
+    for i in wb:
+        if prog.b_avals()[i].dtype != C.F32:
+            raise ReverseError("reverse mode: only float32 broadcast operands are differentiated (their cotangents "
+                               "are exact float32 sums)")
+    for i in wp:
+        if prog.p_avals()[i].dtype != C.F32:
+            raise ReverseError("reverse mode: only float32 per-item operands are differentiated")
+    return Adjoint(prog, tuple(wp), tuple(wb), prog.tag + "+vjp", prog.where)
+
+
+# ------------------------------------------------------------------------------------------ the split
+@dataclasses.dataclass
+class Split:
+    pre: C.Jaxpr            # invars = item invars; outvars = [init carries] + [P vars]
+    cond: C.Jaxpr           # [cond consts] + carries -> pred
+    body: C.Jaxpr           # [body consts] + carries -> carries
+    post: C.Jaxpr           # invars = [P vars] + [final carries]; outvars = item outvars
+    nP: int                 # number of P vars
+    ncar: int
+    cconst: list            # per cond const: ('P', j) | ('L', Lit)
+    bconst: list            # per body const
+    car_slot: list          # per carry: tally slot or None
+
+
+def split(prog):
+    jx = prog.jaxpr
+    nT = prog.nT
+    ws = [i for i, e in enumerate(jx.eqns) if e.prim == "while"]
+    if len(ws) != 1:
+        raise ReverseError(f"reverse mode needs exactly one top-level while loop in the item (found {len(ws)})")
+    w = ws[0]
+    we = jx.eqns[w]
+    pre_e, post_e = jx.eqns[:w], jx.eqns[w + 1:]
+    nc, nb = we.params["cond_nconsts"], we.params["body_nconsts"]
+    cc, bc, init = we.invars[:nc], we.invars[nc:nc + nb], we.invars[nc + nb:]
+    # the slot of each tally value defined before the loop
+    slot = {v.id: k for k, v in enumerate(jx.invars[:nT])}
+    for e in pre_e:
+        if e.prim in ("tallymap_emit", "copy") and isinstance(e.invars[0], C.Var) and e.invars[0].id in slot:
+            slot[e.outvars[0].id] = slot[e.invars[0].id]
+    car_slot = [slot.get(v.id) if isinstance(v, C.Var) else None for v in init]
+    # P: non-tally vars read by the loop's constants or by POST, defined before the loop (operands or PRE results)
+    post_free = set()
+    for e in post_e:
+        for v in e.invars:
+            if isinstance(v, C.Var):
+                post_free.add(v.id)
+        for sub in C.subjaxprs(e):
+            post_free |= _free(sub)
+    for v in jx.outvars:
+        if isinstance(v, C.Var):
+            post_free.add(v.id)
+    defined_before = {v.id: v for v in jx.invars}
+    for e in pre_e:
+        for o in e.outvars:
+            defined_before[o.id] = o
+    need = [v for v in cc + bc if isinstance(v, C.Var)]
+    need += [defined_before[i] for i in sorted(post_free) if i in defined_before]
+    P, seen = [], set()
+    for v in need:
+        if v.id in seen or v.id in slot:
+            continue
+        seen.add(v.id)
+        P.append(v)
+    pidx = {v.id: j for j, v in enumerate(P)}
+
+    def const_ref(v):
+        return ("L", v) if isinstance(v, C.Lit) else ("P", pidx[v.id])
+    pre_out = []
+    for v in init:
+        pre_out.append(v)
+    pre = C.Jaxpr(list(jx.invars), pre_out + P, pre_e)
+    post_in_car = [C.Var(o.aval) for o in we.outvars]
+    ren = {o.id: nv for o, nv in zip(we.outvars, post_in_car)}
+    post = C.Jaxpr([_ren(v, ren) for v in P] + post_in_car, [_ren(v, ren) for v in jx.outvars],
+                   [_ren_eqn(e, ren) for e in post_e])
+    # (P vars keep their identity inside POST: their ids are the same objects)
+    post = C.Jaxpr(list(P) + post_in_car, post.outvars, post.eqns)
+    return Split(pre, we.params["cond_jaxpr"], we.params["body_jaxpr"], post, len(P), len(init),
+                 [const_ref(v) for v in cc], [const_ref(v) for v in bc], car_slot)
+
+
+def _free(jx):
+    defined = {v.id for v in jx.invars}
+    free = set()
+    for e in jx.eqns:
+        for v in e.invars:
+            if isinstance(v, C.Var) and v.id not in defined:
+                free.add(v.id)
+        for o in e.outvars:
+            defined.add(o.id)
+    return free
+
+
+def _ren(v, m):
+    return m.get(v.id, v) if isinstance(v, C.Var) else v
+
+
+def _ren_eqn(e, m):
+    return C.Eqn(e.prim, [_ren(v, m) for v in e.invars], e.outvars, e.params)
+
+
+# ------------------------------------------------------------------------------------------ the kernel
+def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
+    """-> (HIP source, Layout) of the adjoint module."""
+    prog = adj.prog
+    jx = prog.jaxpr
+    nT, nP, nB = prog.nT, prog.nP, prog.nB
+    pav, bav, yav = prog.p_avals(), prog.b_avals(), prog.y_avals()
+    sp = split(prog)
+    ft = [k for k in prog.out_tallies if prog.tallies[k].dtype in (C.F32,)]        # tallies with a cotangent input
+    fy = [j for j, a in enumerate(yav) if a.dtype == C.F32]                           # per-item results with one
+    # ---- buffers: inputs [pi][ct_y (float ys)][bc][ct tallies]; results [ct_bc][scratch][ctl][stats] | [ct_pi][trunc]
+    i_pi = list(range(nP))
+    i_cty = list(range(nP, nP + len(fy)))
+    i_bc = list(range(nP + len(fy), nP + len(fy) + nB))
+    i_ctt = list(range(nP + len(fy) + nB, nP + len(fy) + nB + len(ft)))
+    n_in = nP + len(fy) + nB + len(ft)
+    res = []
+
+    def result(shape, dt, per_item=False):
+        res.append((tuple(shape), np.dtype(dt), per_item))
+        return n_in + len(res) - 1
+    r_gbc = {j: result(bav[j].shape, np.float32) for j in adj.wrt_bc}
+    r_scr = {j: result((K.exact_words(max(1, bav[j].size)),), np.uint32) for j in adj.wrt_bc}
+    r_ctl = result((8,), np.uint32)
+    r_stats = result((5,), np.int32)
+    n_zero = len(res)
+    r_gpi = {i: result(pav[i].shape, np.float32, per_item=True) for i in adj.wrt_pi}
+    r_tr = result((), np.bool_, per_item=True) if prog.trunc is not None else None
+    R = n_in + len(res)
+
+    # ---- activity: operands perturbed -> P active -> carries active (fixpoint over the body)
+    pre_act_in = [False] * nT + [i in adj.wrt_pi for i in range(nP)] + [j in adj.wrt_bc for j in range(nB)]
+    act_pre = AD.activity(sp.pre, pre_act_in)
+    P_act = [v.id in act_pre for v in sp.pre.outvars[sp.ncar:]]
+    car_act = [isinstance(v, C.Var) and v.id in act_pre for v in sp.pre.outvars[:sp.ncar]]
+    car_act = [a and s is None for a, s in zip(car_act, sp.car_slot)]
+    bconst_act = [r[0] == "P" and P_act[r[1]] for r in sp.bconst]
+    while True:
+        a = AD.activity(sp.body, bconst_act + car_act)
+        new = [ca or (isinstance(o, C.Var) and o.id in a and s is None)
+               for ca, o, s in zip(car_act, sp.body.outvars, sp.car_slot)]
+        if new == car_act:
+            break
+        car_act = new
+    active_carries = any(car_act)
+
+    def ct_read_factory():
+        def ct_read(slot, idx):
+            if slot not in ft:
+                return np.float32(0.0)
+            return C.bind("tm_ct_read", [idx.var if C.is_traced(idx) else C.literal(int(idx), C.I32, False)],
+                          [C.AVal((), C.F32)], slot=slot)[0]
+        return ct_read
+    body_slots = {len(sp.bconst) + j: s for j, s in enumerate(sp.car_slot) if s is not None}
+    body_vjp, b_ctout, b_ctin = AD.vjp_jaxpr(sp.body, bconst_act + car_act, ct_read_factory(), body_slots)
+    post_slots = {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None}
+    post_act = P_act + [a for a in car_act]
+    post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, post_act, ct_read_factory(), post_slots)
+    pre_slots = {k: k for k in range(nT)}
+    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pre_act_in, ct_read_factory(), pre_slots)
+    # the cotangent a body step produces for a carry that is not active must not exist; check the masks agree
+    for j, (ci, ca) in enumerate(zip(b_ctin[len(sp.bconst):], car_act)):
+        if ci and not ca:
+            raise ReverseError("internal: carry activity mismatch")
+
+    # ---- emitter with the adjoint's hooks
+    em = Emitter()
+    em.hooks["tallymap_emit"] = lambda em_, e, ins: ins[0]
+
+    def ct_rule(em_, e, ins):
+        k = e.params["slot"]
+        S = prog.tallies[k].S
+        idx = ins[0].el[0]
+        ptr = f"((const float*)P.p[{i_ctt[ft.index(k)]}])"
+        return Val([em_.bind(f"((u32)({idx}) < {S}u ? {ptr}[{idx}] : 0.0f)", C.F32, "ct")], (), C.F32)
+    em.hooks["tm_ct_read"] = ct_rule
+
+    lines = []
+
+    def out(s, ind=0):
+        lines.append("  " * ind + s)
+
+    def run_block(jxp, ins, ind):
+        em.lines, em.ind = [], ind
+        r = em.run(jxp, ins)
+        lines.extend(em.lines)
+        return r
+
+    # kernel-scope names
+    bvals = [Val([f"tm_b{i}_{e}" for e in range(max(1, a.size))], a.shape, a.dtype) for i, a in enumerate(bav)]
+    tallies = [VTally(k) for k in range(nT)]
+    car_names = []
+    decls = []
+    car_avals = [v.aval for v in sp.body.outvars]
+    for j, a in enumerate(car_avals):
+        if sp.car_slot[j] is not None:
+            car_names.append(None)
+            continue
+        names = [f"tm_c{j}_{e}" for e in range(max(1, a.size))]
+        car_names.append(names)
+        for n in names:
+            decls.append(f"  {ctype(a.dtype)} {n};")
+
+    def car_vals():
+        return [VTally(sp.car_slot[j]) if names is None else Val(names, car_avals[j].shape, car_avals[j].dtype)
+                for j, names in enumerate(car_names)]
+    # the stored state: every non-tally carry (the replay needs all of them)
+    st_elems = [(n, car_avals[j].dtype) for j, names in enumerate(car_names) if names is not None for n in names]
+    lam_names = {}
+    for j, names in enumerate(car_names):
+        if names is not None and car_act[j]:
+            lam_names[j] = [f"tm_l{j}_{e}" for e in range(len(names))]
+            for n in lam_names[j]:
+                decls.append(f"  float {n};")
+
+    def const_val(ref, Pv):
+        kind, x = ref
+        if kind == "L":
+            return em.value_of({}, x)
+        return Pv[x]
+
+    src = [__import__("tallymap_amd.backend.compile", fromlist=["prelude"]).prelude(),
+           f"struct TmParams {{ void* p[{R}]; }};",
+           f"#define TM_STATS ((i32*)P.p[{r_stats}])", f"#define TM_CTL ((u32*)P.p[{r_ctl}])"]
+    zero_words = []
+    for j in adj.wrt_bc:
+        zero_words.append((r_gbc[j], max(1, bav[j].size)))
+        zero_words.append((r_scr[j], K.exact_words(max(1, bav[j].size))))
+    zero_words += [(r_ctl, 8), (r_stats, 5)]
+    src.append("extern \"C\" __global__ void tm_zero(const TmParams P, const i64 n_items) {\n"
+               "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, s = (i64)gridDim.x * blockDim.x;\n"
+               + "\n".join(f"  for (i64 i = g; i < {nw}; i += s) ((u32*)P.p[{b}])[i] = 0u;" for b, nw in zero_words)
+               + "\n}")
+    # tm_post: exact readout of the broadcast cotangents; NaN everywhere when an item was truncated
+    post_l = []
+    for j in adj.wrt_bc:
+        S = max(1, bav[j].size)
+        words = f"((const u64*)P.p[{r_scr[j]}])"
+        fl = f"((const u32*)P.p[{r_scr[j]}] + {2 * K.XW * S})"
+        post_l.append(f"for (i64 i = g; i < {S}; i += st) {{ bool bad = false; "
+                      f"const float o = tm_xread(&{words}[i * {K.XW}], &bad); "
+                      f"const bool f = (({fl}[i >> 5] >> (i & 31)) & 1u) != 0u; "
+                      f"if (f || bad) atomicAdd(&TM_STATS[3], 1); "
+                      f"((float*)P.p[{r_gbc[j]}])[i] = (TM_CTL[2] != 0u || f || bad) ? __builtin_nanf(\"\") : o; }}")
+    for i in adj.wrt_pi:
+        n = max(1, pav[i].size)
+        post_l.append(f"if (TM_CTL[2] != 0u) for (i64 i = g; i < n_items * {n}; i += st) "
+                      f"((float*)P.p[{r_gpi[i]}])[i] = __builtin_nanf(\"\");")
+    src.append("extern \"C\" __global__ void tm_post(const TmParams P, const i64 n_items) {\n"
+               "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, st = (i64)gridDim.x * blockDim.x;\n  "
+               + "\n  ".join(post_l) + "\n}")
+
+    # ---------------------------------------------------------------------------------- tm_main
+    out(f"extern \"C\" __global__ void __launch_bounds__({block}) tm_main(const TmParams P, const i64 n_items) {{")
+    out(f"  u64* const tm_ctr = (u64*)P.p[{r_ctl}];")
+    for j in adj.wrt_bc:
+        S = max(1, bav[j].size)
+        out(f"  __shared__ u64 tm_xsh{j}[{K.XW * S}];")
+        out(f"  __shared__ u32 tm_xfl{j}[{(S + 31) // 32}];")
+        out(f"  for (int i = threadIdx.x; i < {K.XW * S}; i += blockDim.x) tm_xsh{j}[i] = 0ull;")
+        out(f"  for (int i = threadIdx.x; i < {(S + 31) // 32}; i += blockDim.x) tm_xfl{j}[i] = 0u;")
+    if adj.wrt_bc:
+        out("  __syncthreads();")
+    for i, a in enumerate(bav):
+        ct = ctype(a.dtype)
+        for e in range(max(1, a.size)):
+            out(f"  const {ct} tm_b{i}_{e} = ((const {ct}*)P.p[{i_bc[i]}])[{e}];")
+    out("  u32 tm_ntr = 0;")
+    lines.extend(decls)
+    if active_carries:
+        for q, (n, dt) in enumerate(st_elems):
+            for buf in ("H", "K", "T"):
+                out(f"  {ctype(dt)} tm_{buf}{q}[{ckpt}];")
+    out("  bool tm_more = true;")
+    out("  while (tm_more) {")
+    out("    const u64 tm_base = tm_claim(tm_ctr, 64u);")       # item schedule: the whole wave claims 64 items
+    out("    if (tm_base + 64u >= (u64)n_items) tm_more = false;")
+    out("    const u64 tm_t = tm_base + (u64)tm_lane();")
+    out("    if (tm_t >= (u64)n_items) continue;")
+    out("    const i64 tm_item = (i64)tm_t;")
+    # operands
+    em.lines, em.ind = [], 2
+    pis = []
+    for i, a in enumerate(pav):
+        n = max(1, a.size)
+        ct = ctype(a.dtype)
+        pis.append(Val([em.bind(f"((const {ct}*)P.p[{i_pi[i]}])[tm_item * {n} + {e}]", a.dtype, "x")
+                        for e in range(n)], a.shape, a.dtype))
+    ctys = []
+    for jj, j in enumerate(fy):
+        a = yav[j]
+        n = max(1, a.size)
+        ctys.append(Val([em.bind(f"((const float*)P.p[{i_cty[jj]}])[tm_item * {n} + {e}]", C.F32, "cy")
+                         for e in range(n)], a.shape, a.dtype))
+    lines.extend(em.lines)
+    item_ins = tallies + pis + bvals
+    pre_outs = run_block(sp.pre, item_ins, 2)
+    Pv = pre_outs[sp.ncar:]
+    # carries <- init
+    for j, names in enumerate(car_names):
+        if names is None:
+            continue
+        for n, el in zip(names, pre_outs[j].el):
+            out(f"{n} = {el};", 2)
+    cc_vals = lambda: [const_val(r, Pv) for r in sp.cconst]
+    bc_vals = lambda: [const_val(r, Pv) for r in sp.bconst]
+    # cotangent accumulators of the active body constants (f32, per item)
+    gconst = {}
+    for q, (r, a) in enumerate(zip(sp.bconst, bconst_act)):
+        if a:
+            av = sp.body.invars[q].aval
+            gconst[q] = [f"tm_gk{q}_{e}" for e in range(max(1, av.size))]
+            for n in gconst[q]:
+                out(f"float {n} = 0.0f;", 2)
+
+    def step_vjp(ind, lam_seed_zero=False):
+        """BODY's VJP at the current carries, with lambda (zero when no carry is active); updates lambda and the
+        constants' accumulators."""
+        ins = bc_vals() + car_vals()
+        cts = []
+        for j, (o, m) in enumerate(zip(sp.body.outvars, b_ctout)):
+            if m:
+                if j in lam_names:
+                    cts.append(Val(lam_names[j], car_avals[j].shape, C.F32))
+                else:
+                    cts.append(Val(["0.0f"] * max(1, car_avals[j].size), car_avals[j].shape, C.F32))
+        r = run_block(body_vjp, ins + cts, ind)
+        k = 0
+        new_lam = {}
+        for q, m in enumerate(b_ctin):
+            if not m:
+                continue
+            v = r[k]
+            k += 1
+            if q < len(sp.bconst):
+                for n, el in zip(gconst[q], v.el):
+                    out(f"{n} = {n} + {el};", ind)
+            else:
+                new_lam[q - len(sp.bconst)] = v
+        for j, v in new_lam.items():
+            if j in lam_names:
+                for n, el in zip(lam_names[j], v.el):
+                    out(f"{n} = {el};", ind)
+
+    def body_fwd(ind):
+        em.lines, em.ind = [], ind
+        cars = car_vals()
+        o = em.run(sp.body, bc_vals() + cars)
+        assign_carries(em, cars, o)
+        lines.extend(em.lines)
+
+    def cond_pred(ind):
+        return run_block(sp.cond, cc_vals() + car_vals(), ind)[0].el[0]
+
+    def store(buf, idx, ind):
+        for q, (n, dt) in enumerate(st_elems):
+            out(f"tm_{buf}{q}[{idx}] = {n};", ind)
+
+    def load(buf, idx, ind):
+        for q, (n, dt) in enumerate(st_elems):
+            out(f"{n} = tm_{buf}{q}[{idx}];", ind)
+    # 1. count pass
+    out("i32 tm_K = 0;", 2)
+    out("while (true) {", 2)
+    p = cond_pred(3)
+    out(f"if (!({p})) break;", 3)
+    if active_carries:
+        out(f"if (tm_K < {ckpt}) {{", 3)
+        store("H", "tm_K", 4)
+        out("}", 3)
+    else:
+        step_vjp(3)
+    body_fwd(3)
+    out("++tm_K;", 3)
+    out("}", 2)
+    # 2. POST forward (the truncation flag) and POST's VJP -> lambda, P cotangents
+    post_ins = Pv + car_vals()
+    post_fwd = run_block(sp.post, post_ins, 2)
+    if prog.trunc is not None:
+        tr = post_fwd[nT + prog.trunc].el[0]
+        out(f"((bool*)P.p[{r_tr}])[tm_item] = {tr};", 2)
+        out(f"if ({tr}) ++tm_ntr;", 2)
+    post_cts = []
+    for j, (o, m) in enumerate(zip(sp.post.outvars, p_ctout)):
+        if not m:
+            continue
+        q = j - nT
+        if q >= 0 and q in fy:
+            post_cts.append(ctys[fy.index(q)])
+        else:
+            post_cts.append(Val(["0.0f"] * max(1, o.aval.size), o.aval.shape, C.F32))
+    pr = run_block(post_vjp, post_ins + post_cts, 2)
+    gP = {}
+    k = 0
+    for q, m in enumerate(p_ctin):
+        if not m:
+            continue
+        v = pr[k]
+        k += 1
+        if q < sp.nP:
+            gP[q] = [f"tm_gp{q}_{e}" for e in range(len(v.el))]
+            for n, el in zip(gP[q], v.el):
+                out(f"float {n} = {el};", 2)
+        else:
+            j = q - sp.nP
+            if j in lam_names:
+                for n, el in zip(lam_names[j], v.el):
+                    out(f"{n} = {el};", 2)
+    for j in lam_names:
+        if not p_ctin[sp.nP + j]:
+            for n in lam_names[j]:
+                out(f"{n} = 0.0f;", 2)
+    # 3. the reverse sweep
+    if active_carries:
+        out(f"if (tm_K <= {ckpt}) {{", 2)
+        out("for (i32 tm_j = tm_K - 1; tm_j >= 0; --tm_j) {", 3)
+        load("H", "tm_j", 4)
+        step_vjp(4)
+        out("}", 3)
+        out("} else {", 2)
+        out(f"const i32 tm_m = tm_K <= {ckpt * ckpt} ? {ckpt} : (tm_K + {ckpt - 1}) / {ckpt};", 3)
+        load("H", "0", 3)
+        out("for (i32 tm_k = 0; tm_k < tm_K; ++tm_k) {", 3)
+        out("if (tm_k % tm_m == 0) {", 4)
+        store("K", "tm_k / tm_m", 5)
+        out("}", 4)
+        body_fwd(4)
+        out("}", 3)
+        out("const i32 tm_ns = (tm_K + tm_m - 1) / tm_m;", 3)
+        out("for (i32 tm_s = tm_ns - 1; tm_s >= 0; --tm_s) {", 3)
+        out("const i32 tm_a = tm_s * tm_m, tm_b = tm_a + tm_m < tm_K ? tm_a + tm_m : tm_K;", 4)
+        out("for (i32 tm_hi = tm_b; tm_hi > tm_a;) {", 4)
+        out(f"const i32 tm_lo = tm_hi - {ckpt} > tm_a ? tm_hi - {ckpt} : tm_a;", 5)
+        load("K", "tm_s", 5)
+        out("for (i32 tm_k = tm_a; tm_k < tm_lo; ++tm_k) {", 5)
+        body_fwd(6)
+        out("}", 5)
+        out("for (i32 tm_k = tm_lo; tm_k < tm_hi; ++tm_k) {", 5)
+        store("T", "tm_k - tm_lo", 6)
+        body_fwd(6)
+        out("}", 5)
+        out("for (i32 tm_k = tm_hi - 1; tm_k >= tm_lo; --tm_k) {", 5)
+        load("T", "tm_k - tm_lo", 6)
+        step_vjp(6)
+        out("}", 5)
+        out("tm_hi = tm_lo;", 5)
+        out("}", 4)
+        out("}", 3)
+        out("}", 2)
+    # 4. PRE's VJP: cotangents of the outputs [init carries] + [P]
+    pre_cts = []
+    for j, (o, m) in enumerate(zip(sp.pre.outvars, r_ctout)):
+        if not m:
+            continue
+        if j < sp.ncar:
+            if j in lam_names:
+                pre_cts.append(Val(lam_names[j], o.aval.shape, C.F32))
+            else:
+                pre_cts.append(Val(["0.0f"] * max(1, o.aval.size), o.aval.shape, C.F32))
+        else:
+            q = j - sp.ncar
+            terms = []
+            if q in gP:
+                terms.append(gP[q])
+            for bq, r in enumerate(sp.bconst):
+                if r[0] == "P" and r[1] == q and bq in gconst:
+                    terms.append(gconst[bq])
+            n = max(1, o.aval.size)
+            if not terms:
+                pre_cts.append(Val(["0.0f"] * n, o.aval.shape, C.F32))
+            else:
+                el = []
+                for e in range(n):
+                    ex = terms[0][e]
+                    for t in terms[1:]:
+                        ex = f"({ex} + {t[e]})"
+                    el.append(ex)
+                pre_cts.append(Val(el, o.aval.shape, C.F32))
+    gr = run_block(pre_vjp, item_ins + pre_cts, 2)
+    k = 0
+    for q, m in enumerate(r_ctin):
+        if not m:
+            continue
+        v = gr[k]
+        k += 1
+        if nT <= q < nT + nP:
+            i = q - nT
+            n = max(1, pav[i].size)
+            for e, el in enumerate(v.el):
+                out(f"((float*)P.p[{r_gpi[i]}])[tm_item * {n} + {e}] = {el};", 2)
+        elif q >= nT + nP:
+            jb = q - nT - nP
+            S = max(1, bav[jb].size)
+            for e, el in enumerate(v.el):
+                out(f"if (tm_xemit(&tm_xsh{jb}[{e * K.XW}], {el})) atomicOr(&tm_xfl{jb}[{e >> 5}], {1 << (e & 31)}u);",
+                    2)
+    # per-item operands differentiated but not active: zero cotangent
+    for i in adj.wrt_pi:
+        if not r_ctin[nT + i]:
+            n = max(1, pav[i].size)
+            for e in range(n):
+                out(f"((float*)P.p[{r_gpi[i]}])[tm_item * {n} + {e}] = 0.0f;", 2)
+    out("  }")
+    out("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")
+    if adj.wrt_bc:
+        out("  __syncthreads();")
+        for j in adj.wrt_bc:
+            S = max(1, bav[j].size)
+            gw = f"((u64*)P.p[{r_scr[j]}])"
+            gf = f"((u32*)P.p[{r_scr[j]}] + {2 * K.XW * S})"
+            out(f"  for (int i = threadIdx.x; i < {K.XW * S}; i += blockDim.x) {{ const i64 x = (i64)tm_xsh{j}[i]; "
+                f"if (x != 0 && tm_xadd(&{gw}[i / {K.XW} * {K.XW}], i % {K.XW}, x)) "
+                f"atomicOr(&{gf}[(i / {K.XW}) >> 5], 1u << ((i / {K.XW}) & 31)); }}")
+            out(f"  for (int i = threadIdx.x; i < {(S + 31) // 32}; i += blockDim.x) "
+                f"if (tm_xfl{j}[i]) atomicOr(&{gf}[i], tm_xfl{j}[i]);")
+    out("}")
+    src.append("\n".join(lines))
+    L = K.Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_gbc, r_ctl=r_ctl, r_stats=r_stats,
+                 r_ys=[r_gpi[i] for i in adj.wrt_pi] + ([r_tr] if r_tr is not None else []), flags=2,
+                 mode="adjoint" + ("" if active_carries else "-forward"), priv=list(adj.wrt_bc),
+                 zero_words=zero_words)
+    L.i_pi, L.i_cty, L.i_bc, L.i_ctt, L.ft, L.fy = i_pi, i_cty, i_bc, i_ctt, ft, fy
+    L.active_carries = active_carries
+    return "\n".join(src) + "\n", L

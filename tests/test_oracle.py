@@ -158,3 +158,27 @@ def test_c2_oracle_invariants(oracle):
     assert 200 < r.per_item.mean() < 1500 and not r.trunc.any()
     g, ntr = oracle.c2_grad(x0, keys, drift, np.ones(128, np.float32), np.ones(2, np.float32))
     assert g == 0.0 and ntr == 0
+
+
+def test_c1_per_item_tangent_pathwise(oracle):
+    """the oracle's forward-mode d/d x0 of each item against the pathwise derivative evaluated in float64 along the
+    item's own (frozen) integer path: x_k = x0 prod_{j<k} f_j with f_j = 0.5 + 0.5 u_j independent of x0, so
+    d/d x0 sum_k ct[bin_k] theta (1 - x_k) = -theta sum_k ct[bin_k] prod_{j<k} f_j."""
+    from tallymap_amd import configs
+    from tallymap_amd import random as R
+    xs, keys, theta = configs.c1_inputs(200)
+    ct = np.linspace(0.5, 2.0, 16).astype(np.float32)
+    _, dx, _ = oracle.c1_grad(xs, keys, theta, ct, per_item=True)
+    f32 = np.float32
+    for i in range(200):
+        x, k, prod, want = f32(xs[i]), 0, 1.0, 0.0
+        while k < 100 and x > f32(0.05):
+            u = R.uniform(R.fold_in(keys[i], k))
+            b = int(np.trunc(np.float32(x * f32(16.0))))
+            f = f32(f32(0.5) + f32(f32(0.5) * u))
+            if 0 <= b < 16:
+                want += float(ct[b]) * -float(theta) * prod
+            prod *= float(f)
+            x = f32(x * f)
+            k += 1
+        assert abs(float(dx[i]) - want) <= 1e-5 * max(1.0, abs(want)), (i, dx[i], want)
