@@ -42,7 +42,7 @@ int tm_register(long long id, const void* image, size_t n, const char* note);
 int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, int flags, long long n_items,
               int block);
 
-/* out[8]: registers per lane of tm_main, private (scratch) bytes per lane, static LDS bytes per block, achieved
+/* out[8]: registers per lane of the item loop (tm_main, or tm_adjoint in a replay adjoint), private (scratch) bytes per lane, static LDS bytes per block, achieved
  * blocks per CU at `block` threads, resident threads on the device, compute units, max threads per block, and the
  * grid tm_launch uses for 2^31 - 1 items. */
 int tm_kernel_info(long long id, int block, long long out[8]);

@@ -90,7 +90,10 @@ class ItemProgram:
         return [k for k, s in enumerate(self.tallies) if s.kind == "sum"]
 
     def digest(self):
-        return digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag))
+        d = self.__dict__.get("_digest")
+        if d is None:
+            d = self.__dict__["_digest"] = digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag))
+        return d
 
 
 # ----------------------------------------------------------------------------------------- tally checks

@@ -144,16 +144,16 @@ def prebuild(configs, n=64):
         pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
         bav = [C.AVal(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
         prog, _ = build_program(cfg["item"], cfg["outputs"], axes, pav, bav, cfg["max_steps"])
-        progs = [prog]
-        try:
-            from . import reverse as R
-            progs.append(R.adjoint_program(prog, R.default_wrt(prog)))
-        except (ImportError, AttributeError):
-            pass
-        for p in progs:
-            src, _ = K.build(p, block=K.BLOCK, schedule="step", refill=1)
-            Cm.code_object(src, name=f"tm_{p.tag}.hip", store_pkg=True)
-            done.append((name, p.tag, Cm._key(src)[:16]))
+        src, _ = K.build(prog, block=K.BLOCK, schedule="step", refill=1)
+        Cm.code_object(src, name=f"tm_{prog.tag}.hip", store_pkg=True)
+        done.append((name, prog.tag, Cm._key(src)[:16]))
+        from . import reverse as R
+        wp, wb = R.default_wrt(prog)
+        for wrt in ((wp, wb), ((), wb)):
+            adj = R.adjoint_program(prog, wrt)
+            src, _ = R.build(adj, block=K.BLOCK, ckpt=R.C_DEFAULT)
+            Cm.code_object(src, name=f"tm_{adj.tag}.hip", store_pkg=True)
+            done.append((name, adj.tag + str(wrt), Cm._key(src)[:16]))
     return done
 
 
@@ -203,6 +203,8 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
         x = ct_tallies.get(k) if ct_tallies else None
         if x is None:
             ins.append(torch.zeros(s.shape, dtype=torch.float32, device="cuda").reshape(-1))
+        elif isinstance(x, (int, float, np.floating, np.integer)):
+            ins.append(torch.full((s.S,), float(x), dtype=torch.float32, device="cuda"))
         else:
             ins.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
                                      else x, np.float32).reshape(-1))

@@ -128,7 +128,10 @@ def code_object(src, name="tm_program", store_pkg=False):
         p = os.path.join(d, k + ".co")
         if os.path.exists(p):
             with open(p, "rb") as fh:
-                return fh.read()
+                data = fh.read()
+            if store_pkg and d != KCACHE:
+                _store(KCACHE, k, data)
+            return data
     L = lib()
     opts = (ctypes.c_char_p * len(OPTS))(*[o.encode() for o in OPTS])
     img, n, log = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_void_p()
@@ -140,11 +143,14 @@ def code_object(src, name="tm_program", store_pkg=False):
         raise BackendError(L.tm_last_error().decode())
     data = ctypes.string_at(img, n.value)
     L.tm_free(img)
-    dirs = [cache_dir()] + ([KCACHE] if store_pkg else [])
-    for d in dirs:
-        os.makedirs(d, exist_ok=True)
-        tmp = os.path.join(d, f"{k}.co.tmp{os.getpid()}")
-        with open(tmp, "wb") as fh:
-            fh.write(data)
-        os.replace(tmp, os.path.join(d, k + ".co"))
+    for d in [cache_dir()] + ([KCACHE] if store_pkg else []):
+        _store(d, k, data)
     return data
+
+
+def _store(d, k, data):
+    os.makedirs(d, exist_ok=True)
+    tmp = os.path.join(d, f"{k}.co.tmp{os.getpid()}")
+    with open(tmp, "wb") as fh:
+        fh.write(data)
+    os.replace(tmp, os.path.join(d, k + ".co"))

@@ -317,7 +317,7 @@ def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
                + "\n  ".join(post_l) + "\n}")
 
     # ---------------------------------------------------------------------------------- tm_main
-    out(f"extern \"C\" __global__ void __launch_bounds__({block}) tm_main(const TmParams P, const i64 n_items) {{")
+    out(f"extern \"C\" __global__ void __launch_bounds__({block}) tm_adjoint(const TmParams P, const i64 n_items) {{")
     out(f"  u64* const tm_ctr = (u64*)P.p[{r_ctl}];")
     for j in adj.wrt_bc:
         S = max(1, bav[j].size)

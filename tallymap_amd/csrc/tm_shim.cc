@@ -48,6 +48,7 @@ struct Rt {
   TM_SYM(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor)
   TM_SYM(hipFuncGetAttribute)
   TM_SYM(hipGetErrorString)
+  TM_SYM(hipGetLastError)
   TM_SYM(hiprtcCreateProgram)
   TM_SYM(hiprtcCompileProgram)
   TM_SYM(hiprtcGetProgramLogSize)
@@ -102,7 +103,8 @@ int bind_hip(const char* path) {
             sym(h, "hipDeviceGetAttribute", r.hipDeviceGetAttribute) &&
             sym(h, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor",
                 r.hipModuleOccupancyMaxActiveBlocksPerMultiprocessor) &&
-            sym(h, "hipFuncGetAttribute", r.hipFuncGetAttribute) && sym(h, "hipGetErrorString", r.hipGetErrorString);
+            sym(h, "hipFuncGetAttribute", r.hipFuncGetAttribute) && sym(h, "hipGetErrorString", r.hipGetErrorString) &&
+            sym(h, "hipGetLastError", r.hipGetLastError);
   if (!ok) return fail("tallymap_rocm: %s lacks a HIP module API symbol", path ? path : "libamdhip64.so.7");
   r.hip = h;
   g_hip_ok = true;
@@ -141,10 +143,19 @@ int loaded(long long id, std::shared_ptr<Loaded>* out) {
   auto L = std::make_shared<Loaded>();
   e = g_rt.hipModuleLoadData(&L->mod, pr->second->image.data());
   if (e != hipSuccess) return fail("tallymap_rocm: loading %s on device %d: %s", pr->second->note.c_str(), dev, herr(e));
-  if ((e = g_rt.hipModuleGetFunction(&L->main, L->mod, "tm_main")) != hipSuccess)
-    return fail("tallymap_rocm: %s has no tm_main: %s", pr->second->note.c_str(), herr(e));
-  if (g_rt.hipModuleGetFunction(&L->zero, L->mod, "tm_zero") != hipSuccess) L->zero = nullptr;
-  if (g_rt.hipModuleGetFunction(&L->post, L->mod, "tm_post") != hipSuccess) L->post = nullptr;
+  // the item loop: tm_main (a forward program) or tm_adjoint (a replay adjoint); tm_zero / tm_post are optional.
+  // A lookup that fails leaves the runtime's per-thread last error set, which the caller's framework would later
+  // report from an unrelated call: every probe that may fail is followed by hipGetLastError to clear it.
+  auto probe = [&](hipFunction_t* f, const char* name) {
+    if (g_rt.hipModuleGetFunction(f, L->mod, name) == hipSuccess) return true;
+    *f = nullptr;
+    (void)g_rt.hipGetLastError();
+    return false;
+  };
+  if (!probe(&L->main, "tm_main") && !probe(&L->main, "tm_adjoint"))
+    return fail("tallymap_rocm: %s has neither tm_main nor tm_adjoint", pr->second->note.c_str());
+  probe(&L->zero, "tm_zero");
+  probe(&L->post, "tm_post");
   if ((e = g_rt.hipDeviceGetAttribute(&L->cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess)
     return fail("tallymap_rocm: device attribute: %s", herr(e));
   modules()[{id, dev}] = L;
