@@ -52,6 +52,39 @@ def activity(jx, active_in):
     return act
 
 
+def relevance(jx, out_rel, emits=True):
+    """indices of jx's invars whose value can reach, through differentiable operations, an output flagged in out_rel
+    or (emits) the value of an emit: the inputs whose cotangent can be nonzero."""
+    rel = {v.id for v, r in zip(jx.outvars, out_rel) if r and isinstance(v, C.Var)}
+    for e in reversed(jx.eqns):
+        if e.prim == "tallymap_emit":
+            if emits and isinstance(e.invars[2], C.Var) and _isf(e.invars[2].aval):
+                rel.add(e.invars[2].id)
+            continue
+        if e.prim in ZERO_D:
+            continue
+        if any(o.id in rel for o in e.outvars):
+            for v in e.invars:
+                if isinstance(v, C.Var) and _isf(v.aval):
+                    rel.add(v.id)
+    return [isinstance(v, C.Var) and v.id in rel for v in jx.invars]
+
+
+def eval_jaxpr(jx, args, ct_read=None):
+    """re-bind jx's equations on `args` (Tracers / numpy scalars) in the current trace -> its outputs.
+    ct_read(slot, idx) replaces the `tm_ct_read` primitive of a VJP program."""
+    env = {v.id: a for v, a in zip(jx.invars, args)}
+    for e in jx.eqns:
+        ins = [_t(v, env) for v in e.invars]
+        if e.prim == "tm_ct_read" and ct_read is not None:
+            outs = [ct_read(e.params["slot"], ins[0])]
+        else:
+            outs = _replay(e, ins)
+        for o, x in zip(e.outvars, outs):
+            env[o.id] = x
+    return [_t(v, env) for v in jx.outvars]
+
+
 def _t(v, env):
     if isinstance(v, C.Lit):
         return v.val.reshape(()).astype(v.aval.dtype)[()] if v.aval.shape == () else v.val
@@ -78,15 +111,18 @@ def _zeros_like(aval):
     return _f(0, aval.dtype)
 
 
-def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True):
+def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=None):
     """-> (Jaxpr, ct_out_mask, ct_in_mask).
     The Jaxpr's invars: jx.invars + [cotangent of each output in ct_out_mask]; outvars: [cotangent of each input
     in ct_in_mask].  ct_out_mask: jx's active float outputs; ct_in_mask: jx's active inputs.
     ct_read(slot, idx) -> the cotangent tally value (a Tracer) for an emit into tally `slot` at index idx; slots:
-    {invar index of a tally input: its slot}."""
+    {invar index of a tally input: its slot}.  ct_given: outputs whose cotangent may be nonzero (default: all); the
+    others get no cotangent input."""
     tslot = {jx.invars[i].id: s for i, s in (slots or {}).items()}
     act = activity(jx, active_in)
     ct_out_mask = [isinstance(v, C.Var) and v.id in act for v in jx.outvars]
+    if ct_given is not None:
+        ct_out_mask = [m and g for m, g in zip(ct_out_mask, ct_given)]
     ct_in_mask = [v.id in act for v in jx.invars]
     b = C.Builder()
     C._STACK.append(b)
@@ -97,10 +133,11 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True):
         recs = []
         for e in jx.eqns:
             ins = [_t(v, env) for v in e.invars]
-            if e.prim in ("tallymap_emit", "copy") and isinstance(e.invars[0], C.Var) and e.invars[0].id in tslot:
+            is_t = isinstance(e.invars[0], C.Var) and e.invars[0].id in tslot
+            if e.prim in ("tallymap_emit", "copy") and is_t:
                 tslot[e.outvars[0].id] = tslot[e.invars[0].id]
-            if e.prim == "tallymap_emit":
-                outs = [ins[0]]
+            if e.prim == "tallymap_emit" or (e.prim == "copy" and is_t):
+                outs = [ins[0]]           # a VJP program never threads the tallies (only reads their cotangents)
             else:
                 outs = _replay(e, ins)
             for o, x in zip(e.outvars, outs):

@@ -151,7 +151,11 @@ def prebuild(configs, n=64):
         wp, wb = R.default_wrt(prog)
         for wrt in ((wp, wb), ((), wb)):
             adj = R.adjoint_program(prog, wrt)
-            src, _ = R.build(adj, block=K.BLOCK, ckpt=R.C_DEFAULT)
+            pl = R.plan(adj)
+            if any(pl.car_act):
+                src, _ = R.build(adj, block=K.BLOCK, ckpt=R.C_DEFAULT)
+            else:
+                src, _ = K.build(R.forward_only_program(adj, pl), block=K.BLOCK, schedule="step", refill=1)
             Cm.code_object(src, name=f"tm_{adj.tag}.hip", store_pkg=True)
             done.append((name, adj.tag + str(wrt), Cm._key(src)[:16]))
     return done
@@ -183,34 +187,53 @@ def compiled_adjoint(adj, opts):
 def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
     """the replay adjoint of prog: cotangents of the per-item operands wrt[0] ([N, ...] each) and the broadcast
     operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
-    0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated)."""
+    0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated).
+    When no loop carry needs a reverse sweep the adjoint is an ordinary item program (reverse.forward_only_program)
+    run by the forward template (step refill); otherwise the checkpointed replay template (reverse.build)."""
     import torch
 
     from . import reverse as R
     adj = R.adjoint_program(prog, wrt)
-    c = compiled_adjoint(adj, opts)
-    L = c.layout
-    ins = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
+    pl = R.plan(adj)
     yav = prog.y_avals()
-    for j in L.fy:
+    ins_p = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
+    for j in pl.fy:
         x = ct_ys.get(j) if ct_ys else None
         a = yav[j]
-        ins.append(device_tensor(x, a.dtype) if x is not None
-                   else torch.zeros((N,) + tuple(a.shape), dtype=torch.float32, device="cuda"))
-    ins += [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
-    for k in L.ft:
+        ins_p.append(device_tensor(x, a.dtype) if x is not None
+                     else torch.zeros((N,) + tuple(a.shape), dtype=torch.float32, device="cuda"))
+    ins_b = [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+    for k in pl.ft:
         s = prog.tallies[k]
         x = ct_tallies.get(k) if ct_tallies else None
         if x is None:
-            ins.append(torch.zeros(s.shape, dtype=torch.float32, device="cuda").reshape(-1))
+            ins_b.append(torch.zeros((s.S,), dtype=torch.float32, device="cuda"))
         elif isinstance(x, (int, float, np.floating, np.integer)):
-            ins.append(torch.full((s.S,), float(x), dtype=torch.float32, device="cuda"))
+            ins_b.append(torch.full((s.S,), float(x), dtype=torch.float32, device="cuda"))
         else:
-            ins.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
-                                     else x, np.float32).reshape(-1))
-    res = launch(c, ins, N)
-    base = L.n_in
-    g_bc = [res[L.r_out[j] - base] for j in adj.wrt_bc]
-    g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
+            ins_b.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
+                                       else x, np.float32).reshape(-1))
+    if not any(pl.car_act):
+        q = _FWD_ONLY.get(adj.digest())
+        if q is None:
+            q = _FWD_ONLY[adj.digest()] = R.forward_only_program(adj, pl)
+        c = compiled(q, opts)
+        res = launch(c, ins_p + ins_b, N)
+        L = c.layout
+        base = L.n_in
+        g_bc = [res[L.r_out[k] - base].reshape(prog.b_avals()[j].shape)
+                for k, j in zip(q.out_tallies, adj.wrt_bc)]
+        ys = [res[r - base] for r in L.r_ys]
+        g_pi = ys[:len(adj.wrt_pi)]
+    else:
+        c = compiled_adjoint(adj, opts)
+        res = launch(c, ins_p + ins_b, N)
+        L = c.layout
+        base = L.n_in
+        g_bc = [res[L.r_out[j] - base] for j in adj.wrt_bc]
+        g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
     ntr = res[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
     return g_pi, g_bc, ntr
+
+
+_FWD_ONLY = {}

@@ -62,13 +62,15 @@ def lit(v, dt):
 
 
 class Val:
-    """an IR value in the emitter: C expressions per element."""
-    __slots__ = ("el", "shape", "dtype")
+    """an IR value in the emitter: C expressions per element (ptr: the device pointer of a broadcast array read in
+    place, for dynamic indexing)."""
+    __slots__ = ("el", "shape", "dtype", "ptr")
 
-    def __init__(self, el, shape, dtype):
+    def __init__(self, el, shape, dtype, ptr=None):
         self.el = list(el)
         self.shape = tuple(shape)
         self.dtype = np.dtype(dtype)
+        self.ptr = ptr
 
 
 class VTally:
@@ -450,6 +452,17 @@ def _copy(em, e, ins):
     if isinstance(x, VTally):
         return x
     return Val(x.el, out.shape, out.dtype)
+
+
+@rule("tallymap_ct_read")
+def _ct_read(em, e, ins):
+    """a cotangent tally read at a dynamic index: 0 outside [0, S) (a dropped emit has no cotangent)."""
+    arr, idx = ins
+    if arr.ptr is None:
+        raise CodegenError("tallymap_ct_read of an array without a device pointer")
+    S = max(1, int(np.prod(arr.shape)))
+    i = idx.el[0]
+    return Val([em.bind(f"((u32)({i}) < {S}u ? {arr.ptr}[{i}] : 0.0f)", C.F32, "ct")], (), C.F32)
 
 
 @rule("threefry2x32")

@@ -30,6 +30,8 @@ from .codegen import Emitter, Val, VTally, assign_carries, ctype, lit
 BLOCK = 256
 LDS_BYTES = 32768          # privatised tallies per block (MI355X: 160 KB LDS per CU)
 XW = 5                     # int64 words per exact bin
+CHUNK = 64                 # items per wave claim
+BCAST_REG = 16             # broadcast operands up to this many elements are loaded into registers
 
 
 @dataclasses.dataclass
@@ -84,9 +86,10 @@ def exact_words(S):
     return 2 * XW * S + (S + 31) // 32
 
 
-def build(prog, block=BLOCK, schedule="step", refill=1, adjoint=None):
-    """-> (HIP source, Layout) of prog's module.  `adjoint`: a backend.reverse.Adjoint (the replay kernel) or
-    None."""
+def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK):
+    """-> (HIP source, Layout) of prog's module.  chunk: items a wave claims with one atomic (their per-item operands
+    are staged in LDS by one coalesced load, and idle lanes take them from there at step granularity)."""
+    chunk = max(1, int(chunk))
     jx = prog.jaxpr
     nT, nP, nB = prog.nT, prog.nP, prog.nB
     pav, bav = prog.p_avals(), prog.b_avals()
@@ -158,11 +161,26 @@ def build(prog, block=BLOCK, schedule="step", refill=1, adjoint=None):
     bvals = []
     for i, a in enumerate(bav):
         ct = ctype(a.dtype)
-        bvals.append(Val([f"tm_b{i}_{e}" for e in range(max(1, a.size))], a.shape, a.dtype))
+        if a.size > BCAST_REG:      # a larger broadcast array is read in place (and can be indexed dynamically)
+            ptr = f"((const {ct}*)P.p[{nP + i}])"
+            bvals.append(Val([f"{ptr}[{e}]" for e in range(a.size)], a.shape, a.dtype, ptr=ptr))
+        else:
+            bvals.append(Val([f"tm_b{i}_{e}" for e in range(max(1, a.size))], a.shape, a.dtype,
+                             ptr=f"((const {ct}*)P.p[{nP + i}])"))
+
+    # per-item operands of 4-byte elements are staged in LDS per wave chunk: word offsets within an item's record
+    stage_off, W = {}, 0
+    for i, a in enumerate(pav):
+        if a.dtype.itemsize == 4:
+            stage_off[i] = W
+            W += max(1, a.size)
 
     def load_pi(i, a):
         ct = ctype(a.dtype)
         n = max(1, a.size)
+        if i in stage_off:
+            return Val([f"__builtin_bit_cast({ct}, tm_st[tm_loc * {W} + {stage_off[i] + e}])" for e in range(n)],
+                       a.shape, a.dtype)
         return Val([f"(({'const ' + ct}*)P.p[{i}])[tm_item * {n} + {e}]" for e in range(n)], a.shape, a.dtype)
 
     decls, pre_lines, step_lines, post_lines = [], [], [], []
@@ -319,6 +337,13 @@ def build(prog, block=BLOCK, schedule="step", refill=1, adjoint=None):
             ct = ctype(s.dtype)
             post.append(f"if (TM_CTL[2] != 0u) for (i64 i = g; i < {s.S}; i += st) "
                         f"(({ct}*)P.p[{r_out[k]}])[i] = __builtin_nanf(\"\");")
+    if getattr(prog, "poison_ys", False) and prog.trunc is not None:
+        # a derived program (the adjoint): every float per-item result is NaN when an item was truncated
+        for j, a in enumerate(yav):
+            if a.dtype in (C.F32, C.F64):
+                n = max(1, a.size)
+                post.append(f"if (TM_CTL[2] != 0u) for (i64 i = g; i < n_items * {n}; i += st) "
+                            f"(({ctype(a.dtype)}*)P.p[{r_ys[j]}])[i] = __builtin_nanf(\"\");")
     if post:
         flags |= 2
         src.append("extern \"C\" __global__ void tm_post(const TmParams P, const i64 n_items) {\n"
@@ -346,10 +371,18 @@ def build(prog, block=BLOCK, schedule="step", refill=1, adjoint=None):
         body.append("  __syncthreads();")
     for i, a in enumerate(bav):
         ct = ctype(a.dtype)
+        if a.size > BCAST_REG:
+            continue
         for e in range(max(1, a.size)):
             body.append(f"  const {ct} tm_b{i}_{e} = ((const {ct}*)P.p[{nP + i}])[{e}];")
+    wpb = block // 64
+    if W:
+        body.append(f"  __shared__ u32 tm_stage[{wpb * chunk * W}];")
+        body.append(f"  u32* const tm_st = tm_stage + (threadIdx.x >> 6) * {chunk * W};")
     body.append("  bool tm_live = false, tm_more = true;")
     body.append("  i64 tm_item = 0;")
+    body.append("  u32 tm_loc = 0;")
+    body.append("  u64 tm_cb = 0, tm_cur = 0, tm_end = 0;     // the wave's chunk: base, next unassigned, end")
     body.append("  i32 tm_drop = 0;")
     body.append("  u32 tm_ntr = 0;")
     body += decls
@@ -361,18 +394,42 @@ def build(prog, block=BLOCK, schedule="step", refill=1, adjoint=None):
                     "tm_ballot(tm_live) == 0ull)) {")
     else:
         body.append("      if (tm_need != 0ull) {")
-    body.append("        const u32 tm_n = (u32)__builtin_popcountll(tm_need);")
-    body.append("        const u64 tm_base = tm_claim(tm_ctr, tm_n);")
-    body.append("        if (tm_base + tm_n >= (u64)n_items) tm_more = false;")
-    body.append("        if (!tm_live) {")
-    body.append("          const u64 tm_t = tm_base + tm_rank(tm_need);")
-    body.append("          if (tm_t < (u64)n_items) {")
-    body.append("            tm_item = (i64)tm_t;")
-    body.append("            tm_live = true;")
+    body.append("        if (tm_cur >= tm_end) {")
+    body.append(f"          const u64 tm_b = tm_claim(tm_ctr, {chunk}u);")
+    body.append("          if (tm_b >= (u64)n_items) {")
+    body.append("            tm_more = false;")
+    body.append("          } else {")
+    body.append(f"            tm_cb = tm_b; tm_cur = tm_b; tm_end = tm_b + {chunk}u < (u64)n_items ? tm_b + {chunk}u "
+                ": (u64)n_items;")
+    if W:
+        body.append(f"            for (u32 q = (u32)tm_lane(); q < {chunk}u; q += 64u) {{")
+        body.append("              const u64 t = tm_cb + q;")
+        body.append("              if (t < tm_end) {")
+        for i, off in stage_off.items():
+            n = max(1, pav[i].size)
+            for e in range(n):
+                body.append(f"                tm_st[q * {W} + {off + e}] = ((const u32*)P.p[{i}])[t * {n} + {e}];")
+        body.append("              }")
+        body.append("            }")
+        body.append("            __builtin_amdgcn_wave_barrier();")
+    body.append("          }")
+    body.append("        }")
+    body.append("        if (tm_cur < tm_end) {")
+    body.append("          const u64 tm_av = tm_end - tm_cur;")
+    body.append("          const u64 tm_n = (u64)__builtin_popcountll(tm_need);")
+    body.append("          if (!tm_live) {")
+    body.append("            const u64 tm_r = tm_rank(tm_need);")
+    body.append("            if (tm_r < tm_av) {")
+    body.append("              tm_item = (i64)(tm_cur + tm_r);")
+    body.append("              tm_loc = (u32)(tm_cur + tm_r - tm_cb);")
+    body.append("              tm_live = true;")
     body += pre_lines
     if mode == "item":
-        body.append("            tm_live = false;")
+        body.append("              tm_live = false;")
+    body.append("            }")
     body.append("          }")
+    body.append("          tm_cur += tm_n < tm_av ? tm_n : tm_av;")
+    body.append("          if (tm_cur >= tm_end && tm_end >= (u64)n_items) tm_more = false;")
     body.append("        }")
     body.append("      }")
     body.append("    }")

@@ -30,6 +30,7 @@ import numpy as np
 
 from .. import _ad as AD
 from .. import _core as C
+from .. import lax as L
 from .._api import ItemProgram, TSpec
 from . import kernel as K
 from .codegen import Emitter, Val, VTally, assign_carries, ctype
@@ -164,6 +165,190 @@ def _ren_eqn(e, m):
     return C.Eqn(e.prim, [_ren(v, m) for v in e.invars], e.outvars, e.params)
 
 
+# ------------------------------------------------------------------------------------------ the plan
+@dataclasses.dataclass
+class Plan:
+    sp: Split
+    pre_act_in: list        # PRE's active inputs (the perturbed operands)
+    P_act: list             # per P var: active
+    car_act: list           # per carry: active AND its cotangent can be nonzero (needs the reverse sweep)
+    bconst_act: list        # per body constant: active and relevant (its cotangent accumulates per step)
+    ft: list                # tally slots with a cotangent input (float32 sums)
+    fy: list                # per-item results with a cotangent input (float32)
+
+
+def plan(adj):
+    prog = adj.prog
+    nT, nP, nB = prog.nT, prog.nP, prog.nB
+    sp = split(prog)
+    yav = prog.y_avals()
+    ft = [k for k in prog.out_tallies if prog.tallies[k].dtype == C.F32]
+    fy = [j for j, a in enumerate(yav) if a.dtype == C.F32]
+    pre_act_in = [False] * nT + [i in adj.wrt_pi for i in range(nP)] + [j in adj.wrt_bc for j in range(nB)]
+    act_pre = AD.activity(sp.pre, pre_act_in)
+    P_act = [isinstance(v, C.Var) and v.id in act_pre for v in sp.pre.outvars[sp.ncar:]]
+    fwd = [isinstance(v, C.Var) and v.id in act_pre and s is None
+           for v, s in zip(sp.pre.outvars[:sp.ncar], sp.car_slot)]
+    bconst_fwd = [r[0] == "P" and P_act[r[1]] for r in sp.bconst]
+    while True:                                   # forward activity of the carries (fixpoint over the body)
+        a = AD.activity(sp.body, bconst_fwd + fwd)
+        new = [f or (isinstance(o, C.Var) and o.id in a and s is None)
+               for f, o, s in zip(fwd, sp.body.outvars, sp.car_slot)]
+        if new == fwd:
+            break
+        fwd = new
+    # backward relevance: a carry whose final value reaches a float per-item result or an emitted value of POST,
+    # or (through steps) of BODY
+    out_rel = [False] * nT + [a.dtype == C.F32 for a in yav]
+    rel_post = AD.relevance(sp.post, out_rel)
+    rel = [r and s is None for r, s in zip(rel_post[sp.nP:], sp.car_slot)]
+    while True:
+        rb = AD.relevance(sp.body, rel)
+        new = [r or (x and s is None) for r, x, s in zip(rel, rb[len(sp.bconst):], sp.car_slot)]
+        if new == rel:
+            break
+        rel = new
+    rb = AD.relevance(sp.body, rel)
+    car_act = [f and r for f, r in zip(fwd, rel)]
+    bconst_act = [f and r for f, r in zip(bconst_fwd, rb[:len(sp.bconst)])]
+    return Plan(sp, pre_act_in, P_act, car_act, bconst_act, ft, fy)
+
+
+def _ct_reader(ft, S_of, arrays=None):
+    """ct_read(slot, idx) for vjp_jaxpr (arrays None: the `tm_ct_read` placeholder primitive) or eval_jaxpr
+    (arrays: the cotangent tally operands, read with `tallymap_ct_read`)."""
+    def ct_read(slot, idx):
+        if slot not in ft:
+            return np.float32(0.0)
+        iv = idx.var if C.is_traced(idx) else C.literal(int(idx), C.I32, False)
+        if arrays is None:
+            return C.bind("tm_ct_read", [iv], [C.AVal((), C.F32)], slot=slot)[0]
+        return C.bind("tallymap_ct_read", [arrays[ft.index(slot)].var, iv], [C.AVal((), C.F32)])[0]
+    return ct_read
+
+
+def forward_only_program(adj, pl):
+    """the adjoint as an ordinary item program, when no loop carry needs a reverse sweep: PRE, the loop with the
+    step VJPs of the body constants accumulated as extra carries, POST, POST's and PRE's VJPs, one exact emit per
+    differentiated broadcast element.  It runs through the forward kernel template (step refill).
+    invars: tallies [forward tallies, discarded][ct of each differentiated broadcast operand, exact] + per-item
+    [operands][result cotangents] + broadcast [operands][tally cotangents]; per-item results [operand
+    cotangents][truncated]."""
+    prog, sp = adj.prog, pl.sp
+    nT, nP, nB = prog.nT, prog.nP, prog.nB
+    pav, bav, yav = prog.p_avals(), prog.b_avals(), prog.y_avals()
+    ft, fy = pl.ft, pl.fy
+    nbc = len(sp.bconst)
+    S_of = {k: prog.tallies[k].S for k in ft}
+    body_vjp, b_ctout, b_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + [False] * sp.ncar, _ct_reader(ft, S_of),
+                                             {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
+                                             ct_given=[False] * sp.ncar)
+    post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, pl.P_act + [False] * sp.ncar, _ct_reader(ft, S_of),
+                                             {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None})
+    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)})
+    tspecs = [dataclasses.replace(s, kind="discard") for s in prog.tallies]
+    tspecs += [TSpec(f"ct{j}", tuple(bav[j].shape) or (1,), np.dtype(np.float32), exact=True) for j in adj.wrt_bc]
+    b = C.Builder()
+    C._STACK.append(b)
+    try:
+        tin = [C.Tracer(b.new_invar(C.AVal((s.S,), s.dtype))) for s in tspecs]
+        pin = [C.Tracer(b.new_invar(a)) for a in pav]
+        cyin = [C.Tracer(b.new_invar(C.AVal(yav[j].shape, C.F32))) for j in fy]
+        bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
+        ctin = [C.Tracer(b.new_invar(C.AVal((prog.tallies[k].S,), C.F32))) for k in ft]
+        ct_read = _ct_reader(ft, S_of, ctin)
+        pre_outs = AD.eval_jaxpr(sp.pre, tin[:nT] + pin + bin_)
+        cars0, Pv = list(pre_outs[:sp.ncar]), list(pre_outs[sp.ncar:])
+
+        def cval(ref):
+            kind, x = ref
+            return Pv[x] if kind == "P" else AD._t(x, {})
+        ccv = [cval(r) for r in sp.cconst]
+        bcv = [cval(r) for r in sp.bconst]
+        gq = [q for q in range(nbc) if b_ctin[q]]
+        g0 = [np.zeros(sp.body.invars[q].aval.shape, np.float32)[()] for q in gq]
+
+        def cond_f(c):
+            return AD.eval_jaxpr(sp.cond, ccv + list(c[0]))[0]
+
+        def body_f(c):
+            cars, g = list(c[0]), list(c[1])
+            vj = AD.eval_jaxpr(body_vjp, bcv + cars, ct_read)
+            g = [gi + vj[k] for k, gi in enumerate(g)]
+            return (AD.eval_jaxpr(sp.body, bcv + cars), g)
+        cars_f, g = L.while_loop(cond_f, body_f, (cars0, g0)) if sp.ncar else (cars0, g0)
+        cars_f = list(cars_f)
+        post_outs = AD.eval_jaxpr(sp.post, Pv + cars_f)
+        post_cts = []
+        for j, m in enumerate(p_ctout):
+            if m:
+                q = j - nT
+                post_cts.append(cyin[fy.index(q)] if q >= 0 and q in fy else np.float32(0.0))
+        pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read)
+        gP = {}
+        k = 0
+        for q, m in enumerate(p_ctin):
+            if m:
+                if q < sp.nP:
+                    gP[q] = pv[k]
+                k += 1
+        for kk, q in enumerate(gq):                 # body constants' step sums onto their P var
+            r = sp.bconst[q]
+            if r[0] == "P":
+                gP[r[1]] = g[kk] if r[1] not in gP else gP[r[1]] + g[kk]
+        pre_cts = []
+        for j, (o, m) in enumerate(zip(sp.pre.outvars, r_ctout)):
+            if m:
+                z = np.zeros(o.aval.shape, np.float32)[()]
+                pre_cts.append(gP.get(j - sp.ncar, z) if j >= sp.ncar else z)
+        gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read)
+        g_pi, g_bc = {}, {}
+        k = 0
+        for q, m in enumerate(r_ctin):
+            if m:
+                if nT <= q < nT + nP:
+                    g_pi[q - nT] = gr[k]
+                elif q >= nT + nP:
+                    g_bc[q - nT - nP] = gr[k]
+                k += 1
+        touts = [C.Tracer(b.local(t.var)) if C.is_traced(t) else t for t in post_outs[:nT]]
+        ct_t = []
+        for jj, j in enumerate(adj.wrt_bc):
+            t = tin[nT + jj]
+            v = g_bc.get(j)
+            n = max(1, bav[j].size)
+            for e in range(n):
+                if v is None:
+                    continue
+                ve = v if (not C.is_traced(v) or v.shape == ()) else v[e]
+                if C.is_traced(ve):
+                    vv = ve.var
+                else:
+                    vv = C.literal(np.float32(ve), C.F32, False)
+                t = C.bind("tallymap_emit", [t.var, C.literal(e, C.I32, False), vv], [t.aval])[0]
+            ct_t.append(t)
+        ys = []
+        for i in adj.wrt_pi:
+            v = g_pi.get(i)
+            if v is None or not C.is_traced(v):
+                v = C.Tracer(C.bind("copy", [C.literal(np.zeros(pav[i].shape, np.float32), C.F32)],
+                                    [C.AVal(pav[i].shape, C.F32)])[0].var)
+            ys.append(v)
+        trunc = None
+        if prog.trunc is not None:
+            ys.append(post_outs[nT + prog.trunc])
+            trunc = len(ys) - 1
+        outs = [b.local(t.var) for t in touts + ct_t] + [b.local(y.var) for y in ys]
+    finally:
+        C._STACK.pop()
+    jx = C.Jaxpr(b.invars, outs, b.eqns)
+    from .._api import check_tallies
+    check_tallies(jx, len(tspecs), adj.where)
+    q = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft), trunc, adj.tag, adj.where)
+    q.poison_ys = True
+    return q
+
+
 # ------------------------------------------------------------------------------------------ the kernel
 def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
     """-> (HIP source, Layout) of the adjoint module."""
@@ -171,9 +356,8 @@ def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
     jx = prog.jaxpr
     nT, nP, nB = prog.nT, prog.nP, prog.nB
     pav, bav, yav = prog.p_avals(), prog.b_avals(), prog.y_avals()
-    sp = split(prog)
-    ft = [k for k in prog.out_tallies if prog.tallies[k].dtype in (C.F32,)]        # tallies with a cotangent input
-    fy = [j for j, a in enumerate(yav) if a.dtype == C.F32]                           # per-item results with one
+    pl = plan(adj)
+    sp, ft, fy = pl.sp, pl.ft, pl.fy
     # ---- buffers: inputs [pi][ct_y (float ys)][bc][ct tallies]; results [ct_bc][scratch][ctl][stats] | [ct_pi][trunc]
     i_pi = list(range(nP))
     i_cty = list(range(nP, nP + len(fy)))
@@ -193,21 +377,7 @@ def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
     r_gpi = {i: result(pav[i].shape, np.float32, per_item=True) for i in adj.wrt_pi}
     r_tr = result((), np.bool_, per_item=True) if prog.trunc is not None else None
     R = n_in + len(res)
-
-    # ---- activity: operands perturbed -> P active -> carries active (fixpoint over the body)
-    pre_act_in = [False] * nT + [i in adj.wrt_pi for i in range(nP)] + [j in adj.wrt_bc for j in range(nB)]
-    act_pre = AD.activity(sp.pre, pre_act_in)
-    P_act = [v.id in act_pre for v in sp.pre.outvars[sp.ncar:]]
-    car_act = [isinstance(v, C.Var) and v.id in act_pre for v in sp.pre.outvars[:sp.ncar]]
-    car_act = [a and s is None for a, s in zip(car_act, sp.car_slot)]
-    bconst_act = [r[0] == "P" and P_act[r[1]] for r in sp.bconst]
-    while True:
-        a = AD.activity(sp.body, bconst_act + car_act)
-        new = [ca or (isinstance(o, C.Var) and o.id in a and s is None)
-               for ca, o, s in zip(car_act, sp.body.outvars, sp.car_slot)]
-        if new == car_act:
-            break
-        car_act = new
+    pre_act_in, P_act, car_act, bconst_act = pl.pre_act_in, pl.P_act, pl.car_act, pl.bconst_act
     active_carries = any(car_act)
 
     def ct_read_factory():
@@ -218,7 +388,8 @@ def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
                           [C.AVal((), C.F32)], slot=slot)[0]
         return ct_read
     body_slots = {len(sp.bconst) + j: s for j, s in enumerate(sp.car_slot) if s is not None}
-    body_vjp, b_ctout, b_ctin = AD.vjp_jaxpr(sp.body, bconst_act + car_act, ct_read_factory(), body_slots)
+    body_vjp, b_ctout, b_ctin = AD.vjp_jaxpr(sp.body, bconst_act + car_act, ct_read_factory(), body_slots,
+                                             ct_given=car_act)
     post_slots = {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None}
     post_act = P_act + [a for a in car_act]
     post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, post_act, ct_read_factory(), post_slots)

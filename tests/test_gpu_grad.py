@@ -90,3 +90,17 @@ def test_c2_grad_full_size():
     g = tm.grad(_mapped(configs.C2), argnums=2)(x0, keys, drift)
     _sync()
     assert float(_np(g)) == 0.0
+
+
+def test_no_stale_runtime_error_after_launches():
+    """a forward launch and both adjoint kinds leave no pending runtime error for the framework's next call (the
+    launch library clears the errors of its optional symbol lookups)."""
+    import torch
+    xs, keys, theta = configs.c1_inputs(512)
+    f = _mapped(configs.C1)
+    f(xs, keys, theta)
+    tm.grad(f, argnums=2)(xs, keys, theta)                         # forward-only adjoint
+    tm.vjp(f, xs, keys, theta, argnums=(0, 2))[1]({"hist": 1.0})   # checkpointed adjoint
+    x = torch.full((8,), 2.0, device="cuda") * 3.0
+    torch.cuda.synchronize()
+    assert float(x.sum().item()) == 48.0
