@@ -59,8 +59,8 @@ def main():
                     help="HBM bytes per dominant-kernel launch measured with rocprofv3 (profiles/)")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}); the multi-GPU design is in "
-              "DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}): items shard contiguously over "
+              "GPUs with one all-reduce of the tallies, which is designed but not built", file=sys.stderr)
         sys.exit(2)
     import torch
 
