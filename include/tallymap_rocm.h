@@ -7,7 +7,8 @@
  *   tm_register      <- tallymap_register      (shim.cc:134-142)
  *   tm_kernel_info   <- tallymap_kernel_info   (shim.cc:147-155)
  *   tm_launch        <- SjLaunchImpl, the body of the XLA FFI handler TallymapLaunch (shim.cc:157-250), as a
- *                       plain C call: an XLA FFI binding for platform "ROCM" forwards to it
+ *                       plain C call: an XLA FFI handler bound for platform "ROCM" forwards its buffers, stream and
+ *                       attrs (kernel_id, block, n_zero, flags, n_items) to it
  *   tm_compile       <- compile.compile_cubin's NVRTC sequence (compile.py:160-173), with hipRTC for gfx950
  *   tm_init          <- compile.py's Drv / dlopen of the driver (shim.cc:44-82): binds the HIP runtime the process
  *                       already uses (no second runtime, no device code in this library)
