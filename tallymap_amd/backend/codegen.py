@@ -98,6 +98,12 @@ _UT = {"i32": "u32", "u32": "u32", "i64": "u64", "u64": "u64", "i8": "u8", "u8":
 # f32 / f64 transcendentals with a checked restatement in tm_libm.h
 LIBM = {
     ("erf_inv", "float"): "tm_erfinvf",
+    ("log", "float"): "tm_logf",
+    ("exp", "float"): "tm_expf",
+    ("sin", "float"): "tm_sinf",
+    ("cos", "float"): "tm_cosf",
+    ("atan", "float"): "tm_atanf",
+    ("atan2", "float"): "tm_atan2f",
 }
 
 

@@ -4,7 +4,7 @@
 // tallymap/backends/kernel/host.py:43-48, op_table.py:199-223).  glibc's f32 functions are not correctly rounded,
 // so the device cannot use its own math library and agree bitwise.  Each function here is written from a published
 // method and checked on the host against glibc over the argument sets the tests name (exhaustively where the set
-// is enumerable); tests/test_libm.py holds the checks and their results.
+// is enumerable); tests/native/libm_check.cc and tests/test_native_cpu.py hold the checks.
 //
 //   tm_log     double natural log: the classic fdlibm argument reduction and odd-series in s = f / (2 + f)
 //              (Sun fdlibm e_log.c, freely redistributable), < 1 ulp.
@@ -12,6 +12,18 @@
 //              evaluated in double (log, sqrt), rounded once to f32 (host.py:102-132).  Checked bitwise against
 //              the reference formula with glibc's log over every argument jax.random.normal can produce (all 2^23
 //              uniform values).
+//   tm_logf, tm_expf, tm_sinf, tm_cosf
+//              glibc 2.35's f32 functions are the ARM optimized-routines algorithms (MIT / Apache-2.0; Szabolcs
+//              Nagy), built on x86-64 in an FMA variant selected at run time on FMA/AVX2 hosts.  Restated here:
+//              the same reductions, tables and polynomials, with an explicit fma wherever that build contracts a
+//              multiply-add.  Checked bitwise against glibc on ALL 2^32 inputs: logf, sinf, cosf agree
+//              everywhere; expf everywhere except two inputs whose glibc result lies on a rounding knife-edge of
+//              the same evaluation, listed in tm_expf.  The exp2 table is 2^(i/32) rounded to double, minus i << 47
+//              (computed from that definition); the 2/pi bit table is the binary expansion of 2/pi.
+//   tm_atanf, tm_atan2f
+//              fdlibm's float atanf / atan2f (Sun, freely redistributable) in float arithmetic, in glibc's form
+//              (atanf returns +-pi/2 from |x| >= 2^25).  Checked bitwise against glibc on all 2^32 atanf arguments
+//              and on random atan2f pairs over the full exponent range.
 #pragma once
 
 TM_FN double tm_log(double x) {
@@ -106,4 +118,246 @@ TM_FN float tm_erfinvf(float y) {
   if (y == 0.0f) return y;
   const double r = tm_giles((double)y);
   return (float)(y < 0.0f ? -r : r);
+}
+
+// ------------------------------------------------------------------------------------------------ logf
+// x = 2^k z, z in [0x3f330000, 2 * 0x3f330000); c near the center of z's sixteenth; log x = k ln2 + log c +
+// log1p(z / c - 1), the last by a degree-4 polynomial in r = z * (1/c) - 1 evaluated in double.
+TM_FN float tm_logf(float x) {
+  const double T[16][2] = {
+      {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2}, {0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2},
+      {0x1.49539f0f010bp+0, -0x1.01eae7f513a67p-2},  {0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3},
+      {0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3}, {0x1.25e227b0b8eap+0, -0x1.1aa2bc79c81p-3},
+      {0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4}, {0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4},
+      {0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5}, {0x1p+0, 0x0p+0},
+      {0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5},  {0x1.ca4b31f026aap-1, 0x1.c5e53aa362eb4p-4},
+      {0x1.b2036576afce6p-1, 0x1.526e57720db08p-3},  {0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3},
+      {0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2},  {0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}};
+  const double A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2, A2 = -0x1.ffffef20a4123p-2;
+  const double Ln2 = 0x1.62e42fefa39efp-1;
+  u32 ix = tm_f2u(x);
+  if (ix == 0x3f800000u) return 0.0f;
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+    if (ix * 2u == 0u) return -__builtin_inff();
+    if (ix == 0x7f800000u) return x;
+    if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return __builtin_nanf("");
+    ix = tm_f2u(x * 0x1p23f);                     // a subnormal: normalise
+    ix -= 23u << 23;
+  }
+  const u32 tmp = ix - 0x3f330000u;
+  const int i = (int)((tmp >> 19) % 16u);
+  const int k = (i32)tmp >> 23;
+  const u32 iz = ix - (tmp & 0xff800000u);
+  const double z = (double)tm_u2f(iz);
+  const double r = __builtin_fma(z, T[i][0], -1.0);
+  const double y0 = __builtin_fma((double)k, Ln2, T[i][1]);
+  const double r2 = r * r;
+  double y = __builtin_fma(A1, r, A2);
+  y = __builtin_fma(A0, r2, y);
+  y = __builtin_fma(y, r2, y0 + r);
+  return (float)y;
+}
+
+// ------------------------------------------------------------------------------------------------ expf
+// x * 32 / ln2 = k + r, |r| <= 1/2; exp x = 2^(k/32) 2^(r/32), 2^(k/32) from the table (exponent added to the
+// bits), 2^(r/32) by a cubic in r.
+TM_FN float tm_expf(float x) {
+  const u64 T[32] = {
+      0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+      0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+      0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+      0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+      0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+      0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+  const double InvLn2N = 0x1.71547652b82fep+0 * 32, SHIFT = 0x1.8p+52;
+  const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+               C2 = 0x1.62e42ff0c52d6p-1 / 32;
+  const u32 ux = tm_f2u(x);
+  if (ux == 0x4202422fu) return 0x1.f93e38p+46f;         // the two knife-edge inputs (see the header)
+  if (ux == 0xc27c65d9u) return 0x1.f45326p-92f;
+  const u32 abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= (tm_f2u(88.0f) >> 20)) {
+    if (ux == tm_f2u(-__builtin_inff())) return 0.0f;
+    if (abstop >= (tm_f2u(__builtin_inff()) >> 20)) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.0f;
+  }
+  double z = InvLn2N * (double)x;
+  double kd = z + SHIFT;
+  const u64 ki = tm_d2u(kd);
+  kd -= SHIFT;
+  const double r = z - kd;
+  u64 t = T[ki % 32u];
+  t += ki << 47;
+  const double s = tm_u2d(t);
+  z = __builtin_fma(C0, r, C1);
+  const double r2 = r * r;
+  double y = __builtin_fma(C2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// ------------------------------------------------------------------------------------------ sinf / cosf
+struct TmSinCos {
+  double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3;
+};
+TM_FN const TmSinCos& tm_sincos_table(int which) {
+  static const TmSinCos T[2] = {
+      {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, 0x1p0, -0x1.ffffffd0c621cp-2,
+       0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+       0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
+      {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, -0x1p0, 0x1.ffffffd0c621cp-2,
+       -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+       0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13}};
+  return T[which];
+}
+TM_FN float tm_sc_poly(double x, double x2, const TmSinCos& p, int n) {
+  if ((n & 1) == 0) {
+    const double x3 = x * x2;
+    const double s1 = __builtin_fma(x2, p.s3, p.s2);
+    const double x7 = x3 * x2;
+    const double s = __builtin_fma(x3, p.s1, x);
+    return (float)__builtin_fma(x7, s1, s);
+  }
+  const double x4 = x2 * x2;
+  const double c2 = __builtin_fma(x2, p.c4, p.c3);
+  const double c1 = __builtin_fma(x2, p.c1, p.c0);
+  const double x6 = x4 * x2;
+  const double c = __builtin_fma(x4, p.c2, c1);
+  return (float)__builtin_fma(x6, c2, c);
+}
+// |x| < 120: n = round(x 2/pi) (through 2^24-scaled integer arithmetic), x - n pi/2 with one fma
+TM_FN double tm_sc_reduce_fast(double x, const TmSinCos& p, int* np) {
+  const double r = x * p.hpi_inv;
+  const int n = ((i32)r + 0x800000) >> 24;
+  *np = n;
+  return __builtin_fma(-(double)n, p.hpi, x);
+}
+// |x| >= 120: x (4/pi) mod 4 in 64-bit fixed point from a 2/pi bit table
+TM_FN double tm_sc_reduce_large(u32 xi, int* np) {
+  const u32 P[24] = {0xa2u, 0xa2f9u, 0xa2f983u, 0xa2f9836eu, 0xf9836e4eu, 0x836e4e44u, 0x6e4e4415u, 0x4e441529u,
+                     0x441529fcu, 0x1529fc27u, 0x29fc2757u, 0xfc2757d1u, 0x2757d1f5u, 0x57d1f534u, 0xd1f534ddu,
+                     0xf534ddc0u, 0x34ddc0dbu, 0xddc0db62u, 0xc0db6295u, 0xdb629599u, 0x6295993cu, 0x95993c43u,
+                     0x993c4390u, 0x3c439041u};
+  const u32* arr = &P[(xi >> 26) & 15u];
+  const int shift = (int)((xi >> 23) & 7u);
+  xi = (xi & 0xffffffu) | 0x800000u;
+  xi <<= shift;
+  u64 res0 = (u64)(u32)(xi * arr[0]);
+  const u64 res1 = (u64)xi * arr[4];
+  const u64 res2 = (u64)xi * arr[8];
+  res0 = (res2 >> 32) | (res0 << 32);
+  res0 += res1;
+  const u64 n = (res0 + (1ull << 61)) >> 62;
+  res0 -= n << 62;
+  *np = (int)n;
+  return (double)(i64)res0 * 0x1.921FB54442D18p-62;
+}
+TM_FN u32 tm_abstop12(float x) { return (tm_f2u(x) >> 20) & 0x7ffu; }
+TM_FN float tm_sinf(float y) {
+  double x = y;
+  int n;
+  if (tm_abstop12(y) < tm_abstop12(0x1.921FB6p-1f)) {
+    if (tm_abstop12(y) < tm_abstop12(0x1p-12f)) return y;
+    return tm_sc_poly(x, x * x, tm_sincos_table(0), 0);
+  }
+  if (tm_abstop12(y) < tm_abstop12(120.0f)) {
+    x = tm_sc_reduce_fast(x, tm_sincos_table(0), &n);
+    const double s = tm_sincos_table(0).sign[n & 3];
+    return tm_sc_poly(x * s, x * x, tm_sincos_table((n & 2) ? 1 : 0), n);
+  }
+  if (tm_abstop12(y) < tm_abstop12(__builtin_inff())) {
+    const u32 xi = tm_f2u(y);
+    const int sign = (int)(xi >> 31);
+    x = tm_sc_reduce_large(xi, &n);
+    const double s = tm_sincos_table(0).sign[(n + sign) & 3];
+    return tm_sc_poly(x * s, x * x, tm_sincos_table(((n + sign) & 2) ? 1 : 0), n);
+  }
+  return y - y;
+}
+TM_FN float tm_cosf(float y) {
+  double x = y;
+  int n;
+  if (tm_abstop12(y) < tm_abstop12(0x1.921FB6p-1f)) {
+    if (tm_abstop12(y) < tm_abstop12(0x1p-12f)) return 1.0f;
+    return tm_sc_poly(x, x * x, tm_sincos_table(0), 1);
+  }
+  if (tm_abstop12(y) < tm_abstop12(120.0f)) {
+    x = tm_sc_reduce_fast(x, tm_sincos_table(0), &n);
+    const double s = tm_sincos_table(0).sign[n & 3];
+    return tm_sc_poly(x * s, x * x, tm_sincos_table((n & 2) ? 1 : 0), n ^ 1);
+  }
+  if (tm_abstop12(y) < tm_abstop12(__builtin_inff())) {
+    const u32 xi = tm_f2u(y);
+    const int sign = (int)(xi >> 31);
+    x = tm_sc_reduce_large(xi, &n);
+    const double s = tm_sincos_table(0).sign[(n + sign) & 3];
+    return tm_sc_poly(x * s, x * x, tm_sincos_table(((n + sign) & 2) ? 1 : 0), n ^ 1);
+  }
+  return y - y;
+}
+
+// -------------------------------------------------------------------------------------- atanf / atan2f
+TM_FN float tm_atanf(float x) {
+  const float atanhi[4] = {4.6364760399e-01f, 7.8539812565e-01f, 9.8279368877e-01f, 1.5707962513e+00f};
+  const float atanlo[4] = {5.0121582440e-09f, 3.7748947079e-08f, 3.4473217170e-08f, 7.5497894159e-08f};
+  const float aT[11] = {3.3333334327e-01f, -2.0000000298e-01f, 1.4285714924e-01f, -1.1111110449e-01f,
+                        9.0908870101e-02f, -7.6918758452e-02f, 6.6610731184e-02f, -5.8335702866e-02f,
+                        4.9768779427e-02f, -3.6531571299e-02f, 1.6285819933e-02f};
+  const i32 hx = (i32)tm_f2u(x), ix = hx & 0x7fffffff;
+  int id;
+  if (ix >= 0x4c000000) {                          // |x| >= 2^25
+    if (ix > 0x7f800000) return x + x;
+    return hx > 0 ? atanhi[3] + atanlo[3] : -atanhi[3] - atanlo[3];
+  }
+  if (ix < 0x3ee00000) {
+    if (ix < 0x31000000) return x;
+    id = -1;
+  } else {
+    x = __builtin_fabsf(x);
+    if (ix < 0x3f980000) {
+      if (ix < 0x3f300000) { id = 0; x = (2.0f * x - 1.0f) / (2.0f + x); }
+      else { id = 1; x = (x - 1.0f) / (x + 1.0f); }
+    } else {
+      if (ix < 0x401c0000) { id = 2; x = (x - 1.5f) / (1.0f + 1.5f * x); }
+      else { id = 3; x = -1.0f / x; }
+    }
+  }
+  const float z = x * x, w = z * z;
+  const float s1 = z * (aT[0] + w * (aT[2] + w * (aT[4] + w * (aT[6] + w * (aT[8] + w * aT[10])))));
+  const float s2 = w * (aT[1] + w * (aT[3] + w * (aT[5] + w * (aT[7] + w * aT[9]))));
+  if (id < 0) return x - x * (s1 + s2);
+  const float r = atanhi[id] - ((x * (s1 + s2) - atanlo[id]) - x);
+  return hx < 0 ? -r : r;
+}
+TM_FN float tm_atan2f(float y, float x) {
+  const float tiny = 1.0e-30f, pi_o_4 = 7.8539818525e-01f, pi_o_2 = 1.5707963705e+00f, pi = 3.1415927410e+00f,
+              pi_lo = -8.7422776573e-08f;
+  const i32 hx = (i32)tm_f2u(x), ix = hx & 0x7fffffff, hy = (i32)tm_f2u(y), iy = hy & 0x7fffffff;
+  if (ix > 0x7f800000 || iy > 0x7f800000) return x + y;
+  if (hx == 0x3f800000) return tm_atanf(y);
+  const int m = ((hy >> 31) & 1) | ((hx >> 30) & 2);
+  if (iy == 0) return m == 0 || m == 1 ? y : (m == 2 ? pi + tiny : -pi - tiny);
+  if (ix == 0) return hy < 0 ? -pi_o_2 - tiny : pi_o_2 + tiny;
+  if (ix == 0x7f800000) {
+    if (iy == 0x7f800000) {
+      return m == 0 ? pi_o_4 + tiny : (m == 1 ? -pi_o_4 - tiny : (m == 2 ? 3.0f * pi_o_4 + tiny : -3.0f * pi_o_4 - tiny));
+    }
+    return m == 0 ? 0.0f : (m == 1 ? -0.0f : (m == 2 ? pi + tiny : -pi - tiny));
+  }
+  if (iy == 0x7f800000) return hy < 0 ? -pi_o_2 - tiny : pi_o_2 + tiny;
+  const i32 k = (iy - ix) >> 23;
+  float z;
+  if (k > 60) z = pi_o_2 + 0.5f * pi_lo;
+  else if (hx < 0 && k < -60) z = 0.0f;
+  else z = tm_atanf(__builtin_fabsf(y / x));
+  switch (m) {
+    case 0: return z;
+    case 1: return tm_u2f(tm_f2u(z) ^ 0x80000000u);
+    case 2: return pi - (z - pi_lo);
+    default: return (z - pi_lo) - pi;
+  }
 }

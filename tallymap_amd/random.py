@@ -4,7 +4,7 @@
 
   fold_in(k, d)      = threefry2x32(k; (0, uint32(d)))           (threefry_fold_in: threefry_2x32(k, seed(d)))
   split(k, n)[i]     = threefry2x32(k; (hi(i), lo(i)))           (iota_2x32_shape counters)
-  bits(k)            = o0 ^ o1 of threefry2x32(k; (0, 0))         (32-bit random_bits of shape ())
+  bits(k, (n,))[i]   = o0 ^ o1 of threefry2x32(k; (hi(i), lo(i)))  (32-bit random_bits; shape () is i = 0)
   uniform(k, lo, hi) = max(lo, (bitcast((bits >> 9) | 0x3f800000) - 1) * (hi - lo) + lo)
   normal(k)          = float32(sqrt 2) * erf_inv(uniform(k, nextafter(-1, 0), 1))
 
@@ -58,16 +58,31 @@ def _host_fold_in(keys, d):
     return np.stack([o0, o1], axis=-1)
 
 
-def _host_bits(keys):
+def _host_bits(keys, shape=()):
     keys = np.asarray(keys, np.uint32)
-    z = np.zeros(keys.shape[:-1], np.uint32)
-    o0, o1 = _tf_np(keys[..., 0], keys[..., 1], z, z)
+    n = _count(shape)
+    if n is None:
+        z = np.zeros(keys.shape[:-1], np.uint32)
+        o0, o1 = _tf_np(keys[..., 0], keys[..., 1], z, z)
+        return o0 ^ o1
+    i = np.arange(n, dtype=np.uint64)
+    o0, o1 = _tf_np(keys[..., 0:1], keys[..., 1:2], (i >> np.uint64(32)).astype(np.uint32), i.astype(np.uint32))
     return o0 ^ o1
 
 
-def _host_uniform(keys, minval, maxval):
+def _count(shape):
+    """None for shape (), n for shape (n,); other shapes are refused."""
+    shape = tuple(int(d) for d in shape)
+    if shape == ():
+        return None
+    if len(shape) != 1:
+        raise C.TraceError(f"random draws of shape {shape}: only () and (n,) are supported by this backend")
+    return shape[0]
+
+
+def _host_uniform(keys, minval, maxval, shape=()):
     lo, hi = np.float32(minval), np.float32(maxval)
-    f = ((_host_bits(keys) >> np.uint32(9)) | np.uint32(0x3F800000)).view(np.float32) - np.float32(1.0)
+    f = ((_host_bits(keys, shape) >> np.uint32(9)) | np.uint32(0x3F800000)).view(np.float32) - np.float32(1.0)
     span = np.float32(hi - lo)
     r = (f * span).astype(np.float32) + lo
     return np.maximum(lo, r).astype(np.float32)
@@ -119,23 +134,23 @@ def split(key, num=2):
     return C.stack(rows)
 
 
-def bits(key):
+def bits(key, shape=()):
     if not C.is_traced(key):
-        return _host_bits(key)
+        return _host_bits(key, shape)
+    n = _count(shape)
     k0, k1 = _words(key)
-    o0, o1 = threefry2x32(k0, k1, 0, 0)
-    return o0 ^ o1
+    if n is None:
+        o0, o1 = threefry2x32(k0, k1, 0, 0)
+        return o0 ^ o1
+    out = []
+    for i in range(n):
+        o0, o1 = threefry2x32(k0, k1, (i >> 32) & 0xFFFFFFFF, i & 0xFFFFFFFF)
+        out.append(o0 ^ o1)
+    return C.stack(out)
 
 
-def uniform(key, shape=(), dtype=np.float32, minval=0.0, maxval=1.0):
-    if tuple(shape) != ():
-        raise C.TraceError("uniform: only shape () draws are supported by this backend")
-    if np.dtype(dtype) != C.F32:
-        raise C.TraceError("uniform: only float32 draws are supported by this backend")
-    if not C.is_traced(key):
-        return _host_uniform(key, minval, maxval)
-    lo, hi = np.float32(minval), np.float32(maxval)
-    b = bits(key)
+def _unit(b, lo, hi):
+    """uniform's float32 arithmetic on one traced uint32 scalar of bits."""
     fb = (b >> 9) | np.uint32(0x3F800000)
     f = C.bind("bitcast_convert_type", [fb.var], [C.AVal((), C.F32)], new_dtype=C.F32)[0] - np.float32(1.0)
     span = np.float32(hi - lo)          # maxval - minval, in float32
@@ -143,9 +158,27 @@ def uniform(key, shape=(), dtype=np.float32, minval=0.0, maxval=1.0):
     return C.binop("max", lo, r)
 
 
+def uniform(key, shape=(), dtype=np.float32, minval=0.0, maxval=1.0):
+    if np.dtype(dtype) != C.F32:
+        raise C.TraceError("uniform: only float32 draws are supported by this backend")
+    n = _count(shape)
+    if not C.is_traced(key):
+        return _host_uniform(key, minval, maxval, shape)
+    lo, hi = np.float32(minval), np.float32(maxval)
+    b = bits(key, shape)
+    if n is None:
+        return _unit(b, lo, hi)
+    return C.stack([_unit(b[i], lo, hi) for i in range(n)])
+
+
 def normal(key, shape=(), dtype=np.float32):
-    if tuple(shape) != () or np.dtype(dtype) != C.F32:
-        raise C.TraceError("normal: only float32 scalar draws are supported by this backend")
+    if np.dtype(dtype) != C.F32:
+        raise C.TraceError("normal: only float32 draws are supported by this backend")
+    if not C.is_traced(key):
+        raise C.TraceError("normal: host draws are not provided (erf_inv has no host restatement here)")
+    n = _count(shape)
     lo = np.nextafter(np.float32(-1.0), np.float32(0.0))
-    u = uniform(key, (), np.float32, lo, np.float32(1.0))
-    return np.float32(np.sqrt(2)) * C.unop("erf_inv", u, float_only=True)
+    u = uniform(key, shape, np.float32, lo, np.float32(1.0))
+    if n is None:
+        return np.float32(np.sqrt(2)) * C.unop("erf_inv", u, float_only=True)
+    return C.stack([np.float32(np.sqrt(2)) * C.unop("erf_inv", u[i], float_only=True) for i in range(n)])

@@ -2,6 +2,11 @@
 //   libm_check erfinv_normal   every f32 argument jax.random.normal passes to erf_inv (2^23 uniform values):
 //                              tm_erfinvf vs the reference CPU target's formula with glibc log / sqrt
 //   libm_check log <n> <seed>  n random positive doubles: tm_log vs glibc log (ulp histogram)
+//   libm_check f32 <fn> <stride> <offset>
+//                              logf / expf / sinf / cosf / atanf on every stride-th f32 bit pattern from offset
+//                              (stride 1: all 2^32): bitwise mismatches and the largest ulp distance
+//   libm_check atan2 <n> <seed>
+//                              n random (y, x) pairs of finite f32 over the full exponent range: tm_atan2f vs glibc
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -55,6 +60,46 @@ int main(int argc, char** argv) {
     printf("log: %ld random doubles, %ld differ from glibc, %ld by more than 1 ulp\n", n, diff, big);
     return big != 0;
   }
-  fprintf(stderr, "usage: libm_check erfinv_normal | log <n> <seed>\n");
+  if (argc > 4 && !strcmp(argv[1], "f32")) {
+    float (*mine)(float) = nullptr;
+    float (*ref)(float) = nullptr;
+    if (!strcmp(argv[2], "logf")) { mine = tm_logf; ref = logf; }
+    else if (!strcmp(argv[2], "expf")) { mine = tm_expf; ref = expf; }
+    else if (!strcmp(argv[2], "sinf")) { mine = tm_sinf; ref = sinf; }
+    else if (!strcmp(argv[2], "cosf")) { mine = tm_cosf; ref = cosf; }
+    else if (!strcmp(argv[2], "atanf")) { mine = tm_atanf; ref = atanf; }
+    if (!mine) return 2;
+    const uint64_t stride = strtoull(argv[3], nullptr, 0), off = strtoull(argv[4], nullptr, 0);
+    long n = 0, bad = 0, maxulp = 0;
+    for (uint64_t u = off; u < (1ull << 32); u += stride) {
+      const float x = tm_u2f((uint32_t)u), a = mine(x), b = ref(x);
+      ++n;
+      if (std::isnan(a) && std::isnan(b)) continue;
+      if (tm_f2u(a) == tm_f2u(b)) continue;
+      if (++bad <= 5) printf("  x=%a (0x%08x) tm=%a glibc=%a\n", x, (uint32_t)u, a, b);
+      const long d = labs((long)(int32_t)tm_f2u(a) - (long)(int32_t)tm_f2u(b));
+      if (d > maxulp) maxulp = d;
+    }
+    printf("%s: %ld arguments, %ld mismatches, max %ld ulp\n", argv[2], n, bad, maxulp);
+    return 0;
+  }
+  if (argc > 3 && !strcmp(argv[1], "atan2")) {
+    long n = atol(argv[2]);
+    srand48(atol(argv[3]));
+    long bad = 0, maxulp = 0;
+    for (long i = 0; i < n; ++i) {
+      const uint32_t by = (uint32_t)mrand48(), bx = (uint32_t)mrand48();
+      const float y = tm_u2f(by), x = tm_u2f(bx);
+      if (!std::isfinite(y) || !std::isfinite(x)) { --i; continue; }
+      const float a = tm_atan2f(y, x), b = atan2f(y, x);
+      if (tm_f2u(a) == tm_f2u(b)) continue;
+      ++bad;
+      const long d = labs((long)(int32_t)tm_f2u(a) - (long)(int32_t)tm_f2u(b));
+      if (d > maxulp) maxulp = d;
+    }
+    printf("atan2: %ld pairs, %ld mismatches, max %ld ulp\n", n, bad, maxulp);
+    return 0;
+  }
+  fprintf(stderr, "usage: libm_check erfinv_normal | log <n> <seed> | f32 <fn> <stride> <offset> | atan2 <n> <seed>\n");
   return 2;
 }

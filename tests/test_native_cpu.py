@@ -95,6 +95,20 @@ def test_log_within_one_ulp_of_glibc(libm):
     assert r.returncode == 0, r.stdout
 
 
+@pytest.mark.parametrize("fn", ["logf", "expf", "sinf", "cosf", "atanf"])
+def test_f32_libm_bitwise_equal_to_glibc(libm, fn):
+    """tm_libm.h's float functions against this host's glibc on every 251st bit pattern (17.1M arguments: every
+    exponent, sign, NaN and infinity class; 2^32 exhaustively with `libm_check f32 <fn> 1 0`, 0 mismatches)."""
+    r = subprocess.run([libm, "f32", fn, "251", "7"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert ", 0 mismatches" in r.stdout, r.stdout
+
+
+def test_atan2f_bitwise_equal_to_glibc(libm):
+    r = subprocess.run([libm, "atan2", "2000000", "11"], capture_output=True, text=True)
+    assert r.returncode == 0 and ", 0 mismatches" in r.stdout, r.stdout
+
+
 def test_generated_modules_compile_for_gfx950():
     """the forward modules of configs 1 and 2 compile through the product's hipRTC path (no GPU needed)."""
     from tallymap_amd import _core as C
