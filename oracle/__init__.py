@@ -52,6 +52,12 @@ def lib():
         L.tmref_c2_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p]
         L.tmref_c2_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
         L.tmref_c2_x0.argtypes = [_p, _i64, _p]
+        L.tmref_c3_fwd.argtypes = [_p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
+        L.tmref_c3_grad.argtypes = [_p, _f, _i64, _i, _i, _p, _p, _p]
+        L.tmref_c4_fwd.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p]
+        L.tmref_c4_grad.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
+        L.tmref_c5_fwd.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
+        L.tmref_c5_grad.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p]
         L.tmref_max_threads.restype = _i
         _lib = L
     return _lib
@@ -181,3 +187,78 @@ def c2_x0(keys):
     out = np.zeros(keys.shape[0], np.float32)
     lib().tmref_c2_x0(_ptr(keys), keys.shape[0], _ptr(out))
     return out
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dt)
+
+
+def _per_item(n, per_item):
+    return (np.zeros(n, np.int32), np.zeros(n, np.uint8)) if per_item else (None, None)
+
+
+def c3_fwd(keys, mu_a, max_steps=1024, nthreads=0, shadow=True, per_item=True):
+    keys = _c(keys, np.uint32)
+    n = keys.shape[0]
+    ab = np.zeros(64 * 64, np.float32)
+    a64 = np.zeros(64 * 64, np.float64) if shadow else None
+    ks, tr = _per_item(n, per_item)
+    st = np.zeros(5, np.int32)
+    lib().tmref_c3_fwd(_ptr(keys), float(np.float32(mu_a)), n, max_steps, nthreads, _ptr(ab), _ptr(a64), _ptr(ks),
+                       _ptr(tr), _ptr(st))
+    return Fwd({"absorbed": ab.reshape(64, 64)}, {"absorbed": a64.reshape(64, 64) if shadow else None}, ks,
+               tr.astype(bool) if tr is not None else None, st)
+
+
+def c3_grad(keys, mu_a, ct, max_steps=1024, nthreads=0):
+    keys, ct = _c(keys, np.uint32), _c(ct, np.float32)
+    out, ntr = np.zeros(1, np.float32), np.zeros(1, np.int32)
+    lib().tmref_c3_grad(_ptr(keys), float(np.float32(mu_a)), keys.shape[0], max_steps, nthreads, _ptr(ct), _ptr(out),
+                        _ptr(ntr))
+    return out[0], int(ntr[0])
+
+
+def c4_fwd(p0, keys, ids, a, max_steps=1024, nthreads=0, shadow=True, per_item=True):
+    p0, keys, ids = _c(p0, np.float32), _c(keys, np.uint32), _c(ids, np.int32)
+    n = p0.shape[0]
+    grid, walker = np.zeros(256 * 256, np.float32), np.zeros(n, np.float32)
+    g64 = np.zeros(256 * 256, np.float64) if shadow else None
+    w64 = np.zeros(n, np.float64) if shadow else None
+    ks, tr = _per_item(n, per_item)
+    st = np.zeros(5, np.int32)
+    lib().tmref_c4_fwd(_ptr(p0), _ptr(keys), _ptr(ids), float(np.float32(a)), n, max_steps, nthreads, _ptr(grid),
+                       _ptr(walker), _ptr(g64), _ptr(w64), _ptr(ks), _ptr(tr), _ptr(st))
+    r = lambda x, sh: x.reshape(sh) if x is not None else None
+    return Fwd({"grid": grid.reshape(256, 256), "walker": walker.reshape(n, 1)},
+               {"grid": r(g64, (256, 256)), "walker": r(w64, (n, 1))}, ks,
+               tr.astype(bool) if tr is not None else None, st)
+
+
+def c4_grad(p0, keys, ids, a, ct_grid, ct_walker, max_steps=1024, nthreads=0):
+    p0, keys, ids = _c(p0, np.float32), _c(keys, np.uint32), _c(ids, np.int32)
+    cg, cw = _c(ct_grid, np.float32), _c(ct_walker, np.float32)
+    out, ntr = np.zeros(1, np.float32), np.zeros(1, np.int32)
+    lib().tmref_c4_grad(_ptr(p0), _ptr(keys), _ptr(ids), float(np.float32(a)), p0.shape[0], max_steps, nthreads,
+                        _ptr(cg), _ptr(cw), _ptr(out), _ptr(ntr))
+    return out[0], int(ntr[0])
+
+
+def c5_fwd(th0, om0, ids, A, max_steps=20_000, nthreads=0, shadow=True, per_item=True):
+    th0, om0, ids = _c(th0, np.float32), _c(om0, np.float32), _c(ids, np.int32)
+    n = th0.shape[0]
+    state = np.zeros(2 * n, np.float32)
+    s64 = np.zeros(2 * n, np.float64) if shadow else None
+    ks, tr = _per_item(n, per_item)
+    st = np.zeros(5, np.int32)
+    lib().tmref_c5_fwd(_ptr(th0), _ptr(om0), _ptr(ids), float(np.float32(A)), n, max_steps, nthreads, _ptr(state),
+                       _ptr(s64), _ptr(ks), _ptr(tr), _ptr(st))
+    return Fwd({"state": state.reshape(n, 2)}, {"state": s64.reshape(n, 2) if shadow else None}, ks,
+               tr.astype(bool) if tr is not None else None, st)
+
+
+def c5_grad(th0, om0, ids, A, ct, max_steps=20_000, nthreads=0):
+    th0, om0, ids, ct = _c(th0, np.float32), _c(om0, np.float32), _c(ids, np.int32), _c(ct, np.float32)
+    out, ntr = np.zeros(1, np.float32), np.zeros(1, np.int32)
+    lib().tmref_c5_grad(_ptr(th0), _ptr(om0), _ptr(ids), float(np.float32(A)), th0.shape[0], max_steps, nthreads,
+                        _ptr(ct), _ptr(out), _ptr(ntr))
+    return out[0], int(ntr[0])

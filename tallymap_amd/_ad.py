@@ -148,6 +148,8 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
         def add(v, c):
             if not isinstance(v, C.Var) or v.id not in act or c is None:
                 return
+            if v.aval.shape == () and C.is_traced(c) and c.shape != ():
+                c = _sum_all(c)           # a scalar operand broadcast against an array: sum the cotangent
             if v.id in ct:
                 ct[v.id] = ct[v.id] + c
             else:
@@ -179,11 +181,12 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
         for v, m in zip(jx.invars, ct_in_mask):
             if m:
                 c = ct.get(v.id)
-                if c is None:
-                    c = C.Tracer(C.bind("copy", [C.Lit(0, v.aval.strong())], [v.aval.strong()])[0].var)
+                if c is None or not C.is_traced(c):
+                    z = np.broadcast_to(np.asarray(0 if c is None else c, v.aval.dtype), v.aval.shape).copy()
+                    c = C.Tracer(C.bind("copy", [C.Lit(z, v.aval.strong())], [v.aval.strong()])[0].var)
                 elif c.dtype != v.aval.dtype:
                     c = C.convert(c, v.aval.dtype)
-                res.append(b.local(c.var) if C.is_traced(c) else c)
+                res.append(b.local(c.var))
     finally:
         C._STACK.pop()
     outv = []
@@ -355,8 +358,71 @@ def r_copy(g, ins, outs, e):
     return [g[0]]
 
 
+# ------------------------------------------------------------------------- structural (small arrays)
+def _reshape(x, shape):
+    if not C.is_traced(x):
+        a = np.asarray(x)
+        return np.broadcast_to(a, shape).copy() if a.size == 1 else np.reshape(a, shape)
+    return C.bind("reshape", [x.var], [C.AVal(tuple(shape), x.dtype)], new_sizes=tuple(shape), dimensions=None)[0]
+
+
+def _sum_all(x):
+    if not C.is_traced(x) or x.shape == ():
+        return x
+    return C.reduce_sum(_reshape(x, (x.aval.size,)))
+
+
+def r_slice(g, ins, outs, e):
+    """the transpose of a leading-axis slice x[i:j] (strides 1): g in rows i..j-1 of a zero array."""
+    x = ins[0]
+    st, lim = e.params["start_indices"], e.params["limit_indices"]
+    if (e.params.get("strides") not in (None, (1,) * len(st)) or any(s != 0 for s in st[1:])
+            or tuple(lim[1:]) != tuple(x.shape[1:])):
+        raise ADError(f"reverse mode of slice {st}:{lim} (only leading-axis slices are supported)")
+    rest = tuple(x.shape[1:])
+    rows = []
+    for r in range(x.shape[0]):
+        if st[0] <= r < lim[0]:
+            rows.append(C.getitem(g[0], r - st[0]))
+        else:
+            rows.append(np.zeros(rest, g[0].dtype))
+    return [C.stack(rows)]
+
+
+def r_reshape(g, ins, outs, e):
+    return [_reshape(g[0], ins[0].shape)]
+
+
+def r_broadcast(g, ins, outs, e):
+    x = ins[0]
+    xs = np.shape(x) if not C.is_traced(x) else x.shape
+    if int(np.prod(xs, dtype=np.int64)) == outs[0].aval.size:
+        return [_reshape(g[0], xs)]
+    if xs == ():
+        return [_sum_all(g[0])]
+    raise ADError(f"reverse mode of broadcast_in_dim {xs} -> {outs[0].shape}")
+
+
+def r_concatenate(g, ins, outs, e):
+    if e.params.get("dimension", 0) != 0:
+        raise ADError("reverse mode of concatenate along an axis other than 0")
+    res, off = [], 0
+    rest = tuple(outs[0].shape[1:])
+    for x in ins:
+        n = (x.shape if C.is_traced(x) else np.shape(x))[0]
+        if C.is_traced(x):
+            res.append(C.bind("slice", [g[0].var], [C.AVal((n,) + rest, g[0].dtype)],
+                              start_indices=(off,) + (0,) * len(rest), limit_indices=(off + n,) + rest,
+                              strides=None)[0])
+        else:
+            res.append(None)
+        off += n
+    return res
+
+
 RULES = {"add": r_add, "sub": r_sub, "mul": r_mul, "div": r_div, "neg": r_neg, "max": r_max, "min": r_min,
          "abs": r_abs, "sqrt": r_sqrt, "rsqrt": r_rsqrt, "exp": r_exp, "log": r_log, "log1p": r_log1p,
          "expm1": r_expm1, "sin": r_sin, "cos": r_cos, "tanh": r_tanh, "logistic": r_logistic, "atan2": r_atan2,
          "pow": r_pow, "integer_pow": r_integer_pow, "erf_inv": r_erf_inv, "select_n": r_select,
-         "convert_element_type": r_convert, "copy": r_copy}
+         "convert_element_type": r_convert, "copy": r_copy, "slice": r_slice, "squeeze": r_reshape,
+         "reshape": r_reshape, "broadcast_in_dim": r_broadcast, "concatenate": r_concatenate}

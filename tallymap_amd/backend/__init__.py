@@ -131,14 +131,16 @@ def kernel_info(c):
     return dict(zip(keys, [int(v) for v in out]))
 
 
-def prebuild(configs, n=64):
-    """compile (through hipRTC, no GPU needed) the forward and adjoint modules of each config in `configs`
-    ({name: dict(item, outputs, in_axes, max_steps)}) into the package's code-object cache -> [(name, tag, key)]."""
+def prebuild(entries, n=64):
+    """compile (through hipRTC, no GPU needed) the forward and adjoint modules of each (name, config) in
+    `entries` (config = dict(item, outputs, in_axes, max_steps); a config whose outputs are sized by N appears once
+    per N) into the package's code-object cache -> [(name, tag, key)].  The operand shapes come from the config's
+    input generator at `n` items (per-item shapes do not depend on N)."""
     from .. import _core as C
     from .._api import build_program
     from .. import configs as CF
     done = []
-    for name, cfg in configs.items():
+    for name, cfg in entries:
         args = getattr(CF, f"{name}_inputs")(n)
         axes = cfg["in_axes"]
         pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]

@@ -433,11 +433,13 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK):
     body.append("        }")
     body.append("      }")
     body.append("    }")
-    body.append("    if (!tm_live) {")
-    body.append("      if (!tm_more) break;")
-    body.append("      continue;")
-    body.append("    }")
+    # One exit, wave-uniform (a ballot), and no `continue`: every lane reaches the claim block above on every
+    # iteration.  A per-lane `continue` lets the compiler's loop structurizer park idle lanes off the exec mask
+    # while live lanes run the header again, and the claim and operand staging would then run with a partial wave.
+    body.append("    if (tm_live) {")
     body += step_lines
+    body.append("    }")
+    body.append("    if (tm_ballot(tm_live || tm_more) == 0ull) break;")
     body.append("  }")
     body.append("  if (tm_drop) atomicAdd(&TM_STATS[4], tm_drop);")
     body.append("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")

@@ -103,7 +103,6 @@ def split(prog):
     for e in pre_e:
         if e.prim in ("tallymap_emit", "copy") and isinstance(e.invars[0], C.Var) and e.invars[0].id in slot:
             slot[e.outvars[0].id] = slot[e.invars[0].id]
-    car_slot = [slot.get(v.id) if isinstance(v, C.Var) else None for v in init]
     # P: non-tally vars read by the loop's constants or by POST, defined before the loop (operands or PRE results)
     post_free = set()
     for e in post_e:
@@ -119,6 +118,22 @@ def split(prog):
     for e in pre_e:
         for o in e.outvars:
             defined_before[o.id] = o
+    cond_jx, body_jx, w_out = we.params["cond_jaxpr"], we.params["body_jaxpr"], list(we.outvars)
+    # a tally the loop does not carry but POST emits into rides through the loop as an untouched carry, so that
+    # every tally value POST sees is a final carry (the adjoint threads tallies only through carries)
+    thru = [defined_before[i] for i in sorted(post_free) if i in slot and i in defined_before]
+    ren_thru = {}
+    if thru:
+        b_in = [C.Var(v.aval) for v in thru]
+        c_in = [C.Var(v.aval) for v in thru]
+        body_jx = C.Jaxpr(list(body_jx.invars) + b_in, list(body_jx.outvars) + b_in, body_jx.eqns)
+        cond_jx = C.Jaxpr(list(cond_jx.invars) + c_in, cond_jx.outvars, cond_jx.eqns)
+        outs = [C.Var(v.aval) for v in thru]
+        ren_thru = {v.id: o for v, o in zip(thru, outs)}
+        init = list(init) + thru
+        w_out = w_out + outs
+        post_e = [_ren_eqn(e, ren_thru) for e in post_e]
+    car_slot = [slot.get(v.id) if isinstance(v, C.Var) else None for v in init]
     need = [v for v in cc + bc if isinstance(v, C.Var)]
     need += [defined_before[i] for i in sorted(post_free) if i in defined_before]
     P, seen = [], set()
@@ -135,13 +150,13 @@ def split(prog):
     for v in init:
         pre_out.append(v)
     pre = C.Jaxpr(list(jx.invars), pre_out + P, pre_e)
-    post_in_car = [C.Var(o.aval) for o in we.outvars]
-    ren = {o.id: nv for o, nv in zip(we.outvars, post_in_car)}
-    post = C.Jaxpr([_ren(v, ren) for v in P] + post_in_car, [_ren(v, ren) for v in jx.outvars],
-                   [_ren_eqn(e, ren) for e in post_e])
+    post_in_car = [C.Var(o.aval) for o in w_out]
+    ren = {o.id: nv for o, nv in zip(w_out, post_in_car)}
+    outv = [_ren(_ren(v, ren_thru), ren) for v in jx.outvars]
+    post = C.Jaxpr([_ren(v, ren) for v in P] + post_in_car, outv, [_ren_eqn(e, ren) for e in post_e])
     # (P vars keep their identity inside POST: their ids are the same objects)
     post = C.Jaxpr(list(P) + post_in_car, post.outvars, post.eqns)
-    return Split(pre, we.params["cond_jaxpr"], we.params["body_jaxpr"], post, len(P), len(init),
+    return Split(pre, cond_jx, body_jx, post, len(P), len(init),
                  [const_ref(v) for v in cc], [const_ref(v) for v in bc], car_slot)
 
 
@@ -513,7 +528,7 @@ def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
     out("    const u64 tm_base = tm_claim(tm_ctr, 64u);")       # item schedule: the whole wave claims 64 items
     out("    if (tm_base + 64u >= (u64)n_items) tm_more = false;")
     out("    const u64 tm_t = tm_base + (u64)tm_lane();")
-    out("    if (tm_t >= (u64)n_items) continue;")
+    out("    if (tm_t < (u64)n_items) {")          # no `continue`: the claim above stays wave-converged
     out("    const i64 tm_item = (i64)tm_t;")
     # operands
     em.lines, em.ind = [], 2
@@ -737,6 +752,7 @@ def build(adj, block=K.BLOCK, ckpt=C_DEFAULT):
             n = max(1, pav[i].size)
             for e in range(n):
                 out(f"((float*)P.p[{r_gpi[i]}])[tm_item * {n} + {e}] = 0.0f;", 2)
+    out("    }")
     out("  }")
     out("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")
     if adj.wrt_bc:

@@ -1,0 +1,137 @@
+"""Parity of BASELINE configs 3-5 on the GPU against the oracle, forward and replay gradient, on the same seeded
+inputs: trip counts, truncation flags and stats bit-exact; tallies with one emit per bin (C4's per-walker
+(N, 1), C5's per-item (N, 2)) bit-exact; shared bins within 1e-5 relative of the oracle's float64 re-summation;
+gradients within 1e-4 relative of the oracle's forward-mode (dual number) gradients.  A bin
+whose emits have mixed signs (C4's grid) is held to 1e-5 of the sum of the emits' magnitudes: the bound any f32
+summation order meets, since its error scales with sum |x|, not with |sum x|."""
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import configs
+
+pytestmark = pytest.mark.gpu
+RTOL = 1e-5
+GTOL = 1e-4
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _np(x):
+    return x.cpu().numpy()
+
+
+def _close(got, want64, rtol=RTOL, mag=None):
+    got = np.asarray(got, np.float64)
+    scale = np.max(np.abs(want64)) if want64.size else 0.0
+    ref = np.abs(want64) if mag is None else np.maximum(np.abs(want64), mag)
+    ok = np.abs(got - want64) <= rtol * ref + 1e-6 * rtol * scale
+    return bool(np.all(ok)), float(np.max(np.abs(got - want64) / np.maximum(np.abs(want64), 1e-30)))
+
+
+def _mapped(cfg, **opts):
+    return tm.vmap(cfg["item"], outputs=cfg["outputs"], in_axes=cfg["in_axes"], max_steps=cfg["max_steps"], **opts)
+
+
+def _common(res, ref):
+    assert np.array_equal(_np(res.per_item), ref.per_item)
+    assert np.array_equal(_np(res.truncated), ref.trunc)
+    assert int(_np(res.stats["dropped_emits"])) == int(ref.stats[4])
+    assert int(_np(res.stats["n_truncated"])) == int(ref.trunc.sum()) == 0
+
+
+def _rel(got, want):
+    return abs(float(got) - float(want)) / max(abs(float(want)), 1e-30)
+
+
+# ------------------------------------------------------------------------------------------------- C3
+@pytest.mark.parametrize("n", [65_536, 4_194_304])
+def test_c3_slab_transport_parity(oracle, n):
+    print(f"case: C3 forward N={n}", flush=True)
+    keys, mu_a = configs.c3_inputs(n)
+    res = _mapped(configs.C3)(keys, mu_a)
+    _sync()
+    ref = oracle.c3_fwd(keys, mu_a)
+    _common(res, ref)
+    ok, err = _close(_np(res.outputs["absorbed"]), ref.tallies64["absorbed"])
+    assert ok, err
+    assert int(ref.stats[4]) > 0          # escapes and r >= 5 deposits are dropped emits
+
+
+@pytest.mark.parametrize("n", [65_536, 4_194_304])
+def test_c3_grad_mu_a(oracle, n):
+    """d sum(absorbed) / d mu_a: the checkpointed replay adjoint (the weight is a loop carry) vs forward mode."""
+    print(f"case: C3 grad mu_a N={n}", flush=True)
+    keys, mu_a = configs.c3_inputs(n)
+    g = tm.grad(_mapped(configs.C3), argnums=1)(keys, mu_a)
+    _sync()
+    want, ntr = oracle.c3_grad(keys, mu_a, np.ones((64, 64), np.float32))
+    assert ntr == 0
+    assert _rel(_np(g), want) <= GTOL, (float(_np(g)), float(want))
+
+
+# ------------------------------------------------------------------------------------------------- C4
+@pytest.mark.parametrize("n", [65_536, 4_194_304])
+def test_c4_walk_on_spheres_parity(oracle, n):
+    print(f"case: C4 forward N={n}", flush=True)
+    p0, keys, ids, a = configs.c4_inputs(n)
+    res = _mapped(configs.c4_config(n))(p0, keys, ids, a)
+    _sync()
+    ref = oracle.c4_fwd(p0, keys, ids, a)
+    _common(res, ref)
+    walker = _np(res.outputs["walker"])
+    assert walker.shape == (n, 1)
+    assert np.array_equal(walker.view(np.uint32), ref.tallies["walker"].view(np.uint32))
+    # sum |score| per grid bin (every walker's score is its walker row; its bin is fixed by its start point)
+    b = ((p0 + np.float32(1.0)) * np.float32(128.0)).astype(np.int32)
+    flat = b[:, 0].astype(np.int64) * 256 + b[:, 1]
+    mag = np.bincount(flat, np.abs(ref.tallies["walker"][:, 0].astype(np.float64)), 256 * 256).reshape(256, 256)
+    ok, err = _close(_np(res.outputs["grid"]), ref.tallies64["grid"], mag=mag)
+    assert ok, err
+
+
+@pytest.mark.parametrize("n", [65_536, 4_194_304])
+def test_c4_grad_amplitude(oracle, n):
+    """d (sum(grid) + sum(walker)) / d a = 2 sum(scores) / a (a multiplies every emit) and the oracle's gradient."""
+    print(f"case: C4 grad a N={n}", flush=True)
+    p0, keys, ids, a = configs.c4_inputs(n)
+    f = _mapped(configs.c4_config(n))
+    g = float(_np(tm.grad(f, argnums=3)(p0, keys, ids, a)))
+    want, ntr = oracle.c4_grad(p0, keys, ids, a, np.ones((256, 256), np.float32), np.ones((n, 1), np.float32))
+    ref = oracle.c4_fwd(p0, keys, ids, a, per_item=False)
+    closed = 2.0 * ref.tallies64["walker"].sum() / float(a)
+    assert ntr == 0
+    assert _rel(g, want) <= GTOL, (g, float(want))
+    assert _rel(g, closed) <= GTOL, (g, closed)
+
+
+# ------------------------------------------------------------------------------------------------- C5
+@pytest.mark.parametrize("n", [16_384, 1_048_576])
+def test_c5_pendulum_parity(oracle, n):
+    print(f"case: C5 forward N={n}", flush=True)
+    th0, om0, ids, A = configs.c5_inputs(n)
+    res = _mapped(configs.c5_config(n))(th0, om0, ids, A)
+    _sync()
+    ref = oracle.c5_fwd(th0, om0, ids, A)
+    _common(res, ref)
+    st = _np(res.outputs["state"])
+    assert st.shape == (n, 2)
+    assert np.array_equal(st.view(np.uint32), ref.tallies["state"].view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [16_384, 1_048_576])
+def test_c5_grad_energy_wrt_amplitude(oracle, n):
+    """reverse-mode replay gradient of sum_i E(final_i) w.r.t. A: the cotangent of the (N, 2) state tally is
+    (sin theta, omega) at the forward's final states."""
+    print(f"case: C5 vjp A N={n}", flush=True)
+    th0, om0, ids, A = configs.c5_inputs(n)
+    f = _mapped(configs.c5_config(n))
+    res, pull = tm.vjp(f, th0, om0, ids, A, argnums=3)
+    ct = configs.c5_energy_ct(_np(res.outputs["state"]))
+    g = float(_np(pull({"state": ct})))
+    want, ntr = oracle.c5_grad(th0, om0, ids, A, ct)
+    assert ntr == 0
+    assert _rel(g, want) <= GTOL, (g, float(want))
