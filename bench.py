@@ -8,10 +8,12 @@ roofline: the dominant kernel's algorithmic HBM bytes per launch (per item: x0 4
 truncation flag 1 B written = 17 B; the gradient launch: 12 B read + 1 B written = 13 B) over its average launch
 duration (HIP events on the launch stream), against MI355X's 8 TB/s.  The path is VALU-bound (threefry, erf_inv in
 double), not HBM-bound: the fraction is reported as measured.  traffic: FETCH_SIZE + WRITE_SIZE per dispatch from
-rocprofv3 counter runs, scaled by the same counters on a copy of known size (profiles/), when given with
---traffic-bytes; else null.
+rocprofv3 counter runs of this bench, scaled by what the same counters read on a plain copy of known size
+(--copy-probe); the recorded measurement at the default N unless --traffic-bytes gives another.
 cpu_baseline: the oracle (the C/OpenMP restatement of the reference's CPU kernel backend) on the host's cores, on a
 bounded sample of the same workload (the first items of the same inputs), forward + gradient, items/s.
+configs: the other BASELINE configs at their own sizes (C1 10,000; C3, C4 4,194,304; C5 1,048,576), forward and
+gradient launches timed the same way, each with the oracle on a bounded sample beside it.
 """
 import argparse
 import json
@@ -27,6 +29,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FWD_BYTES_PER_ITEM = 17
 GRAD_BYTES_PER_ITEM = 13
+# HBM bytes per launch at N = 4,194,304 from rocprofv3 counter passes (profiles/c2_random_walk_traffic.md):
+# 2 x FETCH_SIZE + 1 x WRITE_SIZE (KiB), the factors those counters read on a plain 1 GiB device copy
+MEASURED_TRAFFIC = {"forward": 78_572_136, "gradient": 57_040_424}
 
 
 def cpu_baseline(x0, keys, drift, max_steps, target_s=10.0):
@@ -48,6 +53,110 @@ def cpu_baseline(x0, keys, drift, max_steps, target_s=10.0):
                        f"on {threads} OpenMP threads")
 
 
+def _cfg_runs(name, n, dev_inputs):
+    """(forward launch, gradient launch) closures of config `name` on device inputs: the gradient of each config as
+    BASELINE states it (C1 theta, C3 mu_a, C4 a: of the sum of the float tallies; C5 A: of the summed final energy,
+    whose cotangent (sin theta, omega) comes from the forward's final states)."""
+    import torch
+
+    import tallymap_amd as tm
+    from tallymap_amd import configs
+    cfg = configs.SIZED[name](n) if name in configs.SIZED else configs.CONFIGS[name]
+    f = tm.vmap(cfg["item"], outputs=cfg["outputs"], in_axes=cfg["in_axes"], max_steps=cfg["max_steps"])
+    argn = {"c1": 2, "c3": 1, "c4": 3}
+    if name in argn:
+        g = tm.grad(f, argnums=argn[name])
+        return (lambda: f(*dev_inputs)), (lambda: g(*dev_inputs)), f
+    holder = {}
+
+    def fwd():
+        res, pull = tm.vjp(f, *dev_inputs, argnums=3)
+        st = res.outputs["state"]
+        holder["pull"], holder["ct"] = pull, torch.stack([torch.sin(st[:, 0]), st[:, 1]], 1)
+        return res
+
+    def grad():
+        return holder["pull"]({"state": holder["ct"]})
+    return fwd, grad, f
+
+
+def _cpu_sample(name, inputs, target_s):
+    """the oracle's forward + gradient of config `name` on the first items of `inputs`, grown until the pair takes
+    about target_s / 4 s -> (items/s, n, seconds)."""
+    import oracle as O
+    from tallymap_amd import configs
+    O.build()
+    n = 2048
+    N = len(inputs[0])
+    while True:
+        sl = [x[:n] if np.ndim(x) else x for x in inputs]
+        t0 = time.perf_counter()
+        if name == "c1":
+            O.c1_fwd(*sl, shadow=False)
+            O.c1_grad(*sl, np.ones(16, np.float32))
+        elif name == "c3":
+            O.c3_fwd(*sl, shadow=False, per_item=False)
+            O.c3_grad(*sl, np.ones((64, 64), np.float32))
+        elif name == "c4":
+            ids = np.arange(n, dtype=np.int32)
+            O.c4_fwd(sl[0], sl[1], ids, sl[3], shadow=False, per_item=False)
+            O.c4_grad(sl[0], sl[1], ids, sl[3], np.ones((256, 256), np.float32), np.ones((n, 1), np.float32))
+        else:
+            ids = np.arange(n, dtype=np.int32)
+            r = O.c5_fwd(sl[0], sl[1], ids, sl[3], shadow=False, per_item=False)
+            O.c5_grad(sl[0], sl[1], ids, sl[3], configs.c5_energy_ct(r.tallies["state"]))
+        dt = time.perf_counter() - t0
+        if dt * 4 > target_s or n >= N:
+            return n / dt, n, dt
+        n = min(N, max(n * 2, int(n * target_s / max(dt, 1e-3) / 4)))
+
+
+def bench_configs(steps, warmup, with_cpu):
+    """items/s of configs 1, 3, 4, 5 at their BASELINE sizes, forward and gradient launches timed with HIP events
+    on torch's current stream; the oracle on a bounded sample beside each."""
+    import torch
+
+    from tallymap_amd import configs
+    out = {}
+    sizes = {"c1": 10_000, "c3": 4_194_304, "c4": 4_194_304, "c5": 1_048_576}
+    for name, n in sizes.items():
+        inputs = getattr(configs, f"{name}_inputs")(n)
+        dev = [torch.from_numpy(np.ascontiguousarray(x)).cuda() if np.ndim(x) else torch.tensor(x).cuda()
+               for x in inputs]
+        fwd, grad, f = _cfg_runs(name, n, dev)
+        for _ in range(warmup):
+            fwd()
+            grad()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        t0 = time.perf_counter()
+        for e in evs:
+            e[0].record(stream)
+            r = fwd()
+            e[1].record(stream)
+            grad()
+            e[2].record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+        fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+        grad_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+        assert int(r.stats["n_truncated"].item()) == 0
+        d = {"n_items": n, "max_steps": (configs.SIZED[name](n) if name in configs.SIZED
+                                         else configs.CONFIGS[name])["max_steps"],
+             "items_per_s": n / wall, "fwd_ms": fwd_ms, "grad_ms": grad_ms,
+             "fwd_items_per_s": n / (fwd_ms * 1e-3), "grad_items_per_s": n / (grad_ms * 1e-3),
+             "mean_trip_count": float(r.per_item.double().mean().item()),
+             "max_trip_count": int(r.per_item.max().item())}
+        if with_cpu:
+            v, m, dt = _cpu_sample(name, inputs, 8.0)
+            d["cpu_items_per_s"] = v
+            d["cpu_sample"] = f"first {m} items, forward + gradient, {dt:.2f} s"
+        out[name] = d
+        print(f"bench: {name} done ({wall * 1e3:.1f} ms per fwd+grad step)", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -55,8 +164,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4_194_304)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--headline-only", action="store_true", help="skip the configs 1, 3, 4, 5 section")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="run one plain device copy of BYTES first (its FETCH_SIZE / WRITE_SIZE under rocprofv3 "
+                         "calibrate the traffic counters)")
     ap.add_argument("--traffic-bytes", type=float, default=None,
-                    help="HBM bytes per dominant-kernel launch measured with rocprofv3 (profiles/)")
+                    help="HBM bytes per dominant-kernel launch (default: the rocprofv3 measurement of this kernel at "
+                         "the default N, null at other N)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}): items shard contiguously over "
@@ -67,6 +181,13 @@ def main():
     import tallymap_amd as tm
     from tallymap_amd import backend as B
     from tallymap_amd import configs
+    if a.copy_probe:
+        src = torch.ones(a.copy_probe // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cfg = configs.C2
     x0, keys, drift = configs.c2_inputs(a.n)
     dev = [torch.from_numpy(x0).cuda(), torch.from_numpy(keys).cuda(), torch.tensor(drift).cuda()]
@@ -130,11 +251,15 @@ def main():
         "mean_trip_count": float(r.per_item.double().mean().item()),
         "kernel": {"name": "tm_main (" + dom + ")", **info},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": a.traffic_bytes,
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": a.traffic_bytes if a.traffic_bytes is not None
+                     else (MEASURED_TRAFFIC[dom] if N == 4_194_304 else None),
                      "algorithmic_bytes_per_launch": bpi * N},
     }
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(x0, keys, drift, cfg["max_steps"])
+    if not a.headline_only:
+        out["configs"] = bench_configs(max(3, a.steps // 4), 1, not a.no_cpu)
     print(json.dumps(out))
 
 

@@ -195,8 +195,12 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
     import torch
 
     from . import reverse as R
-    adj = R.adjoint_program(prog, wrt)
-    pl = R.plan(adj)
+    key = (prog.digest(), tuple(tuple(w) for w in wrt))
+    hit = _ADJ.get(key)
+    if hit is None:
+        adj = R.adjoint_program(prog, wrt)
+        hit = _ADJ[key] = (adj, R.plan(adj))
+    adj, pl = hit
     yav = prog.y_avals()
     ins_p = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
     for j in pl.fy:
@@ -239,3 +243,4 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
 
 
 _FWD_ONLY = {}
+_ADJ = {}                   # (program digest, wrt) -> (reverse.Adjoint, reverse.Plan)

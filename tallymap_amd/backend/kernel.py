@@ -352,7 +352,10 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK):
 
     # tm_main
     body = []
-    body.append(f"extern \"C\" __global__ void __launch_bounds__({block}) tm_main(const TmParams P, "
+    # the gradient launch of a forward-only adjoint is named tm_adjoint like the checkpointed one (profiles tell the
+    # forward and gradient launches apart by name; the launcher accepts either entry)
+    entry = "tm_adjoint" if getattr(prog, "poison_ys", False) else "tm_main"
+    body.append(f"extern \"C\" __global__ void __launch_bounds__({block}) {entry}(const TmParams P, "
                 "const i64 n_items) {")
     body.append("  u64* const tm_ctr = (u64*)P.p[%d];" % r_ctl)
     for k in priv:

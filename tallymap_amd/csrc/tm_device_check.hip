@@ -18,6 +18,6 @@ extern "C" __global__ void tm_device_check(float* f, u64* x, u32* u, u64* ctr, i
   const u64 base = tm_claim(ctr, (u32)__builtin_popcountll(tm_ballot(v > 0.0f)));
   bool bad = false;
   if (i < n) f[16 + i] = tm_xread(x, &bad) + (float)base + sh[threadIdx.x & 63] + (float)tm_rank(tm_ballot(true))
-                         + (float)tm_idiv(i, n) + (float)tm_f2i32(v) + (float)tm_log((double)v)
+                         + (float)tm_idiv(i, n) + (float)tm_f2i32(v) + (float)tm_log_erfinv((double)v + 1.5)
                          + tm_logf(v) + tm_expf(v) + tm_sinf(v) + tm_cosf(v) + tm_atan2f(v, sh[o0 & 63u]);
 }

@@ -1,7 +1,10 @@
 // Host checks of tallymap_amd/csrc/tm_libm.h against glibc (test infrastructure).
 //   libm_check erfinv_normal   every f32 argument jax.random.normal passes to erf_inv (2^23 uniform values):
 //                              tm_erfinvf vs the reference CPU target's formula with glibc log / sqrt
-//   libm_check log <n> <seed>  n random positive doubles: tm_log vs glibc log (ulp histogram)
+//   libm_check erfinv_all <stride>
+//                              every stride-th f32 in (-1, 1) (stride 1: all 2,130,706,430, OpenMP): tm_erfinvf vs
+//                              the reference formula, bitwise
+//   libm_check log <n> <seed>  n random t in [2^-24, 1]: |tm_log_erfinv(t) - glibc log(t)| / max(1, |log t|)
 //   libm_check f32 <fn> <stride> <offset>
 //                              logf / expf / sinf / cosf / atanf on every stride-th f32 bit pattern from offset
 //                              (stride 1: all 2^32): bitwise mismatches and the largest ulp distance
@@ -40,25 +43,41 @@ int main(int argc, char** argv) {
       const float u = tm_fmax(lo, s);
       const float a = tm_erfinvf(u), b = ref_erfinvf(u);
       const double ad = fabs((double)u);
-      if (tm_log((1.0 - ad) * (1.0 + ad)) != log((1.0 - ad) * (1.0 + ad))) ++logdiff;
+      if (tm_log_erfinv((1.0 - ad) * (1.0 + ad)) != log((1.0 - ad) * (1.0 + ad))) ++logdiff;
       ++n;
       if (tm_f2u(a) != tm_f2u(b)) { if (++bad < 10) printf("  u=%a tm=%a ref=%a\n", u, a, b); }
     }
     printf("erfinv_normal: %ld arguments, %ld f32 mismatches (double log differs on %ld)\n", n, bad, logdiff);
     return bad != 0;
   }
+  if (argc > 2 && !strcmp(argv[1], "erfinv_all")) {
+    const int64_t stride = atoll(argv[2]);
+    long n = 0, bad = 0;
+#pragma omp parallel for reduction(+ : n, bad) schedule(dynamic, 64)
+    for (int64_t blk = 0; blk < 0x3f800000ll; blk += 1 << 16) {
+      for (int64_t b = blk; b < blk + (1 << 16) && b < 0x3f800000ll; b += stride) {
+        for (int s = 0; s < 2; ++s) {
+          const float y = tm_u2f((uint32_t)b | (s ? 0x80000000u : 0u));
+          ++n;
+          if (tm_f2u(tm_erfinvf(y)) != tm_f2u(ref_erfinvf(y))) ++bad;
+        }
+      }
+    }
+    printf("erfinv_all: %ld arguments, %ld f32 mismatches\n", n, bad);
+    return bad != 0;
+  }
   if (argc > 3 && !strcmp(argv[1], "log")) {
     long n = atol(argv[2]);
     srand48(atol(argv[3]));
-    long diff = 0, big = 0;
+    double worst = 0.0;
     for (long i = 0; i < n; ++i) {
-      uint64_t b = ((uint64_t)(mrand48() & 0x7fefffff) << 32) | (uint32_t)mrand48();
-      double x = tm_u2d(b);
-      double a = tm_log(x), r = log(x);
-      if (a != r) { ++diff; int64_t d = (int64_t)tm_d2u(a) - (int64_t)tm_d2u(r); if (d > 1 || d < -1) ++big; }
+      const double x = 0x1p-24 + (1.0 - 0x1p-24) * drand48();
+      const double r = log(x);
+      const double e = fabs(tm_log_erfinv(x) - r) / (fabs(r) > 1.0 ? fabs(r) : 1.0);
+      if (e > worst) worst = e;
     }
-    printf("log: %ld random doubles, %ld differ from glibc, %ld by more than 1 ulp\n", n, diff, big);
-    return big != 0;
+    printf("log: %ld t in [2^-24, 1], max |error| / max(1, |log t|) = %a\n", n, worst);
+    return worst > 0x1p-51;
   }
   if (argc > 4 && !strcmp(argv[1], "f32")) {
     float (*mine)(float) = nullptr;
@@ -100,6 +119,6 @@ int main(int argc, char** argv) {
     printf("atan2: %ld pairs, %ld mismatches, max %ld ulp\n", n, bad, maxulp);
     return 0;
   }
-  fprintf(stderr, "usage: libm_check erfinv_normal | log <n> <seed> | f32 <fn> <stride> <offset> | atan2 <n> <seed>\n");
+  fprintf(stderr, "usage: libm_check erfinv_normal | erfinv_all <stride> | log <n> <seed> | f32 <fn> <stride> <offset> | atan2 <n> <seed>\n");
   return 2;
 }
