@@ -22,7 +22,7 @@ STATS = ("spawned", "children_dropped", "children_truncated", "fixed_point_overf
 ST = {n: i for i, n in enumerate(STATS)}
 MAX_ITEMS = 2 ** 31 - 1
 PROG_CACHE = 64
-OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill")
+OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact")
 
 
 class UnsupportedError(NotImplementedError):
@@ -306,7 +306,8 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
                every float tally of the call NaN
     backend:   'auto' / 'hip' (the HIP kernel backend; it never falls back)
     opts:      schedule 'step' (default: a lane refills at loop-step granularity) | 'item'; block (threads per
-               block, default 256); refill (idle lanes a wave waits for before it claims, default 1);
+               block, default 256); refill (idle lanes a wave waits for before it claims, default 1); compact
+               (iterations between the tail-phase repacks of a workgroup's live items, default 16; 0: off);
                rev_checkpoints (reverse mode, C states per checkpoint buffer); cuda_math and min_blocks_per_sm
                are accepted for drop-in compatibility and have no meaning on ROCm.
     """

@@ -30,7 +30,8 @@ from .codegen import Emitter, Val, VTally, assign_carries, ctype, lit
 BLOCK = 256
 LDS_BYTES = 32768          # privatised tallies per block (MI355X: 160 KB LDS per CU)
 XW = 5                     # int64 words per exact bin
-CHUNK = 64                 # items per wave claim
+CHUNK = 64
+COMPACT = 16               # iterations between the tail-phase repacks of a workgroup's live items                 # items per wave claim
 BCAST_REG = 16             # broadcast operands up to this many elements are loaded into registers
 
 
@@ -86,10 +87,48 @@ def exact_words(S):
     return 2 * XW * S + (S + 31) // 32
 
 
-def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK):
+_W64 = {"i64", "u64", "double"}
+
+
+def _repack_code(decls, cap):
+    """(pack lines, unpack lines, words per item) moving one item's loop state -- the declared carries and
+    persistent values, and tm_item -- through the LDS pool tm_pool (column w of word w, row q)."""
+    fields = []
+    for d in decls:
+        ct, nm = d.strip().rstrip(";").split()
+        fields.append((ct, nm))
+    fields.append(("i64", "tm_item"))
+    pack, unpack = [], []
+    w = 0
+    for ct, nm in fields:
+        if ct in _W64:
+            pack.append(f"{{ const u64 b = __builtin_bit_cast(u64, {nm}); tm_pool[{w * cap}u + q] = (u32)b; "
+                        f"tm_pool[{(w + 1) * cap}u + q] = (u32)(b >> 32); }}")
+            unpack.append(f"{nm} = __builtin_bit_cast({ct}, (u64)tm_pool[{w * cap}u + q] | "
+                          f"((u64)tm_pool[{(w + 1) * cap}u + q] << 32));")
+            w += 2
+        elif ct == "bool":
+            pack.append(f"tm_pool[{w * cap}u + q] = (u32){nm};")
+            unpack.append(f"{nm} = tm_pool[{w * cap}u + q] != 0u;")
+            w += 1
+        elif ct in ("float", "u32", "i32"):
+            pack.append(f"tm_pool[{w * cap}u + q] = __builtin_bit_cast(u32, {nm});")
+            unpack.append(f"{nm} = __builtin_bit_cast({ct}, tm_pool[{w * cap}u + q]);")
+            w += 1
+        else:                                      # 8- and 16-bit integers
+            pack.append(f"tm_pool[{w * cap}u + q] = (u32){nm};")
+            unpack.append(f"{nm} = ({ct})tm_pool[{w * cap}u + q];")
+            w += 1
+    return pack, unpack, w
+
+
+def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COMPACT):
     """-> (HIP source, Layout) of prog's module.  chunk: items a wave claims with one atomic (their per-item operands
-    are staged in LDS by one coalesced load, and idle lanes take them from there at step granularity)."""
+    are staged in LDS by one coalesced load, and idle lanes take them from there at step granularity).  compact:
+    once every wave of a workgroup has drained the item queue, the waves meet every `compact` iterations and
+    repack their live items densely onto the first waves (0: off; step schedule only)."""
     chunk = max(1, int(chunk))
+    compact = max(0, int(compact))
     jx = prog.jaxpr
     nT, nP, nB = prog.nT, prog.nP, prog.nB
     pav, bav = prog.p_avals(), prog.b_avals()
@@ -389,6 +428,16 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK):
     body.append("  i32 tm_drop = 0;")
     body.append("  u32 tm_ntr = 0;")
     body += decls
+    compact_on = bool(compact) and mode == "step"
+    if compact_on:
+        pack, unpack, nwords = _repack_code(decls, wpb * 64)
+        body.append(f"  __shared__ u32 tm_pool[{nwords * wpb * 64}];   // the repack pool, one column per word")
+        body.append("  __shared__ u32 tm_pn[2];                 // pool counts, alternating between rounds")
+        body.append("  __shared__ u32 tm_ndr;                   // waves of this workgroup whose queue is drained")
+        body.append("  if (threadIdx.x == 0) { tm_pn[0] = 0u; tm_pn[1] = 0u; tm_ndr = 0u; }")
+        body.append("  __syncthreads();")
+        body.append("  bool tm_dr = false, tm_bm = false;         // drained (counted), repack mode")
+        body.append("  u32 tm_it = 0, tm_round = 0;")
     body.append("  while (true) {")
     body.append("    if (tm_more) {")
     body.append("      const u64 tm_need = tm_ballot(!tm_live);")
@@ -442,7 +491,55 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK):
     body.append("    if (tm_live) {")
     body += step_lines
     body.append("    }")
-    body.append("    if (tm_ballot(tm_live || tm_more) == 0ull) break;")
+    if not compact_on:
+        body.append("    if (tm_ballot(tm_live || tm_more) == 0ull) break;")
+    else:
+        # Tail phase.  Every wave counts itself once when its queue is drained; when all are, the workgroup's waves
+        # repack every `compact` iterations (a wave without live lanes goes straight to the next round and waits at
+        # its barrier).  A round: live lanes write their item's loop state to the pool, barrier, every wave reads
+        # the count P (the same for all), P == 0 ends the loop for the whole workgroup, else wave w takes pool items
+        # 64 w .. 64 w + 63, barrier.  The two counters alternate: round r counts into tm_pn[r & 1] and clears the
+        # other, whose last readers finished before this round's first barrier.  Every wave runs the same number of
+        # rounds, and the loop has no other exit.
+        body.append("    if (!tm_more && !tm_dr) {")
+        body.append("      tm_dr = true;")
+        body.append("      if (tm_lane() == 0u) atomicAdd(&tm_ndr, 1u);")
+        body.append("    }")
+        body.append("    if (tm_dr && !tm_bm) {")
+        body.append(f"      if (__builtin_amdgcn_readfirstlane(__atomic_load_n(&tm_ndr, __ATOMIC_RELAXED)) == {wpb}u) {{")
+        body.append("        tm_bm = true;")
+        body.append("        tm_it = 0u;")
+        body.append("      }")
+        body.append("    }")
+        body.append("    if (tm_bm) {")
+        body.append("      if (tm_it == 0u || tm_ballot(tm_live) == 0ull) {")
+        body.append("        u32* const tm_cnt = &tm_pn[tm_round & 1u];")
+        body.append("        const u64 tm_lm = tm_ballot(tm_live);")
+        body.append("        u32 tm_pb = 0u;")
+        body.append("        if (tm_lane() == 0u) tm_pb = atomicAdd(tm_cnt, (u32)__builtin_popcountll(tm_lm));")
+        body.append("        tm_pb = __builtin_amdgcn_readfirstlane(tm_pb);")
+        body.append("        if (tm_live) {")
+        body.append("          const u32 q = tm_pb + (u32)tm_rank(tm_lm);")
+        body += ["          " + ln for ln in pack]
+        body.append("          tm_live = false;")
+        body.append("        }")
+        body.append("        __syncthreads();")
+        body.append("        const u32 tm_P = __builtin_amdgcn_readfirstlane(*tm_cnt);")
+        body.append("        if (tm_P == 0u) break;")
+        body.append("        if (threadIdx.x == 0) tm_pn[(tm_round + 1u) & 1u] = 0u;")
+        body.append("        {")
+        body.append("          const u32 q = threadIdx.x;")
+        body.append("          if (q < tm_P) {")
+        body += ["            " + ln for ln in unpack]
+        body.append("            tm_live = true;")
+        body.append("          }")
+        body.append("        }")
+        body.append("        __syncthreads();")
+        body.append("        ++tm_round;")
+        body.append(f"        tm_it = {compact}u;")
+        body.append("      }")
+        body.append("      --tm_it;")
+        body.append("    }")
     body.append("  }")
     body.append("  if (tm_drop) atomicAdd(&TM_STATS[4], tm_drop);")
     body.append("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")
