@@ -52,8 +52,12 @@ def lib():
         L.tmref_c2_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p]
         L.tmref_c2_grad.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
         L.tmref_c2_x0.argtypes = [_p, _i64, _p]
-        L.tmref_c3_fwd.argtypes = [_p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
-        L.tmref_c3_grad.argtypes = [_p, _f, _i64, _i, _i, _p, _p, _p]
+        _d = ctypes.c_double
+        L.tmref_c3_fwd.argtypes = [_p, _f, _d, _d, _i64, _i, _i, _p, _p, _p, _p, _p]
+        L.tmref_c3_grad.argtypes = [_p, _f, _d, _d, _i64, _i, _i, _p, _p, _p]
+        L.tmref_hg_cost.argtypes = [_p, _i64, _f, _p]
+        L.tmref_hg_rotate.argtypes = [_p, _p, _p, _i64]
+        L.tmref_c5_tableau.argtypes = [_p]
         L.tmref_c4_fwd.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p]
         L.tmref_c4_grad.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
         L.tmref_c5_fwd.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
@@ -197,24 +201,25 @@ def _per_item(n, per_item):
     return (np.zeros(n, np.int32), np.zeros(n, np.uint8)) if per_item else (None, None)
 
 
-def c3_fwd(keys, mu_a, max_steps=1024, nthreads=0, shadow=True, per_item=True):
+def c3_fwd(keys, mu_a, max_steps=1024, nthreads=0, shadow=True, per_item=True, mu_s=0.9, g=0.8):
+    """config 3 forward; mu_s and g are the config's (other values: the special cases the tests pin)."""
     keys = _c(keys, np.uint32)
     n = keys.shape[0]
     ab = np.zeros(64 * 64, np.float32)
     a64 = np.zeros(64 * 64, np.float64) if shadow else None
     ks, tr = _per_item(n, per_item)
     st = np.zeros(5, np.int32)
-    lib().tmref_c3_fwd(_ptr(keys), float(np.float32(mu_a)), n, max_steps, nthreads, _ptr(ab), _ptr(a64), _ptr(ks),
-                       _ptr(tr), _ptr(st))
+    lib().tmref_c3_fwd(_ptr(keys), float(np.float32(mu_a)), float(mu_s), float(g), n, max_steps, nthreads, _ptr(ab),
+                       _ptr(a64), _ptr(ks), _ptr(tr), _ptr(st))
     return Fwd({"absorbed": ab.reshape(64, 64)}, {"absorbed": a64.reshape(64, 64) if shadow else None}, ks,
                tr.astype(bool) if tr is not None else None, st)
 
 
-def c3_grad(keys, mu_a, ct, max_steps=1024, nthreads=0):
+def c3_grad(keys, mu_a, ct, max_steps=1024, nthreads=0, mu_s=0.9, g=0.8):
     keys, ct = _c(keys, np.uint32), _c(ct, np.float32)
     out, ntr = np.zeros(1, np.float32), np.zeros(1, np.int32)
-    lib().tmref_c3_grad(_ptr(keys), float(np.float32(mu_a)), keys.shape[0], max_steps, nthreads, _ptr(ct), _ptr(out),
-                        _ptr(ntr))
+    lib().tmref_c3_grad(_ptr(keys), float(np.float32(mu_a)), float(mu_s), float(g), keys.shape[0], max_steps,
+                        nthreads, _ptr(ct), _ptr(out), _ptr(ntr))
     return out[0], int(ntr[0])
 
 
@@ -262,3 +267,26 @@ def c5_grad(th0, om0, ids, A, ct, max_steps=20_000, nthreads=0):
     lib().tmref_c5_grad(_ptr(th0), _ptr(om0), _ptr(ids), float(np.float32(A)), th0.shape[0], max_steps, nthreads,
                         _ptr(ct), _ptr(out), _ptr(ntr))
     return out[0], int(ntr[0])
+
+
+def hg_cost(u, g):
+    """the Henyey-Greenstein deflection cosines c3's item draws from uniforms u (f32)."""
+    u = _c(u, np.float32)
+    out = np.zeros_like(u)
+    lib().tmref_hg_cost(_ptr(u), u.size, float(np.float32(g)), _ptr(out))
+    return out
+
+
+def hg_rotate(d, cost, phi):
+    """c3's direction update of unit directions d (n, 3) by deflection cosines and azimuths (f32)."""
+    d = np.array(d, np.float32, order="C")
+    cost, phi = _c(cost, np.float32), _c(phi, np.float32)
+    lib().tmref_hg_rotate(_ptr(d), _ptr(cost), _ptr(phi), cost.size)
+    return d
+
+
+def c5_tableau():
+    """the f32 Dormand-Prince tableau c5's item uses: (c[4], A rows 2-6 [15], b [5], e [6])."""
+    out = np.zeros(30, np.float32)
+    lib().tmref_c5_tableau(_ptr(out))
+    return out[:4], out[4:19], out[19:24], out[24:]

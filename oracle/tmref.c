@@ -576,16 +576,46 @@ typedef struct { i32 k; u32 trunc; double g; } gres;
  * float constants rounded to f32 where they meet f32 values, as JAX's weak types do).  Forward-mode tangent
  * w.r.t. mu_a: only the weight w carries one (positions reach integer bins and comparisons only). */
 #define C3_NB 64
-static gres c3_item(const u32* keys, float mu_a, i64 i, int M, tm_thr* t, const float* ct) {
+/* Henyey-Greenstein deflection cosine for uniform u (MCML's inverse-CDF form), in the item's f32 operation order;
+ * g1 = 1 - g^2, g2 = 1 - g, g3 = 2 g, g4 = 1 + g^2 as f32 */
+static inline float hg_cost(float u, float g1, float g2, float g3, float g4) {
+  const float tmp = g1 / (g2 + g3 * u);
+  return (g4 - tmp * tmp) / g3;
+}
+/* rotate the unit direction d by polar cosine cost and azimuth (cp, sp) = (cos phi, sin phi) (MCML's update; the
+ * near-vertical case |uz| > 0.99999 uses the fixed frame) */
+static inline void hg_rotate(float* d, float cost, float cp, float sp) {
+  const float sint = sqrtf(lax_fmax(0.0f, 1.0f - cost * cost));
+  const float ux = d[0], uy = d[1], uz = d[2];
+  const float temp = sqrtf(lax_fmax(0.0f, 1.0f - uz * uz));
+  const int near = fabsf(uz) > 0.99999f;
+  const float den = near ? 1.0f : temp;
+  const float nx = near ? sint * cp : sint * (ux * uz * cp - uy * sp) / den + ux * cost;
+  const float ny = near ? sint * sp : sint * (uy * uz * cp + ux * sp) / den + uy * cost;
+  const float nz = near ? lax_fsign(uz) * cost : -sint * cp * temp + uz * cost;
+  d[0] = nx;
+  d[1] = ny;
+  d[2] = nz;
+}
+void tmref_hg_cost(const float* u, i64 n, float g, float* out) {
+  const double gd = (double)g;
+  const float g1 = (float)(1.0 - gd * gd), g2 = (float)(1.0 - gd), g3 = (float)(2.0 * gd), g4 = (float)(1.0 + gd * gd);
+  for (i64 i = 0; i < n; ++i) out[i] = hg_cost(u[i], g1, g2, g3, g4);
+}
+void tmref_hg_rotate(float* d3n, const float* cost, const float* phi, i64 n) {
+  for (i64 i = 0; i < n; ++i) hg_rotate(d3n + 3 * i, cost[i], cosf(phi[i]), sinf(phi[i]));
+}
+
+/* mu_s and g are the config's 0.9 and 0.8 (passed as the Python floats the item uses, in double) */
+static gres c3_item(const u32* keys, float mu_a, double mu_s_d, double g, i64 i, int M, tm_thr* t, const float* ct) {
   const u32* key = keys + 2 * i;
-  const float mu_s = (float)0.9, mu_t = mu_a + mu_s, frac = mu_a / mu_t, albedo = mu_s / mu_t;
+  const float mu_s = (float)mu_s_d, mu_t = mu_a + mu_s, frac = mu_a / mu_t, albedo = mu_s / mu_t;
   const double dfrac = ((double)mu_t - (double)mu_a) / ((double)mu_t * (double)mu_t);
   const double dalb = -(double)mu_s / ((double)mu_t * (double)mu_t);
-  const float G1 = (float)(1.0 - 0.8 * 0.8), G2 = (float)(1.0 - 0.8), G3 = (float)(2.0 * 0.8),
-              G4 = (float)(1.0 + 0.8 * 0.8), TWO_PI = (float)(2.0 * 3.141592653589793),
-              ZS = (float)(64 / 5.0), DEPTH = 5.0f;
+  const float G1 = (float)(1.0 - g * g), G2 = (float)(1.0 - g), G3 = (float)(2.0 * g), G4 = (float)(1.0 + g * g),
+              TWO_PI = (float)(2.0 * 3.141592653589793), ZS = (float)(64 / 5.0), DEPTH = 5.0f;
   float p[3] = {0.0f, 0.0f, 0.0f}, d[3] = {0.0f, 0.0f, 1.0f}, w = 1.0f;
-  double dw = 0.0, g = 0.0;
+  double dw = 0.0, gacc = 0.0;
   i32 k = 0, cap = 0;
   while (cap < M && w > 0.0f) {
     u32 fk[2];
@@ -600,24 +630,12 @@ static gres c3_item(const u32* keys, float mu_a, i64 i, int M, tm_thr* t, const 
     const int ok = (u32)iz < (u32)C3_NB && (u32)ir < (u32)C3_NB;
     const i64 idx = ok ? (i64)iz * C3_NB + ir : -1;
     if (t) emit(t, 0, idx, w * frac);
-    if (ct && ok) g += (double)ct[idx] * (dw * (double)frac + (double)w * dfrac);
+    if (ct && ok) gacc += (double)ct[idx] * (dw * (double)frac + (double)w * dfrac);
     dw = dw * (double)albedo + (double)w * dalb;
     w = w * albedo;
-    const float tmp = G1 / (G2 + G3 * u[1]);
-    const float cost = (G4 - tmp * tmp) / G3;
-    const float sint = sqrtf(lax_fmax(0.0f, 1.0f - cost * cost));
+    const float cost = hg_cost(u[1], G1, G2, G3, G4);
     const float phi = TWO_PI * u[2];
-    const float cp = cosf(phi), sp = sinf(phi);
-    const float ux = d[0], uy = d[1], uz = d[2];
-    const float temp = sqrtf(lax_fmax(0.0f, 1.0f - uz * uz));
-    const int near = fabsf(uz) > 0.99999f;
-    const float den = near ? 1.0f : temp;
-    const float nx = near ? sint * cp : sint * (ux * uz * cp - uy * sp) / den + ux * cost;
-    const float ny = near ? sint * sp : sint * (uy * uz * cp + ux * sp) / den + uy * cost;
-    const float nz = near ? lax_fsign(uz) * cost : -sint * cp * temp + uz * cost;
-    d[0] = nx;
-    d[1] = ny;
-    d[2] = nz;
+    hg_rotate(d, cost, cosf(phi), sinf(phi));
     if (w < 0.01f) {
       if (u[3] < 0.1f) { w = w * 10.0f; dw = dw * 10.0; }
       else { w = 0.0f; dw = 0.0; }
@@ -626,22 +644,22 @@ static gres c3_item(const u32* keys, float mu_a, i64 i, int M, tm_thr* t, const 
     k = k + 1;
     ++cap;
   }
-  gres res = {k, (u32)(cap >= M && w > 0.0f), g};
+  gres res = {k, (u32)(cap >= M && w > 0.0f), gacc};
   return res;
 }
 
-int tmref_c3_fwd(const u32* keys, float mu_a, i64 n, int M, int nthreads, float* absorbed, double* absorbed64,
-                 i32* ks, uint8_t* trunc, i32* stats) {
+int tmref_c3_fwd(const u32* keys, float mu_a, double mu_s, double g, i64 n, int M, int nthreads, float* absorbed,
+                 double* absorbed64, i32* ks, uint8_t* trunc, i32* stats) {
   const i64 sz[1] = {C3_NB * C3_NB};
   float* outs[1] = {absorbed};
   double* sh[1] = {absorbed64};
   tm_tallies T = {1, sz, outs, absorbed64 ? sh : NULL, C3_NB * C3_NB * 4 <= PRIV_BYTES};
-  FWD_RUN(c3_item(keys, mu_a, i, M, &t, NULL))
+  FWD_RUN(c3_item(keys, mu_a, mu_s, g, i, M, &t, NULL))
 }
 
-int tmref_c3_grad(const u32* keys, float mu_a, i64 n, int M, int nthreads, const float* ct, float* out,
-                  i32* ntrunc) {
-  GRAD_RUN(c3_item(keys, mu_a, i, M, NULL, ct))
+int tmref_c3_grad(const u32* keys, float mu_a, double mu_s, double g, i64 n, int M, int nthreads, const float* ct,
+                  float* out, i32* ntrunc) {
+  GRAD_RUN(c3_item(keys, mu_a, mu_s, g, i, M, NULL, ct))
 }
 
 /* --------------------------------------------------------------------- C4: walk on spheres, unit disk */
@@ -701,6 +719,15 @@ int tmref_c4_grad(const float* p0, const u32* keys, const i32* ids, float a, i64
  * stop_gradient-ed and the acceptance test is discrete). */
 typedef struct { float y0, y1; double d0, d1; } dual2;
 
+/* Dormand & Prince (1980) RK5(4)7M as the item writes it (Python floats): c2..c5; a21; a31 a32; a41..a43;
+ * a51..a54; a61..a65; b1 b3 b4 b5 b6 (b2 = 0, b7 = 0); e1 e3 e4 e5 e6 e7 (the 5th minus the 4th order weights) */
+static const double C5_TAB[30] = {1.0 / 5, 3.0 / 10, 4.0 / 5, 8.0 / 9,
+                                  1.0 / 5, 3.0 / 40, 9.0 / 40, 44.0 / 45, -56.0 / 15, 32.0 / 9, 19372.0 / 6561,
+                                  -25360.0 / 2187, 64448.0 / 6561, -212.0 / 729, 9017.0 / 3168, -355.0 / 33,
+                                  46732.0 / 5247, 49.0 / 176, -5103.0 / 18656,
+                                  35.0 / 384, 500.0 / 1113, 125.0 / 192, -2187.0 / 6784, 11.0 / 84,
+                                  71.0 / 57600, -71.0 / 16695, 71.0 / 1920, -17253.0 / 339200, 22.0 / 525, -1.0 / 40};
+
 static inline dual2 c5_rhs(float tt, dual2 y, float A) {
   const float DAMP = (float)-0.1, WD = (float)(2.0 / 3.0);
   const float c = cosf(WD * tt);
@@ -729,18 +756,16 @@ static inline dual2 c5_comb(dual2 y, float h, int m, const float* c, const dual2
 static gres c5_item(const float* th0, const float* om0, const i32* ids, float A, i64 n, i64 i, int M, tm_thr* t,
                     const float* ct) {
   const float T1 = 50.0f, RTOL = (float)1e-6, ATOL = (float)1e-8;
-  const float C2 = (float)(1.0 / 5), C3 = (float)(3.0 / 10), C4 = (float)(4.0 / 5), C5 = (float)(8.0 / 9);
-  const float A2[1] = {(float)(1.0 / 5)};
-  const float A3[2] = {(float)(3.0 / 40), (float)(9.0 / 40)};
-  const float A4[3] = {(float)(44.0 / 45), (float)(-56.0 / 15), (float)(32.0 / 9)};
-  const float A5[4] = {(float)(19372.0 / 6561), (float)(-25360.0 / 2187), (float)(64448.0 / 6561),
-                       (float)(-212.0 / 729)};
-  const float A6[5] = {(float)(9017.0 / 3168), (float)(-355.0 / 33), (float)(46732.0 / 5247), (float)(49.0 / 176),
-                       (float)(-5103.0 / 18656)};
-  const float B[5] = {(float)(35.0 / 384), (float)(500.0 / 1113), (float)(125.0 / 192), (float)(-2187.0 / 6784),
-                      (float)(11.0 / 84)};
-  const float E[6] = {(float)(71.0 / 57600), (float)(-71.0 / 16695), (float)(71.0 / 1920),
-                      (float)(-17253.0 / 339200), (float)(22.0 / 525), (float)(-1.0 / 40)};
+  float TB[30];
+  for (int j = 0; j < 30; ++j) TB[j] = (float)C5_TAB[j];
+  const float C2 = TB[0], C3 = TB[1], C4 = TB[2], C5 = TB[3];
+  const float* A2 = TB + 4;
+  const float* A3 = TB + 5;
+  const float* A4 = TB + 7;
+  const float* A5 = TB + 10;
+  const float* A6 = TB + 14;
+  const float* B = TB + 19;
+  const float* E = TB + 24;
   const float DAMP = (float)-0.1;
   dual2 y = {th0[i], om0[i], 0.0, 0.0};
   dual2 f0 = {y.y1, DAMP * y.y1 - sinf(y.y0) + A, 0.0, 1.0};
@@ -791,6 +816,11 @@ static gres c5_item(const float* th0, const float* om0, const i32* ids, float A,
   if (ct && in) g = (double)ct[2 * (i64)id] * y.d0 + (double)ct[2 * (i64)id + 1] * y.d1;
   gres res = {k, (u32)(cap >= M && tt < T1), g};
   return res;
+}
+
+/* the f32 tableau c5_item uses: c2..c5, A rows 2-6 (15), b (5: stages 1, 3-6), e (6: stages 1, 3-7) */
+void tmref_c5_tableau(float* out) {
+  for (int i = 0; i < 30; ++i) out[i] = (float)C5_TAB[i];
 }
 
 int tmref_c5_fwd(const float* th0, const float* om0, const i32* ids, float A, i64 n, int M, int nthreads,

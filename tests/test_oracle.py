@@ -182,3 +182,147 @@ def test_c1_per_item_tangent_pathwise(oracle):
             x = f32(x * f)
             k += 1
         assert abs(float(dx[i]) - want) <= 1e-5 * max(1.0, abs(want)), (i, dx[i], want)
+
+
+# ------------------------------------------------------------------------------------------- C3 pins
+def test_c3_no_scattering_is_beer_lambert(oracle):
+    """mu_s = 0: a photon deposits its whole weight once, at its first interaction depth z ~ Exp(mu_a) on the axis
+    (radius bin 0), or escapes past z = 5.  The depth histogram follows Beer-Lambert, P(bin j) = exp(-mu_a z_j) -
+    exp(-mu_a z_(j+1)), z_j = 5 j / 64, within 5 binomial standard deviations per bin; and the pathwise gradient
+    w.r.t. mu_a is exactly 0 (the deposit w mu_a / mu_t is 1)."""
+    from tallymap_amd import random as R
+    n, mu_a = 400_000, np.float32(0.5)
+    keys = R.split(R.PRNGKey(3), n)
+    r = oracle.c3_fwd(keys, mu_a, mu_s=0.0)
+    t = r.tallies64["absorbed"]
+    assert np.all(t[:, 1:] == 0)
+    assert r.per_item.max() == 1 and not r.trunc.any()
+    z = 5.0 * np.arange(65) / 64
+    p = np.exp(-0.5 * z[:-1]) - np.exp(-0.5 * z[1:])
+    dev = np.abs(t[:, 0] - n * p)
+    assert np.all(dev <= 5 * np.sqrt(n * p * (1 - p)) + 1), dev.max()
+    assert abs(t.sum() - n * (1 - np.exp(-2.5))) <= 5 * np.sqrt(n * 0.08)
+    g, ntr = oracle.c3_grad(keys, mu_a, np.ones((64, 64), np.float32), mu_s=0.0)
+    assert ntr == 0 and g == 0.0
+
+
+def test_c3_henyey_greenstein_and_rotation(oracle):
+    """The deflection cosine drawn from uniforms on a fine midpoint grid has mean g (the Henyey-Greenstein
+    anisotropy), for g = 0.8 and g = 0.3, and stays in [-1, 1].  The direction update keeps directions unit length
+    and turns each by exactly the sampled angle (old . new = cos theta), including the near-vertical frame, and two
+    azimuths phi1, phi2 at the same deflection end cos(phi1 - phi2) apart around the old direction."""
+    u = ((np.arange(1 << 20) + 0.5) / (1 << 20)).astype(np.float32)
+    for g in (0.8, 0.3):
+        c = oracle.hg_cost(u, g).astype(np.float64)
+        assert abs(c.mean() - g) < 2e-4, (g, c.mean())
+        assert c.min() >= -1.0 - 1e-6 and c.max() <= 1.0 + 1e-6
+    rng = np.random.default_rng(1)
+    n = 20_000
+    d = rng.standard_normal((n, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    d[:4] = [[0, 0, 1], [0, 0, -1], [0, 0, 1], [1e-4, 0, -1.0]]
+    d = (d / np.linalg.norm(d, axis=1, keepdims=True)).astype(np.float32)
+    cost = rng.uniform(-1, 1, n).astype(np.float32)
+    phi1 = rng.uniform(0, 2 * np.pi, n).astype(np.float32)
+    phi2 = rng.uniform(0, 2 * np.pi, n).astype(np.float32)
+    a = oracle.hg_rotate(d, cost, phi1).astype(np.float64)
+    b = oracle.hg_rotate(d, cost, phi2).astype(np.float64)
+    dd = d.astype(np.float64)
+    # f32 roundoff of the update grows like eps / (1 - uz^2) near the vertical (sqrt(1 - uz^2) cancels)
+    tol = 2e-5 + 4e-8 / np.maximum(1.0 - dd[:, 2] ** 2, 1e-12)
+    near = np.abs(dd[:, 2]) > 0.99999                # the fixed frame treats d as vertical: the angle is off by at
+    tol[near] = 2e-5 + np.hypot(dd[near, 0], dd[near, 1])  # most the transverse component it ignores
+    assert np.all(np.abs(np.linalg.norm(a, axis=1) - 1.0) <= tol)
+    assert np.all(np.abs(np.sum(dd * a, axis=1) - cost) <= 2 * tol)
+    va = a - cost[:, None] * dd
+    vb = b - cost[:, None] * dd
+    nrm = np.linalg.norm(va, axis=1) * np.linalg.norm(vb, axis=1)
+    ok = nrm > 1e-3
+    cosd = np.sum(va * vb, axis=1)[ok] / nrm[ok]
+    assert np.allclose(cosd, np.cos(phi1[ok].astype(np.float64) - phi2[ok]), atol=2e-3)
+
+
+# ------------------------------------------------------------------------------------------- C4 pins
+def test_c4_walk_on_spheres_estimates_the_harmonic_extension(oracle):
+    """Walk on spheres estimates the harmonic function with boundary values sin(3 theta), u(r, theta) = r^3
+    sin(3 theta): from fixed start points the mean score / a of 200,000 walkers agrees within 5 standard errors plus
+    the 1e-3 shell's bias.  d(sum of the walker tally) / d a = sum(scores) / a (a multiplies every score)."""
+    from tallymap_amd import random as R
+    n = 200_000
+    keys = R.split(R.PRNGKey(11), n)
+    ids = np.arange(n, dtype=np.int32)
+    for x, y in ((0.5, 0.3), (-0.2, 0.6), (0.1, -0.85)):
+        p0 = np.tile(np.array([x, y], np.float32), (n, 1))
+        r = oracle.c4_fwd(p0, keys, ids, np.float32(1.0))
+        s = r.tallies64["walker"][:, 0]
+        exact = np.hypot(x, y) ** 3 * np.sin(3 * np.arctan2(y, x))
+        assert abs(s.mean() - exact) <= 5 * s.std() / np.sqrt(n) + 3e-3, (x, y, s.mean(), exact)
+        assert not r.trunc.any()
+    a = np.float32(0.75)
+    r = oracle.c4_fwd(p0, keys, ids, a)
+    g, ntr = oracle.c4_grad(p0, keys, ids, a, np.zeros((256, 256), np.float32), np.ones((n, 1), np.float32))
+    assert abs(float(g) - r.tallies64["walker"].sum() / 0.75) <= 1e-5 * np.abs(r.tallies64["walker"]).sum()
+
+
+# ------------------------------------------------------------------------------------------- C5 pins
+def test_c5_tableau_is_dormand_prince(oracle):
+    """the oracle's and the item's coefficients are scipy's RK45 (Dormand-Prince 5(4)) tableau, as f32 (the error
+    weights up to sign, which the error norm does not see)."""
+    from scipy.integrate._ivp.rk import RK45
+
+    from tallymap_amd import configs
+    c, a, b, e = oracle.c5_tableau()
+    assert np.array_equal(c, RK45.C[1:5].astype(np.float32))
+    assert np.array_equal(a, np.concatenate([RK45.A[i, :i] for i in range(1, 6)]).astype(np.float32))
+    assert np.array_equal(b, RK45.B[[0, 2, 3, 4, 5]].astype(np.float32))
+    assert np.array_equal(e, (-RK45.E[[0, 2, 3, 4, 5, 6]]).astype(np.float32))
+    assert np.array_equal(np.float32(configs.DP_C), c)
+    assert np.array_equal(np.float32(np.concatenate(configs.DP_A)), a)
+    assert np.array_equal(np.float32(configs.DP_B), b)
+    assert np.array_equal(np.float32(configs.DP_E), e)
+
+
+def _pendulum(A):
+    def f(t, y):
+        return [y[1], -0.1 * y[1] - np.sin(y[0]) + A * np.cos(2.0 / 3.0 * t)]
+    return f
+
+
+def test_c5_undriven_pendulum_matches_scipy(oracle):
+    """A = 0 (no drive): the damped pendulum is not chaotic; the oracle's adaptive f32 DP5(4) final states at t = 50
+    agree with scipy's solve_ivp (RK45, rtol 1e-11, float64) within 2e-4."""
+    from scipy.integrate import solve_ivp
+    rng = np.random.default_rng(5)
+    th0 = rng.uniform(-3.0, 3.0, 12).astype(np.float32)
+    om0 = rng.uniform(-2.0, 2.0, 12).astype(np.float32)
+    ids = np.arange(12, dtype=np.int32)
+    r = oracle.c5_fwd(th0, om0, ids, np.float32(0.0))
+    assert not r.trunc.any()
+    for i in range(12):
+        s = solve_ivp(_pendulum(0.0), (0.0, 50.0), [float(th0[i]), float(om0[i])], rtol=1e-11, atol=1e-13)
+        assert np.allclose(r.tallies64["state"][i], s.y[:, -1], atol=2e-4), (i, r.tallies64["state"][i], s.y[:, -1])
+
+
+def test_c5_gradient_matches_finite_differences(oracle):
+    """a weak drive (A = 0.1) from small initial states, where the motion is not chaotic: the oracle's forward-mode
+    gradient of E(final) w.r.t. A for each item agrees with a central difference (h = 1e-3) of scipy's float64
+    solution within 2e-3 relative."""
+    from scipy.integrate import solve_ivp
+    rng = np.random.default_rng(6)
+    n = 6
+    th0 = rng.uniform(-0.5, 0.5, n).astype(np.float32)
+    om0 = rng.uniform(-0.5, 0.5, n).astype(np.float32)
+    ids = np.arange(n, dtype=np.int32)
+    A, h = 0.1, 1e-3
+    r = oracle.c5_fwd(th0, om0, ids, np.float32(A))
+    st = r.tallies["state"]
+    ct_all = np.stack([np.sin(st[:, 0].astype(np.float64)), st[:, 1]], 1).astype(np.float32)
+    for i in range(n):
+        ct = np.zeros((n, 2), np.float32)
+        ct[i] = ct_all[i]
+        g, ntr = oracle.c5_grad(th0, om0, ids, np.float32(A), ct)
+        y = [solve_ivp(_pendulum(a), (0.0, 50.0), [float(th0[i]), float(om0[i])], rtol=1e-12, atol=1e-14).y[:, -1]
+             for a in (A + h, A - h)]
+        dy = (y[0] - y[1]) / (2 * h)
+        want = float(ct[i].astype(np.float64) @ dy)
+        assert abs(float(g) - want) <= 2e-3 * abs(want), (i, float(g), want)
