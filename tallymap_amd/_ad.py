@@ -111,10 +111,10 @@ def _zeros_like(aval):
     return _f(0, aval.dtype)
 
 
-def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=None):
+def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=None, with_primal=False):
     """-> (Jaxpr, ct_out_mask, ct_in_mask).
     The Jaxpr's invars: jx.invars + [cotangent of each output in ct_out_mask]; outvars: [cotangent of each input
-    in ct_in_mask].  ct_out_mask: jx's active float outputs; ct_in_mask: jx's active inputs.
+    in ct_in_mask], preceded (with_primal) by jx's own outputs, replayed: one program for a step and its VJP.  ct_out_mask: jx's active float outputs; ct_in_mask: jx's active inputs.
     ct_read(slot, idx) -> the cotangent tally value (a Tracer) for an emit into tally `slot` at index idx; slots:
     {invar index of a tally input: its slot}.  ct_given: outputs whose cotangent may be nonzero (default: all); the
     others get no cotangent input."""
@@ -178,6 +178,14 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
             for v, c in zip(e.invars, cin):
                 add(v, c)
         res = []
+        if with_primal:
+            for v in jx.outvars:
+                x = _t(v, env)
+                if C.is_traced(x):
+                    res.append(b.local(x.var))
+                else:
+                    a = np.asarray(x, v.aval.dtype)
+                    res.append(C.Lit(np.broadcast_to(a, v.aval.shape).copy(), v.aval.strong()))
         for v, m in zip(jx.invars, ct_in_mask):
             if m:
                 c = ct.get(v.id)
@@ -191,7 +199,7 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
         C._STACK.pop()
     outv = []
     for r in res:
-        outv.append(r if isinstance(r, C.Var) else C.Lit(r, C.AVal((), np.asarray(r).dtype)))
+        outv.append(r if isinstance(r, (C.Var, C.Lit)) else C.Lit(r, C.AVal((), np.asarray(r).dtype)))
     return C.Jaxpr(b.invars, outv, b.eqns), ct_out_mask, ct_in_mask
 
 

@@ -22,7 +22,8 @@ STATS = ("spawned", "children_dropped", "children_truncated", "fixed_point_overf
 ST = {n: i for i, n in enumerate(STATS)}
 MAX_ITEMS = 2 ** 31 - 1
 PROG_CACHE = 64
-OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact")
+OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact", "rev_schedule",
+        "rev_tape", "rev_refill")
 
 
 class UnsupportedError(NotImplementedError):
@@ -308,7 +309,11 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
     opts:      schedule 'step' (default: a lane refills at loop-step granularity) | 'item'; block (threads per
                block, default 256); refill (idle lanes a wave waits for before it claims, default 1); compact
                (iterations between the tail-phase repacks of a workgroup's live items, default 16; 0: off);
-               rev_checkpoints (reverse mode, C states per checkpoint buffer); cuda_math and min_blocks_per_sm
+               rev_schedule (reverse mode: 'step', the default, a step-refilled replay over a tape in HBM, or
+               'item', one item per lane with in-lane checkpoints); rev_tape (states a lane's tape holds, default
+               512; longer items are swept from checkpoints); rev_refill (free lanes a wave waits for before the
+               step-scheduled replay hands it items, default 32; 64 suits items of equal length); rev_checkpoints (the 'item' schedule's C states per
+               checkpoint buffer); cuda_math and min_blocks_per_sm
                are accepted for drop-in compatibility and have no meaning on ROCm.
     """
     if fn is None:

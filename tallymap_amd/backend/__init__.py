@@ -92,7 +92,10 @@ def launch(c, ins, N, stream=None):
     L = c.layout
     outs = []
     for shape, dt, per_item in L.res:
-        sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
+        if per_item == "tape":          # per launched lane (the launcher's persistent grid at this N)
+            sh = (_lanes(c, N),) + tuple(shape)
+        else:
+            sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
         outs.append(torch.empty(sh, dtype=torch_dtype(dt), device="cuda"))
     bufs = [t.data_ptr() for t in ins] + [t.data_ptr() for t in outs]
     arr = (ctypes.c_void_p * len(bufs))(*bufs)
@@ -120,6 +123,17 @@ def run(prog, pi, bc, N, opts):
     ys = [res[r - base] for r in L.r_ys]
     ntr = res[L.r_ctl - base][2:3].view(__import__("torch").int32)[0] if prog.trunc is not None else None
     return Outputs(tallies, stats, ys, ntr)
+
+
+_LANES = {}
+
+
+def _lanes(c, N):
+    """the lanes tm_launch starts for c at N items: min(ceil(N / block), CUs x blocks per CU) x block."""
+    r = _LANES.get(c.id)
+    if r is None:
+        r = _LANES[c.id] = kernel_info(c)["resident_threads"]
+    return min(-(-int(N) // c.block) * c.block, r)
 
 
 def kernel_info(c):
@@ -156,7 +170,8 @@ def prebuild(entries, n=64):
             adj = R.adjoint_program(prog, wrt)
             pl = R.plan(adj)
             if any(pl.car_act):
-                src, _ = R.build(adj, block=K.BLOCK, ckpt=R.C_DEFAULT)
+                from . import replay as RP
+                src, _ = RP.build(adj, block=K.BLOCK, tape=RP.TAPE)
             else:
                 src, _ = K.build(R.forward_only_program(adj, pl), block=K.BLOCK, schedule="step", refill=1)
             Cm.code_object(src, name=f"tm_{adj.tag}.hip", store_pkg=True)
@@ -167,15 +182,24 @@ def prebuild(entries, n=64):
 def compiled_adjoint(adj, opts):
     """the registered adjoint kernel of `adj` (a reverse.Adjoint) under opts."""
     from . import reverse as R
+    from . import replay as RP
     block = int(opts.get("block", K.BLOCK))
     ck = int(opts.get("rev_checkpoints", R.C_DEFAULT) or R.C_DEFAULT)
-    key = (adj.digest(), block, "adjoint", ck)
+    sched = opts.get("rev_schedule", "step")
+    tape = int(opts.get("rev_tape", RP.TAPE) or RP.TAPE)
+    rrefill = int(opts.get("rev_refill", RP.REFILL))
+    if sched not in ("step", "item"):
+        raise ValueError(f"tallymap_amd: rev_schedule must be 'step' or 'item', got {sched!r}")
+    key = (adj.digest(), block, "adjoint", sched, ck if sched == "item" else (tape, rrefill))
     with _LOCK:
         hit = _KERNELS.get(key)
         if hit is not None:
             _KERNELS.move_to_end(key)
             return hit
-    src, L = R.build(adj, block=block, ckpt=ck)
+    if sched == "step":
+        src, L = RP.build(adj, block=block, tape=tape, refill=rrefill)
+    else:
+        src, L = R.build(adj, block=block, ckpt=ck)
     img = Cm.code_object(src, name=f"tm_{adj.tag}.hip")
     kid = int(Cm._key(src)[:15], 16)
     Cm.check(Cm.lib().tm_register(kid, img, len(img), f"{adj.tag} {adj.where}".encode()))

@@ -63,7 +63,8 @@ def test_c3_slab_transport_parity(oracle, n):
 
 @pytest.mark.parametrize("n", [65_536, 4_194_304])
 def test_c3_grad_mu_a(oracle, n):
-    """d sum(absorbed) / d mu_a: the checkpointed replay adjoint (the weight is a loop carry) vs forward mode."""
+    """d sum(absorbed) / d mu_a: the replay adjoint (the weight is a loop carry) vs forward mode; the one-item-per-lane
+    replay gives bitwise the same exact sum."""
     print(f"case: C3 grad mu_a N={n}", flush=True)
     keys, mu_a = configs.c3_inputs(n)
     g = tm.grad(_mapped(configs.C3), argnums=1)(keys, mu_a)
@@ -71,6 +72,10 @@ def test_c3_grad_mu_a(oracle, n):
     want, ntr = oracle.c3_grad(keys, mu_a, np.ones((64, 64), np.float32))
     assert ntr == 0
     assert _rel(_np(g), want) <= GTOL, (float(_np(g)), float(want))
+    if n == 65_536:
+        gi = tm.grad(_mapped(configs.C3, rev_schedule="item"), argnums=1)(keys, mu_a)
+        _sync()
+        assert np.float32(_np(gi)).view(np.uint32) == np.float32(_np(g)).view(np.uint32)
 
 
 # ------------------------------------------------------------------------------------------------- C4

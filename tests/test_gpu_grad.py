@@ -1,6 +1,6 @@
 """Reverse mode on the GPU: the replay adjoint kernel against the oracle's forward-mode (dual number) gradients.
-Gradients within 1e-4 relative; the per-item cotangents bitwise independent of the checkpoint
-count C (reference tests/reverse.py:216); truncation makes every cotangent NaN (reference _primitive.py:586-594)."""
+Gradients within 1e-4 relative; the per-item cotangents bitwise independent of the replay's
+schedule, tape size and checkpoint count (reference tests/reverse.py:216); truncation makes every cotangent NaN (reference _primitive.py:586-594)."""
 import numpy as np
 import pytest
 
@@ -39,14 +39,22 @@ def test_c1_grad_theta(oracle):
     assert abs(got - closed) <= GTOL * abs(closed)
 
 
-@pytest.mark.parametrize("C", [16, 4, 2, 1])
-def test_c1_grad_xs_and_checkpoint_independence(oracle, C):
-    """cotangents of xs (per item, through the loop state: the checkpointed replay) and of theta with weights ct;
-    C = 1, 2, 4 force the replay and the K > C^2 branch; per-item results bitwise equal to C = 16."""
-    print(f"case: C1 vjp (xs, theta) C={C}", flush=True)
+VARIANTS = [dict(), dict(rev_tape=4), dict(rev_tape=2), dict(rev_refill=1), dict(rev_refill=64),
+            dict(rev_schedule="item"), dict(rev_schedule="item", rev_checkpoints=4),
+            dict(rev_schedule="item", rev_checkpoints=1)]
+
+
+@pytest.mark.parametrize("opts", VARIANTS, ids=["step", "tape4", "tape2", "refill1", "refill64", "item16", "item4",
+                                                "item1"])
+def test_c1_grad_xs_and_replay_variants(oracle, opts):
+    """cotangents of xs (per item, through the loop state: the replay) and of theta with weights ct, against the
+    oracle; the replay variants -- the step-scheduled tape (an ~8-step item overflows a 4- or 2-slot tape into the
+    checkpointed sweep; waves refilled by 1 or 64 free lanes) and the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its segment
+    re-runs) -- give bitwise the same per-item cotangents and broadcast cotangent (reference tests/reverse.py:216)."""
+    print(f"case: C1 vjp (xs, theta) {opts}", flush=True)
     xs, keys, theta = configs.c1_inputs()
     ct = np.linspace(0.5, 2.0, 16).astype(np.float32)
-    res, pull = tm.vjp(_mapped(configs.C1, rev_checkpoints=C), xs, keys, theta, argnums=(0, 2))
+    res, pull = tm.vjp(_mapped(configs.C1, **opts), xs, keys, theta, argnums=(0, 2))
     gx, gth = pull({"hist": ct})
     _sync()
     want_th, want_x, ntr = oracle.c1_grad(xs, keys, theta, ct, per_item=True)
@@ -54,11 +62,12 @@ def test_c1_grad_xs_and_checkpoint_independence(oracle, C):
     assert abs(float(_np(gth)) - float(want_th)) <= GTOL * abs(float(want_th))
     err = np.abs(gx - want_x) / np.maximum(np.abs(want_x), 1.0)
     assert err.max() <= GTOL, err.max()
-    if C != 16:
-        _, pull16 = tm.vjp(_mapped(configs.C1), xs, keys, theta, argnums=(0, 2))
-        gx16, _ = pull16({"hist": ct})
+    if opts:
+        _, pull0 = tm.vjp(_mapped(configs.C1), xs, keys, theta, argnums=(0, 2))
+        gx0, gth0 = pull0({"hist": ct})
         _sync()
-        assert np.array_equal(gx.view(np.uint32), _np(gx16).view(np.uint32))
+        assert np.array_equal(gx.view(np.uint32), _np(gx0).view(np.uint32))
+        assert np.float32(_np(gth)).view(np.uint32) == np.float32(_np(gth0)).view(np.uint32)
 
 
 def test_c1_grad_truncation_is_nan(oracle):
