@@ -66,13 +66,14 @@ def compiled(prog, opts, adjoint=None):
     schedule = opts.get("schedule", "step")
     refill = int(opts.get("refill", 1))
     compact = int(opts.get("compact", K.COMPACT))
-    key = (prog.digest(), block, schedule, refill, compact)
+    mb = int(opts.get("min_blocks_per_sm", 0) or 0)
+    key = (prog.digest(), block, schedule, refill, compact, mb)
     with _LOCK:
         hit = _KERNELS.get(key)
         if hit is not None:
             _KERNELS.move_to_end(key)
             return hit
-    src, L = K.build(prog, block=block, schedule=schedule, refill=refill, compact=compact)
+    src, L = K.build(prog, block=block, schedule=schedule, refill=refill, compact=compact, min_blocks=mb)
     img = Cm.code_object(src, name=f"tm_{prog.tag}.hip")
     kid = int(Cm._key(src)[:15], 16)
     Cm.check(Cm.lib().tm_register(kid, img, len(img), f"{prog.tag} {prog.where}".encode()))

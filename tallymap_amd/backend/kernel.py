@@ -122,11 +122,12 @@ def _repack_code(decls, cap):
     return pack, unpack, w
 
 
-def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COMPACT):
+def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COMPACT, min_blocks=0):
     """-> (HIP source, Layout) of prog's module.  chunk: items a wave claims with one atomic (their per-item operands
     are staged in LDS by one coalesced load, and idle lanes take them from there at step granularity).  compact:
     once every wave of a workgroup has drained the item queue, the waves meet every `compact` iterations and
-    repack their live items densely onto the first waves (0: off; step schedule only)."""
+    repack their live items densely onto the first waves (0: off; step schedule only).  min_blocks: workgroups per
+    CU the compiler must leave registers for (as waves per SIMD in __launch_bounds__; 0: its own choice)."""
     chunk = max(1, int(chunk))
     compact = max(0, int(compact))
     jx = prog.jaxpr
@@ -394,7 +395,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     # the gradient launch of a forward-only adjoint is named tm_adjoint like the checkpointed one (profiles tell the
     # forward and gradient launches apart by name; the launcher accepts either entry)
     entry = "tm_adjoint" if getattr(prog, "poison_ys", False) else "tm_main"
-    body.append(f"extern \"C\" __global__ void __launch_bounds__({block}) {entry}(const TmParams P, "
+    lb = f"{block}, {max(1, int(min_blocks) * block // 256)}" if min_blocks else f"{block}"
+    body.append(f"extern \"C\" __global__ void __launch_bounds__({lb}) {entry}(const TmParams P, "
                 "const i64 n_items) {")
     body.append("  u64* const tm_ctr = (u64*)P.p[%d];" % r_ctl)
     for k in priv:
@@ -418,8 +420,17 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         for e in range(max(1, a.size)):
             body.append(f"  const {ct} tm_b{i}_{e} = ((const {ct}*)P.p[{nP + i}])[{e}];")
     wpb = block // 64
+    compact_on = bool(compact) and mode == "step"
+    if compact_on:
+        pack, unpack, nwords = _repack_code(decls, wpb * 64)
+    # one LDS array serves the operand staging of claimed chunks and, once every wave of the workgroup has drained
+    # the queue (no wave stages any more), the repack pool
+    n_stage = wpb * chunk * W
+    n_pool = nwords * wpb * 64 if compact_on else 0
+    if n_stage or n_pool:
+        body.append(f"  __shared__ u32 tm_lds[{max(n_stage, n_pool)}];")
     if W:
-        body.append(f"  __shared__ u32 tm_stage[{wpb * chunk * W}];")
+        body.append("  u32* const tm_stage = tm_lds;")
         body.append(f"  u32* const tm_st = tm_stage + (threadIdx.x >> 6) * {chunk * W};")
     body.append("  bool tm_live = false, tm_more = true;")
     body.append("  i64 tm_item = 0;")
@@ -428,10 +439,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append("  i32 tm_drop = 0;")
     body.append("  u32 tm_ntr = 0;")
     body += decls
-    compact_on = bool(compact) and mode == "step"
     if compact_on:
-        pack, unpack, nwords = _repack_code(decls, wpb * 64)
-        body.append(f"  __shared__ u32 tm_pool[{nwords * wpb * 64}];   // the repack pool, one column per word")
+        body.append("  u32* const tm_pool = tm_lds;                  // the repack pool, one column per word")
         body.append("  __shared__ u32 tm_pn[2];                 // pool counts, alternating between rounds")
         body.append("  __shared__ u32 tm_ndr;                   // waves of this workgroup whose queue is drained")
         body.append("  if (threadIdx.x == 0) { tm_pn[0] = 0u; tm_pn[1] = 0u; tm_ndr = 0u; }")
