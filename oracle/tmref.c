@@ -24,6 +24,11 @@
  * kernel.py:870-941) by a multi-limb magnitude accumulator that shares no code or format with the product's.
  * Every float tally also gets a float64 shadow sum of the same emits: the re-summation the tolerances are
  * measured against.
+ *
+ * Pinned by tests/test_oracle.py (known answers, closed forms, special cases, scipy) except where noted:
+ *   PARITY UNPINNED: fold_in / split / uniform / normal layering on the threefry core (JAX's partitionable PRNG;
+ *   JAX is absent here: pinned only by agreement with the independent numpy restatement in tallymap_amd.random);
+ *   c3_item's forward-mode gradient with scattering (pinned through its mu_s = 0 special case only).
  */
 #include <fenv.h>
 #include <math.h>

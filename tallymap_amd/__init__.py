@@ -3,7 +3,8 @@
 An item function of ONE item (its own while loop, its own jax.random draws, results added into write-only
 tallies) is traced into a jaxpr-shaped program, lowered to HIP, compiled with hipRTC for gfx950 and launched as
 one persistent wave64 kernel through the C-ABI library libtallymap_rocm.so.  Reverse-mode gradients run the
-checkpointed replay adjoint through the same path.
+replay adjoint (a step-scheduled replay over a tape in HBM, or an ordinary item program when no loop carry needs a
+reverse sweep) through the same path.
 """
 from . import lax, numpy, random
 from ._api import STATS, Result, Sum, TallyError, UnsupportedError, grad, vjp, vmap

@@ -217,7 +217,8 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
     operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
     0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated).
     When no loop carry needs a reverse sweep the adjoint is an ordinary item program (reverse.forward_only_program)
-    run by the forward template (step refill); otherwise the checkpointed replay template (reverse.build)."""
+    run by the forward template (step refill); otherwise the replay kernel opts['rev_schedule'] names: 'step' (the
+    default, replay.build: step refill over a tape) or 'item' (reverse.build: in-lane checkpoints)."""
     import torch
 
     from . import reverse as R
