@@ -14,6 +14,8 @@ cpu_baseline: the oracle (the C/OpenMP restatement of the reference's CPU kernel
 bounded sample of the same workload (the first items of the same inputs), forward + gradient, items/s.
 configs: the other BASELINE configs at their own sizes (C1 10,000; C3, C4 4,194,304; C5 1,048,576), forward and
 gradient launches timed the same way, each with the oracle on a bounded sample beside it.
+atomics / emit_roofline: the atomic adds/s of the patterns the kernels issue (backend/atomics.py; MI355X publishes no
+atomic peak), and C2's forward emit rate against the peak of the LDS u64 adds its constant emits are counted with.
 """
 import argparse
 import json
@@ -164,7 +166,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4_194_304)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--headline-only", action="store_true", help="skip the configs 1, 3, 4, 5 section")
+    ap.add_argument("--headline-only", action="store_true", help="skip the configs 1, 3, 4, 5 and atomics sections")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="run one plain device copy of BYTES first (its FETCH_SIZE / WRITE_SIZE under rocprofv3 "
                          "calibrate the traffic counters)")
@@ -259,6 +261,19 @@ def main():
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(x0, keys, drift, cfg["max_steps"])
     if not a.headline_only:
+        # the atomic peaks MI355X does not publish, measured; C2's emits add the constant 1.0 to its privatised
+        # occupancy (128 bins) and wall (2 bins) tallies, one per kept step and one per item, which the kernel
+        # counts with LDS u64 adds (the flush adds count x 1.0): their peak is lds_u64_128's
+        from tallymap_amd.backend import atomics
+        peaks = {p: atomics.run(p) for p in atomics.PATTERNS}
+        emits = float(r.outputs["occ"].double().sum().item() + r.outputs["wall"].double().sum().item())
+        rate = emits / (fwd_ms * 1e-3)
+        out["atomics"] = {p: {"adds_per_s": v["adds_per_s"], "exact": v["exact"]} for p, v in peaks.items()}
+        out["emit_roofline"] = {"kernel": "tm_main (forward)", "emits_per_launch": emits, "achieved": rate,
+                                "peak": peaks["lds_u64_128"]["adds_per_s"], "unit": "LDS u64 atomic adds/s",
+                                "frac": rate / peaks["lds_u64_128"]["adds_per_s"],
+                                "f32_peak": peaks["lds_f32_128"]["adds_per_s"]}
+        print("bench: atomics done", file=sys.stderr, flush=True)
         out["configs"] = bench_configs(max(3, a.steps // 4), 1, not a.no_cpu)
     print(json.dumps(out))
 

@@ -162,6 +162,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             priv.append(k)
 
     em = Emitter()
+    counts = {}                 # (tally slot, f32 bits of a constant emitted value) -> (LDS u64 counter array, value)
 
     def emit_rule(em_, e, ins):
         t, idx, val = ins
@@ -175,6 +176,18 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         em_.close("} else {")
         em_.ind += 1
         v = val.el[0]
+        lv = e.invars[2]
+        if (k in priv and s.dtype == C.F32 and not s.exact and isinstance(lv, C.Lit)
+                and np.isfinite(float(lv.val)) and float(lv.val) != 0.0):
+            # a constant f32 emit into a privatised tally: count it (integer LDS atomics run far faster than f32
+            # ones on CDNA), the flush adds count x constant
+            c = np.float32(lv.val)
+            key = (k, int(c.view(np.uint32)))
+            if key not in counts:
+                counts[key] = (f"tm_cn{k}_{len(counts)}", c)
+            em_.line(f"atomicAdd(&{counts[key][0]}[{ei}], 1ull);")
+            em_.close()
+            return t
         if s.exact:
             acc = f"tm_xsh{k}" if k in priv else f"((u64*)P.p[{r_scr[k]}])"
             fl = f"tm_xfl{k}" if k in priv else f"((u32*)P.p[{r_scr[k]}] + {2 * XW * s.S})"
@@ -411,6 +424,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             ct = ctype(s.dtype)
             body.append(f"  __shared__ {ct} tm_sh{k}[{s.S}];")
             body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) tm_sh{k}[i] = ({ct})0;")
+    body.append("//TM_COUNT_DECLS")
     if priv:
         body.append("  __syncthreads();")
     for i, a in enumerate(bav):
@@ -568,11 +582,22 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             elif s.dtype == C.F32:
                 body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const float x = tm_sh{k}[i]; "
                             f"if (x != 0.0f) tm_gadd_f32(&((float*)P.p[{r_out[k]}])[i], x); }}")
+                for (kk, _), (nm, c) in counts.items():
+                    if kk == k:
+                        body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const u64 n = {nm}[i]; "
+                                    f"if (n != 0ull) tm_gadd_f32(&((float*)P.p[{r_out[k]}])[i], "
+                                    f"(float)n * {lit(c, np.float32)}); }}")
             else:
                 ct = ctype(s.dtype)
                 body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const {ct} x = tm_sh{k}[i]; "
                             f"if (x != 0) atomicAdd(&(({ct}*)P.p[{r_out[k]}])[i], x); }}")
     body.append("}")
+    cdecl = []
+    for (k, _), (nm, c) in counts.items():
+        S = prog.tallies[k].S
+        cdecl.append(f"  __shared__ u64 {nm}[{S}];")
+        cdecl.append(f"  for (int i = threadIdx.x; i < {S}; i += blockDim.x) {nm}[i] = 0ull;")
+    body[body.index("//TM_COUNT_DECLS")] = "\n".join(cdecl)
     src.append("\n".join(body))
     L = Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_out, r_ctl=r_ctl, r_stats=r_stats, r_ys=r_ys,
                flags=flags, mode=mode, priv=priv, zero_words=zero_words)
