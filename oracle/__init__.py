@@ -62,6 +62,8 @@ def lib():
         L.tmref_c4_grad.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p]
         L.tmref_c5_fwd.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
         L.tmref_c5_grad.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p]
+        L.tmref_exact_begin.argtypes = [_i, _p]
+        L.tmref_exact_read.argtypes = [_i, _p, _p]
         L.tmref_max_threads.restype = _i
         _lib = L
     return _lib
@@ -290,3 +292,22 @@ def c5_tableau():
     out = np.zeros(30, np.float32)
     lib().tmref_c5_tableau(_ptr(out))
     return out[:4], out[4:19], out[19:24], out[24:]
+
+
+def exact_tallies(run, sizes):
+    """run() (an oracle forward call) with every tally also summed exactly -> [(f32 exact sums, bad flags)] per
+    tally in slot order: the correctly rounded f32 of each bin's exact sum, NaN with bad = True where a non-finite
+    value was emitted or the total leaves f32 (the meaning of Sum(fixed_point=True))."""
+    sz = np.ascontiguousarray(sizes, np.int64)
+    lib().tmref_exact_begin(len(sizes), _ptr(sz))
+    try:
+        r = run()
+        out = []
+        for k, n in enumerate(sizes):
+            v = np.zeros(int(n), np.float32)
+            b = np.zeros(int(n), np.uint8)
+            lib().tmref_exact_read(k, _ptr(v), _ptr(b))
+            out.append((v, b.astype(bool)))
+    finally:
+        lib().tmref_exact_end()
+    return r, out

@@ -271,9 +271,34 @@ typedef struct {
 typedef struct {
   float* f[8];
   double* d[8];
+  exsum* x[8];            /* per-thread exact sums (tmref_exact_begin) */
   const tm_tallies* T;
   i64 dropped;
 } tm_thr;
+
+/* Exact f32 sums of the next forward call's tallies (the meaning of Sum(fixed_point=True), reference
+ * _api.py:55-84): tmref_exact_begin before the call, tmref_exact_read per tally after it, tmref_exact_end. */
+static exsum* g_ex[8];
+static i64 g_ex_n[8];
+static int g_exact = 0;
+void tmref_exact_begin(int nt, const i64* sizes) {
+  for (int k = 0; k < nt && k < 8; ++k) {
+    g_ex[k] = (exsum*)calloc((size_t)sizes[k], sizeof(exsum));
+    g_ex_n[k] = sizes[k];
+  }
+  g_exact = 1;
+}
+void tmref_exact_read(int k, float* out, uint8_t* bad) {
+  for (i64 i = 0; i < g_ex_n[k]; ++i) {
+    int b = 0;
+    out[i] = ex_read(&g_ex[k][i], &b);
+    bad[i] = (uint8_t)b;
+  }
+}
+void tmref_exact_end(void) {
+  for (int k = 0; k < 8; ++k) { free(g_ex[k]); g_ex[k] = NULL; g_ex_n[k] = 0; }
+  g_exact = 0;
+}
 
 /* an IEEE compare-and-swap add (host.py:158-161) */
 static inline void cas_addf(float* a, float v) {
@@ -290,6 +315,7 @@ static inline void cas_addd(double* a, double v) {
 
 static inline void emit(tm_thr* t, int k, i64 idx, float v) {
   if ((u64)idx >= (u64)t->T->size[k]) { t->dropped++; return; }
+  if (t->x[k]) ex_add(&t->x[k][idx], v);
   if (t->T->priv) t->f[k][idx] += v; else cas_addf(&t->T->out[k][idx], v);
   if (t->d[k]) t->d[k][idx] += (double)v;
   else if (t->T->shadow) cas_addd(&t->T->shadow[k][idx], (double)v);
@@ -301,6 +327,7 @@ static void thr_init(tm_thr* t, const tm_tallies* T) {
   for (int k = 0; k < T->nt; ++k) {
     if (T->priv) t->f[k] = (float*)calloc((size_t)T->size[k], sizeof(float));
     if (T->shadow && T->priv) t->d[k] = (double*)calloc((size_t)T->size[k], sizeof(double));
+    if (g_exact && g_ex[k]) t->x[k] = (exsum*)calloc((size_t)T->size[k], sizeof(exsum));
   }
 }
 
@@ -313,6 +340,11 @@ static void thr_flush(tm_thr* t, i32* stats) {
     }
     free(t->f[k]);
     free(t->d[k]);
+    if (t->x[k]) {
+#pragma omp critical
+      for (i64 i = 0; i < T->size[k]; ++i) ex_merge(&g_ex[k][i], &t->x[k][i]);
+      free(t->x[k]);
+    }
   }
   if (t->dropped) __atomic_fetch_add(&stats[ST_DROPPED], (i32)t->dropped, __ATOMIC_RELAXED);
 }

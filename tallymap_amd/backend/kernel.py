@@ -586,7 +586,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                     if kk == k:
                         body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const u64 n = {nm}[i]; "
                                     f"if (n != 0ull) tm_gadd_f32(&((float*)P.p[{r_out[k]}])[i], "
-                                    f"(float)n * {lit(c, np.float32)}); }}")
+                                    f"tm_u64_f32(n) * {lit(c, np.float32)}); }}")
             else:
                 ct = ctype(s.dtype)
                 body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const {ct} x = tm_sh{k}[i]; "

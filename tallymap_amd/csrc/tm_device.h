@@ -44,6 +44,35 @@ TM_FN u32 tm_f2u(float f) { return __builtin_bit_cast(u32, f); }
 TM_FN double tm_u2d(u64 u) { return __builtin_bit_cast(double, u); }
 TM_FN u64 tm_d2u(double d) { return __builtin_bit_cast(u64, d); }
 
+// ------------------------------------------------------------------------- 64-bit shifts by a variable amount
+// Built from 32-bit shifts of the two halves, s in [0, 63].  gfx950 returns wrong results from a 64-bit VALU
+// shift (v_lshlrev_b64 / v_lshrrev_b64 / v_ashrrev_i64) whose shift-amount VGPR is the last register of an
+// 8-register allocation block (v7, v15, ..., v39 in a 40-register kernel): measured on MI355X as corrupted exact
+// sums, the register placement being the register allocator's choice.  Every 64-bit shift by a non-constant amount
+// in device code goes through these, so that no such instruction is emitted; backend/compile.py rejects a code
+// object that still contains one.
+TM_FN u64 tm_shl64(u64 x, u32 s) {
+  const u32 lo = (u32)x, hi = (u32)(x >> 32);
+  const u32 rh = s >= 32u ? lo << (s - 32u) : (s ? (hi << s) | (lo >> (32u - s)) : hi);
+  const u32 rl = s >= 32u ? 0u : lo << s;
+  return ((u64)rh << 32) | (u64)rl;
+}
+TM_FN u64 tm_shr64(u64 x, u32 s) {
+  const u32 lo = (u32)x, hi = (u32)(x >> 32);
+  const u32 rl = s >= 32u ? hi >> (s - 32u) : (s ? (lo >> s) | (hi << (32u - s)) : lo);
+  const u32 rh = s >= 32u ? 0u : hi >> s;
+  return ((u64)rh << 32) | (u64)rl;
+}
+TM_FN i64 tm_sar64(i64 x, u32 s) {
+  const u32 lo = (u32)(u64)x;
+  const i32 hi = (i32)(u32)((u64)x >> 32);
+  const u32 rl = s >= 32u ? (u32)(hi >> (s - 32u)) : (s ? (lo >> s) | ((u32)hi << (32u - s)) : lo);
+  const u32 rh = (u32)(hi >> (s >= 32u ? 31u : s));
+  return (i64)(((u64)rh << 32) | (u64)rl);
+}
+// u64 -> f32 rounded once, through an exact double (n < 2^53): the direct conversion lowers to a 64-bit shift
+TM_FN float tm_u64_f32(u64 n) { return (float)(double)n; }
+
 // ------------------------------------------------------------------------------------------- lax helpers
 template <class T> TM_FN T tm_fmax(T a, T b) {
   return (a > b || a != a) ? a : ((b > a || b != b) ? b : (a == (T)0 ? a + b : a));
@@ -67,13 +96,19 @@ TM_FN i64 tm_irem(i64 a, i64 b) {
 }
 
 template <class T, class U> TM_FN T tm_shl(T a, T b) {
-  return ((U)b >= (U)(sizeof(T) * 8)) ? (T)0 : (T)((U)a << (U)b);
+  if ((U)b >= (U)(sizeof(T) * 8)) return (T)0;
+  if constexpr (sizeof(T) == 8) return (T)tm_shl64((u64)a, (u32)b);
+  else return (T)((U)a << (U)b);
 }
 template <class T, class U> TM_FN T tm_shrl(T a, T b) {
-  return ((U)b >= (U)(sizeof(T) * 8)) ? (T)0 : (T)((U)a >> (U)b);
+  if ((U)b >= (U)(sizeof(T) * 8)) return (T)0;
+  if constexpr (sizeof(T) == 8) return (T)tm_shr64((u64)a, (u32)b);
+  else return (T)((U)a >> (U)b);
 }
 template <class T, class U> TM_FN T tm_shra(T a, T b) {
-  return ((U)b >= (U)(sizeof(T) * 8)) ? (T)(a < (T)0 ? (T)-1 : (T)0) : (T)(a >> (U)b);
+  if ((U)b >= (U)(sizeof(T) * 8)) return (T)(a < (T)0 ? (T)-1 : (T)0);
+  if constexpr (sizeof(T) == 8) return (T)tm_sar64((i64)a, (u32)b);
+  else return (T)(a >> (U)b);
 }
 
 // float -> integer toward zero, saturating, NaN -> 0
@@ -195,7 +230,7 @@ template <class Add> TM_FN bool tm_xemit_with(u64* a, float v, Add add) {
   const u64 m = (u64)(b & 0x7fffffu) | (e ? 0x800000ull : 0ull);
   if (m == 0ull) return false;
   const u32 p = e ? e - 1u : 0u, j = p / 63u, s = p - 63u * j;
-  const i64 lo = (i64)((m << s) & 0x7fffffffffffffffull), hi = s >= 40u ? (i64)(m >> (63u - s)) : 0ll;
+  const i64 lo = (i64)(tm_shl64(m, s) & 0x7fffffffffffffffull), hi = s >= 40u ? (i64)tm_shr64(m, 63u - s) : 0ll;
   const bool neg = (b >> 31) != 0u;
   bool lost = false;
   if (lo) lost = tm_xadd_with(a, (int)j, neg ? -lo : lo, add);
@@ -221,7 +256,7 @@ TM_FN float tm_xread(const u64* a, bool* bad) {
     const i64 w = (i64)a[j];
     const int sh = 63 * j, l = sh >> 6, b = sh & 63;
     const u64 ext = w < 0 ? ~0ull : 0ull;
-    const u64 x0 = (u64)w << b, x1 = b ? (u64)(w >> (64 - b)) : ext;
+    const u64 x0 = tm_shl64((u64)w, (u32)b), x1 = b ? (u64)tm_sar64(w, (u32)(64 - b)) : ext;
     u64 c = 0ull;
     for (int k = l; k < 6; ++k) {
       const u64 y = k == l ? x0 : (k == l + 1 ? x1 : ext);
@@ -243,8 +278,8 @@ TM_FN float tm_xread(const u64* a, bool* bad) {
   if (t < 0) return 0.0f;
   const int s = __builtin_clzll(d[t]);
   const u64 d1 = t >= 1 ? d[t - 1] : 0ull;
-  const u64 top = s ? (d[t] << s) | (d1 >> (64 - s)) : d[t];
-  bool st = s ? (d1 << s) != 0ull : d1 != 0ull;
+  const u64 top = s ? tm_shl64(d[t], (u32)s) | tm_shr64(d1, (u32)(64 - s)) : d[t];
+  bool st = s ? tm_shl64(d1, (u32)s) != 0ull : d1 != 0ull;
   for (int j = 0; j < t - 1; ++j) st = st || d[j] != 0ull;
   u64 q = top >> 40;
   const u64 r = top & 0xffffffffffull, half = 0x8000000000ull;

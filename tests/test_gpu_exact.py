@@ -1,0 +1,88 @@
+"""Sum(fixed_point=True) of float32 on the GPU: each bin is the correctly rounded f32 of the exact sum of every finite
+value emitted into it (reference _api.py:55-84), so the device result is BITWISE the oracle's exact sum and
+bitwise independent of the schedule, the launch shape and the order of the emits; a non-finite emit makes its bin
+NaN and counts in stats['fixed_point_overflow']."""
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import configs
+from tallymap_amd import numpy as jnp
+
+pytestmark = pytest.mark.gpu
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _np(x):
+    return x.cpu().numpy()
+
+
+def _bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+def _mapped(cfg, outputs, **opts):
+    return tm.vmap(cfg["item"], outputs=outputs, in_axes=cfg["in_axes"], max_steps=cfg["max_steps"], **opts)
+
+
+C1_EXACT = {"hist": tm.Sum((16,), fixed_point=True)}
+
+
+@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(block=64), dict(refill=8), dict(compact=0)],
+                         ids=["step", "item", "block64", "refill8", "nocompact"])
+def test_c1_exact_hist_bitwise(oracle, opts):
+    """C1 with an exact histogram (LDS exact accumulators): bitwise the oracle's exact sums, under every schedule."""
+    print(f"case: C1 exact {opts}", flush=True)
+    xs, keys, theta = configs.c1_inputs(1 << 18)
+    res = _mapped(configs.C1, C1_EXACT, **opts)(xs, keys, theta)
+    _sync()
+    ref, ex = oracle.exact_tallies(lambda: oracle.c1_fwd(xs, keys, theta), [16])
+    want, bad = ex[0]
+    assert not bad.any()
+    assert np.array_equal(_bits(_np(res.outputs["hist"])), _bits(want))
+    assert np.array_equal(_np(res.per_item), ref.per_item)
+    assert int(_np(res.stats["fixed_point_overflow"])) == 0
+
+
+def test_c2_exact_tallies_bitwise(oracle):
+    print("case: C2 exact N=65536", flush=True)
+    x0, keys, drift = configs.c2_inputs(65_536)
+    outs = {"occ": tm.Sum((128,), fixed_point=True), "wall": tm.Sum((2,), fixed_point=True)}
+    res = _mapped(configs.C2, outs)(x0, keys, drift)
+    _sync()
+    ref, ex = oracle.exact_tallies(lambda: oracle.c2_fwd(x0, keys, drift), [128, 2])
+    assert np.array_equal(_bits(_np(res.outputs["occ"])), _bits(ex[0][0]))
+    assert np.array_equal(_bits(_np(res.outputs["wall"])), _bits(ex[1][0]))
+
+
+def test_c3_exact_global_accumulators_bitwise(oracle):
+    """C3's 64 x 64 exact tally does not fit LDS (40 B per bin): its words take global 64-bit atomics."""
+    print("case: C3 exact N=65536", flush=True)
+    keys, mu_a = configs.c3_inputs(65_536)
+    outs = {"absorbed": tm.Sum((64, 64), fixed_point=True)}
+    res = _mapped(configs.C3, outs)(keys, mu_a)
+    _sync()
+    ref, ex = oracle.exact_tallies(lambda: oracle.c3_fwd(keys, mu_a), [64 * 64])
+    assert np.array_equal(_bits(_np(res.outputs["absorbed"])).ravel(), _bits(ex[0][0]))
+    assert np.array_equal(_np(res.per_item), ref.per_item)
+
+
+def _two_bins(t, x):
+    t = t.add("h", 0, x)
+    return t.add("h", 1, jnp.where(x > 0.5, jnp.inf, x))
+
+
+def test_nonfinite_emit_poisons_its_bin():
+    print("case: exact non-finite emit", flush=True)
+    x = np.linspace(0.0, 1.0, 1000, dtype=np.float32)
+    res = tm.vmap(_two_bins, outputs={"h": tm.Sum((2,), fixed_point=True)}, in_axes=(0,))(x)
+    _sync()
+    h = _np(res.outputs["h"])
+    from oracle import exact as X
+    assert _bits(h[0]) == _bits(X.exact_sum(x)[0])
+    assert np.isnan(h[1])
+    assert int(_np(res.stats["fixed_point_overflow"])) >= 1

@@ -137,3 +137,56 @@ def test_generated_modules_compile_for_gfx950():
         assert L.mode == "step"
         img = Cm.code_object(src)
         assert img[:4] == b"\x7fELF" or len(img) > 1000
+
+
+def test_shift64_helpers_match_native_shifts(tmp_path):
+    """tm_shl64 / tm_shr64 / tm_sar64 (32-bit halves) equal the host's 64-bit shifts for every amount 0..63."""
+    exe = _build("tests/native/shift64_check.cc", str(tmp_path / "shift64_check"))
+    r = subprocess.run([exe], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "0 mismatches", r.stdout
+
+
+def test_shift_hazard_scanner_flags_only_block_end_amount_registers():
+    from tallymap_amd.backend import compile as Cm
+    dis = "\n".join([
+        "0000000000002e00 <tm_main>:",
+        "\tv_lshlrev_b64 v[18:19], v39, v[4:5]                        // 000000003564: D28F0012 00020927",
+        "\tv_lshrrev_b64 v[18:19], v40, v[4:5]                        // 000000003764: D2900012 00020912",
+        "\tv_ashrrev_i64 v[2:3], v7, v[2:3]",
+        "\tv_lshlrev_b64 v[2:3], 7, v[2:3]",
+        "\tv_lshrrev_b32_e32 v15, 7, v15",
+        "0000000000003e00 <tm_post>:",
+        "\tv_lshrrev_b64 v[4:5], v15, v[4:5]"])
+    assert Cm.shift_hazards_in(dis) == [("tm_main", "v_lshlrev_b64 v[18:19], v39, v[4:5]"),
+                                        ("tm_main", "v_ashrrev_i64 v[2:3], v7, v[2:3]"),
+                                        ("tm_post", "v_lshrrev_b64 v[4:5], v15, v[4:5]")]
+
+
+def test_exact_kernels_compile_without_shift_hazards():
+    """the exact-sum kernels of every schedule and accumulator placement compile with no 64-bit shift by a VGPR
+    amount at all (the case gfx950 gets wrong when the amount lands in v(8k+7))."""
+    from tallymap_amd import _core as C
+    from tallymap_amd import configs
+    from tallymap_amd._api import build_program
+    from tallymap_amd.backend import compile as Cm
+    from tallymap_amd.backend import kernel as K
+    import tallymap_amd as tm
+    if Cm.objdump() is None:
+        pytest.skip("llvm-objdump is not installed")
+    args = configs.c1_inputs(8)
+    axes = (0, 0, None)
+    pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
+    bav = [C.AVal(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
+    prog, _ = build_program(configs.C1["item"], {"hist": tm.Sum((16,), fixed_point=True)}, axes, pav, bav, 100)
+    saved = K.LDS_BYTES
+    try:
+        for lds in (saved, 0):
+            K.LDS_BYTES = lds
+            for o in (dict(schedule="item"), dict(), dict(refill=3), dict(block=64), dict(compact=0)):
+                src, _ = K.build(prog, **o)
+                img = Cm.code_object(src)
+                d = subprocess.run([Cm.objdump(), "-d", "--mcpu=gfx950", "/dev/stdin"], input=img,
+                                   capture_output=True, check=True).stdout.decode()
+                assert not re.search(r"v_(lshlrev_b64|lshrrev_b64|ashrrev_i64)\S*\s+v\[\d+:\d+\],\s*v\d+,", d), o
+    finally:
+        K.LDS_BYTES = saved

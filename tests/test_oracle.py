@@ -92,8 +92,9 @@ def test_exact_sum_against_python_integers(oracle):
         assert bad and np.isnan(got)
 
 
-def _c1_python(xs, keys, theta, M=100):
-    """brute-force pure-Python restatement of the quickstart walker on numpy float32 scalars (tiny N)."""
+def _c1_python(xs, keys, theta, M=100, emits=None):
+    """brute-force pure-Python restatement of the quickstart walker on numpy float32 scalars (tiny N); emits: a
+    list of 16 lists that collects every in-range emitted f32 value per bin."""
     from tallymap_amd import random as R
     f32 = np.float32
     hist = np.zeros(16, np.float64)
@@ -105,6 +106,8 @@ def _c1_python(xs, keys, theta, M=100):
             idx = int(np.trunc(np.float32(x * f32(16.0))))
             if 0 <= idx < 16:
                 hist[idx] += float(f32(theta * f32(f32(1.0) - x)))
+                if emits is not None:
+                    emits[idx].append(f32(theta * f32(f32(1.0) - x)))
             x = f32(x * f32(f32(0.5) + f32(f32(0.5) * u)))
             k += 1
         ks.append(k)
@@ -121,6 +124,21 @@ def test_c1_oracle_brute_force(oracle):
     assert np.array_equal(r.trunc, tr)
     assert np.allclose(r.tallies64["hist"], h, rtol=1e-12, atol=0)
     assert np.allclose(r.tallies["hist"], h, rtol=1e-5)
+
+
+def test_oracle_exact_tallies_against_python_integers(oracle):
+    """the oracle's exact tally mode (Sum(fixed_point=True)): each bin equals the Python-integer exact sum of the
+    brute-force walker's emitted f32 values, rounded once (reference tests/edge.py:2038-2065), for any team size."""
+    from tallymap_amd import configs
+    xs, keys, theta = configs.c1_inputs(300)
+    emits = [[] for _ in range(16)]
+    _c1_python(xs, keys, theta, emits=emits)
+    want = np.array([X.exact_sum(np.array(e, np.float32))[0] if e else np.float32(0) for e in emits], np.float32)
+    for nt in (1, 3):
+        _, ex = oracle.exact_tallies(lambda: oracle.c1_fwd(xs, keys, theta, nthreads=nt), [16])
+        got, bad = ex[0]
+        assert not bad.any()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_c1_oracle_truncation_planted(oracle):
