@@ -64,6 +64,9 @@ def lib():
         L.tmref_c5_grad.argtypes = [_p, _p, _p, _f, _i64, _i, _i, _p, _p, _p]
         L.tmref_exact_begin.argtypes = [_i, _p]
         L.tmref_exact_read.argtypes = [_i, _p, _p]
+        L.tmref_wide_begin.argtypes = [_i, _p, _p]
+        L.tmref_wide_read.argtypes = [_i, _p, _p, _p]
+        L.tmref_wide_overflows.restype = _i64
         L.tmref_max_threads.restype = _i
         _lib = L
     return _lib
@@ -311,3 +314,62 @@ def exact_tallies(run, sizes):
     finally:
         lib().tmref_exact_end()
     return r, out
+
+
+_IRANGE = {"int32": (-2.0 ** 31, 2.0 ** 31), "uint32": (0.0, 2.0 ** 32), "int64": (-2.0 ** 63, 2.0 ** 63),
+           "uint64": (0.0, 2.0 ** 64)}
+
+
+def wide_readout(total, bad, scale, dtype):
+    """the output bin of a scaled fixed-point Sum from its exact integer total (reference kernel.py:652-664): the
+    total rounded once to double (Python's int -> float rounds to nearest, ties to even), times the double 1/scale,
+    into `dtype`.  -> (value, counted): counted = the bin adds to fixed_point_overflow at readout (a float total
+    beyond float64 that is not already flagged; an integer total out of range, which saturates)."""
+    dt = np.dtype(dtype)
+    v = float(total) * (1.0 / scale) if abs(total) < 2 ** 1024 else float("inf") * (1 if total > 0 else -1)
+    if dt == np.float64:
+        big = not abs(v) <= 1.7976931348623157e308
+        return (np.float64("nan") if bad or big else np.float64(v)), (big and not bad)
+    lo, hi = _IRANGE[dt.name]
+    out = not (lo <= v < hi)
+    if v != v:
+        x = 0
+    elif v <= lo:
+        x = int(lo)
+    elif v >= hi:
+        x = int(hi) - 1
+    else:
+        x = int(v)                                  # toward zero
+    return np.array(x).astype(dt)[()], out
+
+
+def wide_tallies(run, tallies):
+    """run() (an oracle forward call) with the tallies also summed in scaled fixed point: tallies = [(bins, scale,
+    dtype) or None] per tally slot (None: not summed) -> (run's result, [(values, bad flags, exact integer totals)
+    or None], overflow count: the emits that were not representable plus the bins counted at readout)."""
+    n = len(tallies)
+    sz = np.ascontiguousarray([t[0] if t else 0 for t in tallies], np.int64)
+    sc = np.ascontiguousarray([float(t[1]) if t else 0.0 for t in tallies], np.float64)
+    lib().tmref_wide_begin(n, _ptr(sz), _ptr(sc))
+    try:
+        r = run()
+        out, over = [], int(lib().tmref_wide_overflows())
+        for k, t in enumerate(tallies):
+            if not t:
+                out.append(None)
+                continue
+            bins, scale, dtype = t
+            lo = np.zeros(bins, np.uint64)
+            hi = np.zeros(bins, np.int64)
+            b = np.zeros(bins, np.uint8)
+            lib().tmref_wide_read(k, _ptr(lo), _ptr(hi), _ptr(b))
+            tot = [int(h) * 2 ** 64 + int(l) for l, h in zip(lo, hi)]
+            vals, bad = [], b.astype(bool)
+            for i in range(bins):
+                v, c = wide_readout(tot[i], bool(bad[i]), scale, dtype)
+                vals.append(v)
+                over += int(c)
+            out.append((np.array(vals, dtype=np.dtype(dtype)), bad, tot))
+    finally:
+        lib().tmref_wide_end()
+    return r, out, over

@@ -168,6 +168,7 @@ u32 tmref_bits32(const u32* k) { return bits32(k); }
  * of the reference's exact accumulator (kernel.py:870-941), in an unrelated representation. */
 #define XL 6
 typedef struct { u64 p[XL], n[XL]; int bad; } exsum;
+typedef struct { __int128 s; int bad; } wsum;     /* a scaled fixed-point bin (tmref_wide_begin) */
 
 static void ex_addmag(u64* a, u64 m, unsigned s) {
   unsigned l = s >> 6, b = s & 63u;
@@ -272,6 +273,8 @@ typedef struct {
   float* f[8];
   double* d[8];
   exsum* x[8];            /* per-thread exact sums (tmref_exact_begin) */
+  wsum* w[8];             /* per-thread fixed-point sums (tmref_wide_begin) */
+  i64 wover;
   const tm_tallies* T;
   i64 dropped;
 } tm_thr;
@@ -300,6 +303,43 @@ void tmref_exact_end(void) {
   g_exact = 0;
 }
 
+/* Scaled fixed-point sums of the next forward call's tallies (Sum(fixed_point=True, scale) of a non-f32 dtype,
+ * reference _api.py:55-84): each emit adds round(v * scale) (nearest, ties to even) to a 128-bit integer per bin; an
+ * emit with |v * scale| >= 9.2e18 is not added, flags its bin and is counted.  tmref_wide_begin before the call,
+ * tmref_wide_read per tally after it (the 128-bit totals as low / high words), tmref_wide_end.  The readout (total
+ * rounded once to double, times 1/scale, into the dtype) is test code (oracle/__init__.py). */
+static wsum* g_w[8];
+static i64 g_w_n[8];
+static double g_w_scale[8];
+static int g_wide = 0;
+static i64 g_w_over = 0;
+void tmref_wide_begin(int nt, const i64* sizes, const double* scales) {
+  for (int k = 0; k < nt && k < 8; ++k) {
+    g_w[k] = scales[k] > 0.0 ? (wsum*)calloc((size_t)sizes[k], sizeof(wsum)) : NULL;
+    g_w_n[k] = sizes[k];
+    g_w_scale[k] = scales[k];
+  }
+  g_w_over = 0;
+  g_wide = 1;
+}
+void tmref_wide_read(int k, u64* lo, i64* hi, uint8_t* bad) {
+  for (i64 i = 0; i < g_w_n[k]; ++i) {
+    lo[i] = (u64)(unsigned __int128)g_w[k][i].s;
+    hi[i] = (i64)(g_w[k][i].s >> 64);
+    bad[i] = (uint8_t)g_w[k][i].bad;
+  }
+}
+i64 tmref_wide_overflows(void) { return g_w_over; }
+void tmref_wide_end(void) {
+  for (int k = 0; k < 8; ++k) { free(g_w[k]); g_w[k] = NULL; g_w_n[k] = 0; }
+  g_wide = 0;
+}
+static inline void wide_add(wsum* w, double scale, float v, i64* over) {
+  const double x = (double)v * scale;
+  if (!(fabs(x) < 9.2e18)) { w->bad = 1; ++*over; return; }
+  w->s += (__int128)(i64)rint(x);
+}
+
 /* an IEEE compare-and-swap add (host.py:158-161) */
 static inline void cas_addf(float* a, float v) {
   u32* u = (u32*)a;
@@ -316,6 +356,7 @@ static inline void cas_addd(double* a, double v) {
 static inline void emit(tm_thr* t, int k, i64 idx, float v) {
   if ((u64)idx >= (u64)t->T->size[k]) { t->dropped++; return; }
   if (t->x[k]) ex_add(&t->x[k][idx], v);
+  if (t->w[k]) wide_add(&t->w[k][idx], g_w_scale[k], v, &t->wover);
   if (t->T->priv) t->f[k][idx] += v; else cas_addf(&t->T->out[k][idx], v);
   if (t->d[k]) t->d[k][idx] += (double)v;
   else if (t->T->shadow) cas_addd(&t->T->shadow[k][idx], (double)v);
@@ -328,6 +369,7 @@ static void thr_init(tm_thr* t, const tm_tallies* T) {
     if (T->priv) t->f[k] = (float*)calloc((size_t)T->size[k], sizeof(float));
     if (T->shadow && T->priv) t->d[k] = (double*)calloc((size_t)T->size[k], sizeof(double));
     if (g_exact && g_ex[k]) t->x[k] = (exsum*)calloc((size_t)T->size[k], sizeof(exsum));
+    if (g_wide && g_w[k]) t->w[k] = (wsum*)calloc((size_t)T->size[k], sizeof(wsum));
   }
 }
 
@@ -344,6 +386,18 @@ static void thr_flush(tm_thr* t, i32* stats) {
 #pragma omp critical
       for (i64 i = 0; i < T->size[k]; ++i) ex_merge(&g_ex[k][i], &t->x[k][i]);
       free(t->x[k]);
+    }
+    if (t->w[k]) {
+#pragma omp critical
+      {
+        for (i64 i = 0; i < T->size[k]; ++i) {
+          g_w[k][i].s += t->w[k][i].s;
+          g_w[k][i].bad |= t->w[k][i].bad;
+        }
+        g_w_over += t->wover;
+      }
+      t->wover = 0;
+      free(t->w[k]);
     }
   }
   if (t->dropped) __atomic_fetch_add(&stats[ST_DROPPED], (i32)t->dropped, __ATOMIC_RELAXED);

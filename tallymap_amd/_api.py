@@ -21,6 +21,7 @@ from ._tree import flatten, unflatten
 STATS = ("spawned", "children_dropped", "children_truncated", "fixed_point_overflow", "dropped_emits")
 ST = {n: i for i, n in enumerate(STATS)}
 MAX_ITEMS = 2 ** 31 - 1
+SUM_DTYPES = (C.F32, C.F64, C.I32, C.U32, C.I64, C.U64)
 PROG_CACHE = 64
 OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact", "rev_schedule",
         "rev_tape", "rev_refill")
@@ -36,11 +37,21 @@ class TallyError(TypeError):
 
 @dataclasses.dataclass(frozen=True)
 class Sum:
-    """a commutative (sum) output of `shape` and `dtype` (reference _api.py:55-84).  fixed_point=True with float32
-    is the EXACT sum: each bin the correctly rounded f32 of the exact sum of every finite value emitted into it."""
+    """a commutative (sum) output of `shape` and `dtype` (reference _api.py:55-84); dtype float32, float64, int32,
+    uint32, int64 or uint64.
+
+    fixed_point=True with float32 is the EXACT sum: each bin the correctly rounded f32 of the exact sum of every
+    finite value emitted into it (`scale` unused); a non-finite emit or a total beyond float32 makes the bin NaN,
+    counted in stats['fixed_point_overflow'].
+    fixed_point=True with another dtype accumulates round(v * scale) (nearest, ties to even) in an int64 low word
+    with a signed carry word, so a bin's total is exact past 2^63 / scale and bitwise independent of the order of
+    the emits; the output is that total / scale in `dtype`.  An emit with |v * scale| >= 9.2e18 is dropped, counted
+    in 'fixed_point_overflow', and makes its bin NaN (a float output); a total that does not fit `dtype` is counted
+    there too (a float output is NaN, an integer one saturates)."""
     shape: object
     dtype: object = np.float32
     fixed_point: bool = False
+    scale: float = 2.0 ** 32
 
 
 class Result(collections.namedtuple("Result", "outputs per_item truncated stats")):
@@ -55,6 +66,8 @@ class TSpec:
     dtype: np.dtype
     exact: bool = False
     kind: str = "sum"          # 'sum' | 'discard' (a derived program's tally that is not output)
+    fixed: bool = False        # the scaled fixed-point sum (Sum(fixed_point=True) of a dtype other than float32)
+    scale: float = 0.0
 
     @property
     def S(self):
@@ -202,8 +215,8 @@ def _jx_key(jx):
 def digest(jx, tallies=(), extra=()):
     """structural sha256 of a program (reference _jaxpr.py:301-309): variable names are canonical, literals by
     their bytes."""
-    h = hashlib.sha256(repr((_jx_key(jx), tuple((s.name, s.shape, s.dtype.name, s.exact, s.kind)
-                                                  for s in tallies), extra)).encode())
+    h = hashlib.sha256(repr((_jx_key(jx), tuple((s.name, s.shape, s.dtype.name, s.exact, s.kind, s.fixed,
+                                                   s.scale) for s in tallies), extra)).encode())
     return h.hexdigest()
 
 
@@ -239,12 +252,17 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         s = outs_spec[n]
         shape = (s.shape,) if isinstance(s.shape, int) else tuple(s.shape)
         dt = np.dtype(s.dtype)
+        if dt not in SUM_DTYPES:
+            raise UnsupportedError(f"tallymap: Sum output {n!r} of dtype {dt}: supported are "
+                                   f"{', '.join(d.name for d in SUM_DTYPES)}")
         exact = bool(s.fixed_point) and dt == C.F32
-        if s.fixed_point and not exact:
-            raise UnsupportedError("tallymap: Sum(fixed_point=True) is supported for float32 (the exact sum) only")
+        fixed = bool(s.fixed_point) and not exact
+        scale = float(s.scale) if fixed else 0.0
+        if fixed and not (np.isfinite(scale) and scale > 0.0):
+            raise ValueError(f"tallymap: Sum output {n!r}: scale must be finite and positive, got {s.scale!r}")
         if int(np.prod(shape, dtype=np.int64)) > MAX_ITEMS:
             raise ValueError(f"tallymap: output {n!r} has more than 2^31 - 1 cells")
-        tspecs.append(TSpec(n, shape, dt, exact))
+        tspecs.append(TSpec(n, shape, dt, exact, fixed=fixed, scale=scale))
     where = item_name(fn)
     tav = [C.AVal((s.S,), s.dtype) for s in tspecs]
     shapes = {s.name: s.shape for s in tspecs}

@@ -325,6 +325,8 @@ def _coerce(x, dt, weak):
         if x.dtype != dt:
             return convert(x, dt, weak=weak).var
         return x.var
+    if _pyscalar(x):       # a Python scalar takes the operation's dtype at full precision (JAX's weak typing)
+        return Lit(np.asarray(x).astype(dt), AVal((), dt, weak=True))
     v = literal(x)
     return Lit(v.val.astype(dt), AVal(v.aval.shape, dt, weak=v.aval.weak))
 
@@ -351,6 +353,8 @@ def binop(prim, a, b):
 def _aval(x):
     if isinstance(x, Tracer):
         return x.aval
+    if _pyscalar(x):       # (its value is converted once, to the operation's dtype: _coerce)
+        return AVal((), BOOL if isinstance(x, (bool, np.bool_)) else (I32 if isinstance(x, int) else F32), True)
     return literal(x).aval
 
 

@@ -229,6 +229,11 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
         hit = _ADJ[key] = (adj, R.plan(adj))
     adj, pl = hit
     yav = prog.y_avals()
+    wide = [prog.tallies[k].name for k in (ct_tallies or {}) if prog.tallies[k].dtype == np.float64]
+    wide += [f"per-item result {j}" for j in (ct_ys or {}) if yav[j].dtype == np.float64]
+    if wide:
+        raise Cm.BackendError(f"tallymap_amd: reverse mode through float64 outputs ({', '.join(wide)}) is not "
+                              "supported by this backend (float32 outputs and per-item results only)")
     ins_p = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
     for j in pl.fy:
         x = ct_ys.get(j) if ct_ys else None

@@ -87,6 +87,37 @@ def exact_words(S):
     return 2 * XW * S + (S + 31) // 32
 
 
+def wide_words(S):
+    """u32 words of a scaled fixed-point tally's scratch: per bin a u64 low word, then an i32 carry word per bin,
+    then a u32 flag per bin (reference kernel.py:952-956)."""
+    return 4 * S
+
+
+def scratch_words(s):
+    return exact_words(s.S) if s.exact else wide_words(s.S)
+
+
+_IRANGE = {"int32": ("-2147483648.0", "2147483648.0", "tm_d2i32"), "uint32": ("0.0", "4294967296.0", "tm_d2u32"),
+           "int64": ("-9223372036854775808.0", "9223372036854775808.0", "tm_d2i64"),
+           "uint64": ("0.0", "18446744073709551616.0", "tm_d2u64")}
+
+
+def _wide_readout(s, lo, cw, fl, out):
+    """tm_post's readout of a scaled fixed-point tally (reference kernel.py:652-664): the exact total rounded once
+    to double, times 1/scale, in the output dtype.  A total that does not fit is counted in fixed_point_overflow
+    (unless the bin is already flagged); a float bin is NaN when flagged or too big, an integer one saturates."""
+    v = f"tm_wide_f64({lo}[i], {cw}[i]) * {lit(1.0 / s.scale, np.float64)}"
+    if s.dtype == C.F64:
+        return (f"for (i64 i = g; i < {s.S}; i += st) {{ const double v = {v}; "
+                f"const bool big = !(__builtin_fabs(v) <= 1.7976931348623157e308); "
+                f"if (big && !{fl}[i]) atomicAdd(&TM_STATS[3], 1); "
+                f"((double*){out})[i] = ({fl}[i] || big) ? __builtin_nan(\"\") : v; }}")
+    lo_, hi_, cv = _IRANGE[s.dtype.name]
+    ct = ctype(s.dtype)
+    return (f"for (i64 i = g; i < {s.S}; i += st) {{ const double v = {v}; "
+            f"if (!(v >= {lo_} && v < {hi_})) atomicAdd(&TM_STATS[3], 1); (({ct}*){out})[i] = ({ct}){cv}(v); }}")
+
+
 _W64 = {"i64", "u64", "double"}
 
 
@@ -142,7 +173,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         return n_in + len(res) - 1
     outs = prog.out_tallies
     r_out = {k: result(prog.tallies[k].shape, prog.tallies[k].dtype) for k in outs}
-    r_scr = {k: result((exact_words(prog.tallies[k].S),), np.uint32) for k in outs if prog.tallies[k].exact}
+    r_scr = {k: result((scratch_words(prog.tallies[k]),), np.uint32) for k in outs
+             if prog.tallies[k].exact or prog.tallies[k].fixed}
     r_ctl = result((8,), np.uint32)
     r_stats = result((5,), np.int32)
     n_zero = len(res)
@@ -154,9 +186,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     budget = LDS_BYTES
     for k in outs:
         s = prog.tallies[k]
-        nbytes = s.S * (8 * XW if s.exact else 4)
-        if s.dtype not in (C.F32, C.I32, C.U32) and not s.exact:
-            continue
+        nbytes = s.S * (8 * XW if s.exact else (12 if s.fixed else np.dtype(s.dtype).itemsize))
         if nbytes <= budget:
             budget -= nbytes
             priv.append(k)
@@ -192,15 +222,28 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             acc = f"tm_xsh{k}" if k in priv else f"((u64*)P.p[{r_scr[k]}])"
             fl = f"tm_xfl{k}" if k in priv else f"((u32*)P.p[{r_scr[k]}] + {2 * XW * s.S})"
             em_.line(f"if (tm_xemit(&{acc}[(i64){ei} * {XW}], {v})) atomicOr(&{fl}[{ei} >> 5], 1u << ({ei} & 31));")
+        elif s.fixed:
+            lo = f"tm_wsh{k}" if k in priv else f"((u64*)P.p[{r_scr[k]}])"
+            cw = f"tm_wsc{k}" if k in priv else f"((i32*)P.p[{r_scr[k]}] + {2 * s.S})"
+            em_.line(f"if (!tm_wemit(&{lo}[{ei}], &{cw}[{ei}], (double){v}, {lit(s.scale, np.float64)})) {{ "
+                     f"atomicAdd(&TM_STATS[3], 1); ((u32*)P.p[{r_scr[k]}] + {3 * s.S})[{ei}] = 1u; }}")
         elif s.dtype == C.F32:
             if k in priv:
                 em_.line(f"tm_ladd_f32(&tm_sh{k}[{ei}], {v});")
             else:
                 em_.line(f"tm_gadd_f32(&((float*)P.p[{r_out[k]}])[{ei}], {v});")
+        elif s.dtype == C.F64:
+            if k in priv:
+                em_.line(f"tm_ladd_f64(&tm_sh{k}[{ei}], {v});")
+            else:
+                em_.line(f"tm_gadd_f64(&((double*)P.p[{r_out[k]}])[{ei}], {v});")
         elif s.dtype in (C.I32, C.U32):
             ct = ctype(s.dtype)
             dst = f"tm_sh{k}" if k in priv else f"(({ct}*)P.p[{r_out[k]}])"
             em_.line(f"atomicAdd(&{dst}[{ei}], {v});")
+        elif s.dtype in (C.I64, C.U64):
+            dst = f"tm_sh{k}" if k in priv else f"((u64*)P.p[{r_out[k]}])"
+            em_.line(f"tm_gadd_u64((u64*)&{dst}[{ei}], (u64){v});")
         else:
             raise NotImplementedError(f"sum output of dtype {s.dtype}")
         em_.close()
@@ -361,7 +404,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         zero_words.append((r_out[k], s.S * np.dtype(s.dtype).itemsize // 4 if np.dtype(s.dtype).itemsize >= 4
                            else (s.S * np.dtype(s.dtype).itemsize + 3) // 4))
         if k in r_scr:
-            zero_words.append((r_scr[k], exact_words(s.S)))
+            zero_words.append((r_scr[k], scratch_words(s)))
     zero_words += [(r_ctl, 8), (r_stats, 5)]
     zl = []
     for b, nw in zero_words:
@@ -382,6 +425,9 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                         f"const bool f = (({fl}[i >> 5] >> (i & 31)) & 1u) != 0u; "
                         f"if (f || bad) atomicAdd(&TM_STATS[3], 1); "
                         f"((float*)P.p[{r_out[k]}])[i] = (f || bad) ? __builtin_nanf(\"\") : o; }}")
+        elif s.fixed:
+            post.append(_wide_readout(s, f"((const u64*)P.p[{r_scr[k]}])", f"((const i32*)P.p[{r_scr[k]}] + {2 * s.S})",
+                                      f"((const u32*)P.p[{r_scr[k]}] + {3 * s.S})", f"P.p[{r_out[k]}]"))
     poison = [k for k in outs if prog.tallies[k].dtype in (C.F32, C.F64)]
     if prog.trunc is not None and poison:
         # (the readout and the poison visit a bin from the same thread, in program order)
@@ -420,6 +466,11 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             body.append(f"  __shared__ u32 tm_xfl{k}[{(s.S + 31) // 32}];")
             body.append(f"  for (int i = threadIdx.x; i < {nw}; i += blockDim.x) tm_xsh{k}[i] = 0ull;")
             body.append(f"  for (int i = threadIdx.x; i < {(s.S + 31) // 32}; i += blockDim.x) tm_xfl{k}[i] = 0u;")
+        elif s.fixed:
+            body.append(f"  __shared__ u64 tm_wsh{k}[{s.S}];")
+            body.append(f"  __shared__ i32 tm_wsc{k}[{s.S}];")
+            body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ tm_wsh{k}[i] = 0ull; "
+                        f"tm_wsc{k}[i] = 0; }}")
         else:
             ct = ctype(s.dtype)
             body.append(f"  __shared__ {ct} tm_sh{k}[{s.S}];")
@@ -579,6 +630,20 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                             f"atomicOr(&{gf}[(i / {XW}) >> 5], 1u << ((i / {XW}) & 31)); }}")
                 body.append(f"  for (int i = threadIdx.x; i < {(s.S + 31) // 32}; i += blockDim.x) "
                             f"if (tm_xfl{k}[i]) atomicOr(&{gf}[i], tm_xfl{k}[i]);")
+            elif s.fixed:
+                # a block's copy: its low word added with the carry it makes, plus the block's own carries
+                glo = f"((u64*)P.p[{r_scr[k]}])"
+                gc = f"((i32*)P.p[{r_scr[k]}] + {2 * s.S})"
+                body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const u64 x = tm_wsh{k}[i]; "
+                            f"const i32 c = tm_wsc{k}[i]; if (x != 0ull) tm_wadd(&{glo}[i], &{gc}[i], (i64)x); "
+                            f"if (c != 0) atomicAdd(&{gc}[i], c); }}")
+            elif s.dtype == C.F64:
+                body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const double x = tm_sh{k}[i]; "
+                            f"if (x != 0.0) tm_gadd_f64(&((double*)P.p[{r_out[k]}])[i], x); }}")
+            elif s.dtype in (C.I64, C.U64):
+                ct = ctype(s.dtype)
+                body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const {ct} x = tm_sh{k}[i]; "
+                            f"if (x != 0) tm_gadd_u64(&((u64*)P.p[{r_out[k]}])[i], (u64)x); }}")
             elif s.dtype == C.F32:
                 body.append(f"  for (int i = threadIdx.x; i < {s.S}; i += blockDim.x) {{ const float x = tm_sh{k}[i]; "
                             f"if (x != 0.0f) tm_gadd_f32(&((float*)P.p[{r_out[k]}])[i], x); }}")

@@ -198,6 +198,32 @@ TM_DFN void tm_ladd_f32(float* a, float v) {       // a: LDS
   tm_lds_cas_addf(a, v);
 }
 TM_DFN void tm_gadd_i32(i32* a, i32 v) { atomicAdd(a, v); }
+// f64 atomic adds that keep subnormals: a CAS loop of the IEEE add below 2^-970 (where a sum of two addends can
+// be subnormal), the native add above
+TM_DFN void tm_cas_addd(double* a, double v) {
+  u64* const u = (u64*)a;
+  u64 o = __hip_atomic_load(u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), w;
+  do {
+    w = o;
+    o = atomicCAS((unsigned long long*)u, (unsigned long long)w, (unsigned long long)tm_d2u(tm_u2d(w) + v));
+  } while (o != w);
+}
+TM_DFN void tm_gadd_f64(double* a, double v) {
+  if (v == 0.0) return;
+  if (!(__builtin_fabs(v) < 0x1p-970)) { unsafeAtomicAdd(a, v); return; }
+  tm_cas_addd(a, v);
+}
+TM_DFN void tm_ladd_f64(double* a, double v) {     // a: LDS
+  if (v == 0.0) return;
+  if (!(__builtin_fabs(v) < 0x1p-970)) { atomicAdd(a, v); return; }
+  u64* const u = (u64*)a;
+  u64 o = *(volatile u64*)u, w;
+  do {
+    w = o;
+    o = atomicCAS((unsigned long long*)u, (unsigned long long)w, (unsigned long long)tm_d2u(tm_u2d(w) + v));
+  } while (o != w);
+}
+TM_DFN void tm_gadd_u64(u64* a, u64 v) { atomicAdd((unsigned long long*)a, (unsigned long long)v); }
 
 #endif  // device only
 
@@ -294,3 +320,63 @@ TM_FN float tm_xread(const u64* a, bool* bad) {
   const float f = (float)o;
   return neg ? -f : f;
 }
+
+// --------------------------------------------------------------------- the scaled fixed-point sum (WIDE)
+// A bin is an int64 low word (two's complement, wrapping) and an i32 carry word, the net signed carry out of the
+// low word: an add of q whose old value o wraps (q > 0 and o + q < o: +1; q < 0 and o + q > o: -1) adds its carry,
+// so the exact total low + carry * 2^64 does not depend on the order of the adds.  An emit adds round(v * scale)
+// (nearest, ties to even); |v * scale| >= 9.2e18 is not representable: the emit is dropped and flags its bin
+// (reference kernel.py:844-869, _api.py:55-84).  `add(lo, q)` adds q and returns the old value.
+template <class Add> TM_FN int tm_wadd_with(u64* lo, i64 q, Add add) {      // -> the carry: -1, 0 or +1
+  const i64 o = add(lo, q);
+  const i64 r = (i64)((u64)o + (u64)q);
+  return (q > 0 && r < o) ? 1 : ((q < 0 && r > o) ? -1 : 0);
+}
+// round(v * scale) -> *q; false when not representable
+TM_FN bool tm_wvalue(double v, double scale, i64* q) {
+  const double x = v * scale;
+  if (!(__builtin_fabs(x) < 9.2e18)) return false;
+  *q = (i64)__builtin_rint(x);
+  return true;
+}
+// low + carry * 2^64 rounded once to double (nearest, ties to even)
+TM_FN double tm_wide_f64(u64 lo, i32 c) {
+  if (c == 0) return (double)(i64)lo;
+  u64 h = (u64)((i64)c - (i64)(lo >> 63)), l = lo;       // the 128-bit two's complement h:l
+  const bool neg = (i64)h < 0;
+  if (neg) {
+    l = ~l + 1ull;
+    h = ~h + (l == 0ull ? 1ull : 0ull);
+  }
+  if (h == 0ull) {
+    const double m = (double)l;
+    return neg ? -m : m;
+  }
+  const int e = 64 - __builtin_clzll(h);                   // the magnitude has 64 + e bits
+  const u64 t = e == 64 ? h : (tm_shl64(h, (u32)(64 - e)) | tm_shr64(l, (u32)e));   // its top 64 bits
+  const u64 sticky = e == 64 ? l : tm_shl64(l, (u32)(64 - e));                      // the bits below them
+  const double m = (double)(t | (sticky != 0ull ? 1ull : 0ull)) * tm_u2d((u64)(1023 + e) << 52);
+  return neg ? -m : m;
+}
+TM_FN u64 tm_d2u64(double x) {
+  return x != x ? 0ull : (x <= 0.0 ? 0ull : (x >= 18446744073709551616.0 ? ~0ull : (u64)x));
+}
+
+#if defined(__HIP__) || defined(__HIPCC_RTC__)
+struct TmAtomicAddW {
+  __device__ i64 operator()(u64* a, i64 q) const {
+    return (i64)atomicAdd((unsigned long long*)a, (unsigned long long)q);
+  }
+};
+TM_DFN void tm_wadd(u64* lo, i32* c, i64 q) {
+  const int k = tm_wadd_with(lo, q, TmAtomicAddW());
+  if (k) atomicAdd(c, k);
+}
+// one emit of v: false when v * scale is not representable (the caller counts it and flags the bin)
+TM_DFN bool tm_wemit(u64* lo, i32* c, double v, double scale) {
+  i64 q = 0;
+  if (!tm_wvalue(v, scale, &q)) return false;
+  if (q != 0) tm_wadd(lo, c, q);
+  return true;
+}
+#endif  // device only

@@ -36,6 +36,20 @@ def test_weak_types_follow_jax():
     assert all(e.outvars[0].aval.dtype in (np.float32, np.int32, np.bool_) for e in p.jaxpr.eqns)
 
 
+def test_python_scalars_take_the_operand_dtype_at_full_precision():
+    """a Python float meeting a float64 operand (or a Python int meeting an int64 one) becomes a constant of that
+    dtype directly, not through float32 / int32 (JAX's weak typing)."""
+    def item(t, x, n):
+        t = t.add("f", 0, x * 4e18 + 0.1)
+        return t.add("i", 0, n * 4_000_000_000_000_000_000)
+    p = _prog(item, {"f": tm.Sum((1,), np.float64), "i": tm.Sum((1,), np.int64)},
+              [((), np.float64), ((), np.int64)], [], (0, 0))
+    lits = [v.val for e in p.jaxpr.eqns for v in e.invars if isinstance(v, C.Lit) and v.aval.shape == ()]
+    assert any(x.dtype == np.float64 and x == 4e18 for x in lits)
+    assert any(x.dtype == np.float64 and x == 0.1 for x in lits)
+    assert any(x.dtype == np.int64 and x == 4_000_000_000_000_000_000 for x in lits)
+
+
 def test_tally_read_fork_drop_raise():
     def forked(t, x):
         t1 = t.add("h", 0, x)

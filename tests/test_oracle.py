@@ -141,6 +141,39 @@ def test_oracle_exact_tallies_against_python_integers(oracle):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_oracle_fixed_point_tallies_against_python_integers(oracle):
+    """the oracle's scaled fixed-point mode (Sum(fixed_point=True, scale) of a non-f32 dtype): each bin's integer
+    total equals the Python sum of round-half-even(v * scale) over the brute-force walker's emits, for scales that
+    keep every emit exact (2^32), round them (16, 2^-1: many emits round to 0 or ties) and overflow every emit
+    (1e21: all bins NaN, one count per emit); the readout is total * (1/scale) for float64 and saturates integer
+    dtypes."""
+    from tallymap_amd import configs
+    xs, keys, theta = configs.c1_inputs(300)
+    emits = [[] for _ in range(16)]
+    _c1_python(xs, keys, theta, emits=emits)
+    n_emits = sum(len(e) for e in emits)
+    for scale in (2.0 ** 32, 16.0, 0.5):
+        want = [sum(round(float(v) * scale) for v in e) for e in emits]
+        for nt in (1, 3):
+            _, out, over = oracle.wide_tallies(lambda: oracle.c1_fwd(xs, keys, theta, nthreads=nt),
+                                               [(16, scale, np.float64)])
+            vals, bad, tot = out[0]
+            assert tot == want and not bad.any() and over == 0
+            assert np.array_equal(vals, np.array([float(t) * (1.0 / scale) for t in want]))
+    _, out, over = oracle.wide_tallies(lambda: oracle.c1_fwd(xs, keys, theta), [(16, 1e21, np.float64)])
+    vals, bad, tot = out[0]
+    assert over == n_emits and all(bad == np.array([len(e) > 0 for e in emits])) and tot == [0] * 16
+    assert np.isnan(vals[bad]).all()
+    # the readout into integer dtypes: truncation toward zero, saturation counted
+    assert oracle.wide_readout(7, False, 2.0, np.int32) == (3, False)
+    assert oracle.wide_readout(-7, False, 2.0, np.int32) == (-3, False)
+    assert oracle.wide_readout(2 ** 40, False, 1.0, np.int32) == (2 ** 31 - 1, True)
+    assert oracle.wide_readout(-1, False, 1.0, np.uint32) == (0, True)
+    assert oracle.wide_readout(2 ** 70, False, 1.0, np.uint64) == (2 ** 64 - 1, True)
+    v, c = oracle.wide_readout(2 ** 100, False, 2.0 ** -1000, np.float64)
+    assert np.isnan(v) and c
+
+
 def test_c1_oracle_truncation_planted(oracle):
     """a tiny max_steps truncates items: trip counts hit the cap, truncation flags are set; a planted mistake in
     the cap (one step more) is visible in the counts."""
