@@ -150,6 +150,22 @@ def bench_configs(steps, warmup, with_cpu):
              "fwd_items_per_s": n / (fwd_ms * 1e-3), "grad_items_per_s": n / (grad_ms * 1e-3),
              "mean_trip_count": float(r.per_item.double().mean().item()),
              "max_trip_count": int(r.per_item.max().item())}
+        # forward mode: one fused primal + tangent launch, tangent 1 on the gradient's broadcast parameter
+        import tallymap_amd as tm
+        pos = {"c1": 2, "c3": 1, "c4": 3, "c5": 3}[name]
+        tans = tuple(torch.ones((), dtype=torch.float32, device="cuda") if i == pos else None
+                     for i in range(len(dev)))
+        for _ in range(warmup):
+            tm.jvp(f, dev, tans)
+        torch.cuda.synchronize()
+        jev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+        for e in jev:
+            e[0].record(stream)
+            tm.jvp(f, dev, tans)
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        d["jvp_ms"] = float(np.mean([e[0].elapsed_time(e[1]) for e in jev]))
+        d["jvp_items_per_s"] = n / (d["jvp_ms"] * 1e-3)
         if with_cpu:
             v, m, dt = _cpu_sample(name, inputs, 8.0)
             d["cpu_items_per_s"] = v

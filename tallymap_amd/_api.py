@@ -472,3 +472,128 @@ def grad(mapped, weights=None, argnums=None):
         return _pullback(mapped, args, argnums)(
             weights if weights is not None else {n: 1.0 for n in mapped._names})
     return g
+
+
+# ----------------------------------------------------------------------------------------- forward mode
+MAX_LANES = 16                 # tangent directions per jacfwd kernel (reference: dual lanes <= 16 per kernel)
+_JVP = collections.OrderedDict()
+
+
+def _jvp_prog(prog, pp, pb, lanes):
+    from ._fwd import jvp_program
+    key = (prog.digest(), pp, pb, lanes)
+    q = _JVP.get(key)
+    if q is None:
+        q = _JVP[key] = jvp_program(prog, pp, pb, lanes)
+        while len(_JVP) > PROG_CACHE:
+            _JVP.popitem(last=False)
+    return q
+
+
+def _run_tangents(mapped, args, tans, lanes):
+    """one launch of the jvp program with `lanes` directions.  tans[pos]: None or a list of `lanes` tangent arrays
+    for positional argument pos (its shape) -> (primal Result, per lane {name: tangent tally}, per lane [tangents
+    of the float per-item results (None for the others)])."""
+    from . import backend as B
+    prog, meta, pi, bc, N, axes = mapped._prepare(args)
+    pt, bt, pp, pb = [], [], [], []
+    for pos, x in enumerate(axes):
+        leaves, _ = flatten(args[pos])
+        tl = tans[pos]
+        for j, leaf in enumerate(leaves):
+            dt = _np_dtype(leaf)
+            on = tl is not None and np.issubdtype(dt, np.floating)
+            (pp if x == 0 else pb).append(on)
+            if on:
+                for t in tl:
+                    tleaves, _ = flatten(t)
+                    (pt if x == 0 else bt).append(tleaves[j])
+    q = _jvp_prog(prog, tuple(pp), tuple(pb), lanes)
+    o = B.run(q, list(pi) + pt, list(bc) + bt, N, mapped._opts)
+    names = mapped._names
+    nT = prog.nT
+    res_out = {n: o.tallies[i].reshape(prog.tallies[i].shape) for i, n in enumerate(names)}
+    ny = len(prog.y_avals())
+    ys = list(o.ys[:ny])
+    trunc = ys.pop() if prog.trunc is not None else None
+    stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
+    stats["n_truncated"] = o.n_truncated
+    primal = Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
+    t_tal = [dict() for _ in range(lanes)]
+    k = nT
+    for slot in q.tangent_tallies:
+        for l in range(lanes):
+            if prog.tallies[slot].kind == "sum":
+                t_tal[l][prog.tallies[slot].name] = o.tallies[k].reshape(prog.tallies[slot].shape)
+            k += 1
+    t_ys = [[None] * ny for _ in range(lanes)]
+    m = ny
+    for j in q.tangent_ys:
+        for l in range(lanes):
+            t_ys[l][j] = o.ys[m]
+            m += 1
+    if prog.trunc is not None:
+        for l in range(lanes):
+            t_ys[l].pop(prog.trunc)
+    return primal, t_tal, [unflatten(meta["ytree"], t) for t in t_ys], meta
+
+
+def jvp(mapped, primals, tangents):
+    """(Result, tangent Result): the forward-mode derivative of the mapped call along `tangents` (jax.jvp of a
+    tallymap call, reference _api.py:305-345, _primitive.py:419-436).  primals: the positional arguments;
+    tangents: one per argument, None (not perturbed) or an array (pytree) of the argument's shape; only float
+    leaves are perturbed.  The tangent Result holds the tangent of every float output and of every float per-item
+    result (None for the others); ONE launch of the fused jvp kernel (primal and tangents in one pass)."""
+    primals, tangents = tuple(primals), tuple(tangents)
+    if len(tangents) != len(primals):
+        raise ValueError("tallymap: jvp needs one tangent (or None) per primal argument")
+    primal, t_tal, t_ys, _ = _run_tangents(mapped, primals, [None if t is None else [t] for t in tangents], 1)
+    return primal, Result(t_tal[0], t_ys[0], None, None)
+
+
+def jacfwd(mapped, argnums=0):
+    """the forward-mode Jacobian of every float output w.r.t. the BROADCAST float arguments in argnums (jax.jacfwd
+    of a tallymap call): -> f(*args) -> {name: {argnum: array of shape output.shape + arg.shape}}.  The unit
+    tangents of the argument's elements run as dual lanes, up to 16 per fused kernel."""
+    an = (argnums,) if isinstance(argnums, int) else tuple(argnums)
+
+    def jac(*args):
+        prog, meta, pi, bc, N, axes = mapped._prepare(args)
+        dirs = []
+        for a in an:
+            if axes[a] == 0:
+                raise UnsupportedError("tallymap: jacfwd is supported w.r.t. broadcast (in_axes=None) arguments; "
+                                       "use jvp for a per-item argument")
+            x = np.asarray(args[a])
+            if not np.issubdtype(x.dtype, np.floating):
+                raise TypeError(f"tallymap: jacfwd w.r.t. argument {a} of dtype {x.dtype}")
+            for i in range(x.size):
+                e = np.zeros(x.size, x.dtype)
+                e[i] = 1
+                dirs.append((a, e.reshape(x.shape)))
+        cols = {n: [] for n in mapped._names}
+        for s in range(0, len(dirs), MAX_LANES):
+            chunk = dirs[s:s + MAX_LANES]
+            tans = [None] * len(args)
+            for a in an:
+                lanes = [d if aa == a else np.zeros_like(np.asarray(args[a])) for aa, d in chunk]
+                tans[a] = lanes
+            _, t_tal, _, _ = _run_tangents(mapped, args, tans, len(chunk))
+            for l in range(len(chunk)):
+                for n in mapped._names:
+                    if n in t_tal[l]:
+                        cols[n].append(t_tal[l][n])
+        out = {}
+        import torch
+        for n, cs in cols.items():
+            if not cs:
+                continue
+            full = torch.stack(cs, dim=-1)
+            per, k = {}, 0
+            for a in an:
+                sz = int(np.asarray(args[a]).size)
+                per[a] = full[..., k:k + sz].reshape(tuple(full.shape[:-1]) + np.shape(args[a]))
+                k += sz
+            out[n] = per
+        return out
+    return jac

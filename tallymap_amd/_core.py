@@ -121,7 +121,8 @@ class Builder:
         self.parent = parent
         self.eqns = []
         self.invars = []
-        self.captured = []          # outer Vars captured, in order
+        self.captured = []          # outer Vars captured, in order (Vars of the parent builder)
+        self.cap_local = []         # the local Var standing for each of them
         self.env = {}               # outer Var -> local Var
         self.owned = set()          # ids of Vars defined in this builder
 
@@ -143,6 +144,7 @@ class Builder:
         v = Var(var.aval)
         self.owned.add(v.id)
         self.captured.append(outer)
+        self.cap_local.append(v)
         self.env[var.id] = v
         return v
 

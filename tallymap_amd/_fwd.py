@@ -1,0 +1,313 @@
+"""Forward-mode differentiation of item programs: the jvp / jacfwd programs (reference _api.py:305-345 builds them
+with jax.jvp on the item; _primitive.py:419-436, 693-801 runs them as fused tangent kernels).
+
+jvp_jaxpr(jx, tin, lanes) builds a program that takes jx's inputs and, for every input flagged in `tin`, `lanes`
+tangents, and returns jx's outputs followed by `lanes` tangents of every output that has one.  `lanes` > 1 carries
+several tangent directions through one program (the dual lanes of jacfwd): each direction has its own tangent
+variables, loop carries and tangent tallies, all advanced in the same pass over the item.
+
+  * elementwise primitives: the tangent is sum_i d f / d x_i * t_i, each term the reverse-mode rule of _ad.py applied
+    to t_i (the rules are JAX's derivatives: lax.py jvp rules);
+  * structural linear primitives (copy, slice, reshape, broadcast_in_dim, concatenate) and select_n: the same
+    operation on the tangents;
+  * an emit `t.add(name, i, v)` emits v's tangent into the tangent tally at the same index (an index out of range is
+    dropped there too); every float tally has a tangent tally, of the same format (exact, fixed point, plain);
+  * while: carries are extended by the tangents of the carries that become active (a fixed point over the body);
+    the cond ignores them.  cond: every branch gets the same tangent inputs and returns the union of tangents;
+  * comparisons, integer arithmetic, threefry, floor / ceil / round / sign and stop_gradient have no tangent.
+"""
+import numpy as np
+
+from . import _ad as A
+from . import _core as C
+from . import lax as L
+
+STRUCT = {"copy", "slice", "squeeze", "reshape", "broadcast_in_dim", "concatenate"}
+
+
+def _isf(aval):
+    return aval.dtype in (C.F32, C.F64)
+
+
+def _zero(aval):
+    z = np.zeros(aval.shape, aval.dtype)
+    return C.Tracer(C.bind("copy", [C.Lit(z, aval.strong())], [aval.strong()])[0].var)
+
+
+def _sum(a, b):
+    if a is None:
+        return b
+    if b is None:
+        return a
+    return a + b
+
+
+def _fit(t, aval):
+    """tangent t as aval's dtype and shape (a scalar tangent of an operand broadcast against an array stays scalar
+    only when the output is scalar)."""
+    if t is None:
+        return None
+    if not C.is_traced(t):
+        a = np.broadcast_to(np.asarray(t, aval.dtype), aval.shape).copy()
+        return C.Tracer(C.bind("copy", [C.Lit(a, aval.strong())], [aval.strong()])[0].var)
+    if t.dtype != aval.dtype:
+        t = C.convert(t, aval.dtype)
+    if t.shape != aval.shape:
+        t = C.Tracer(C.bind("broadcast_in_dim", [t.var], [aval.strong()], shape=aval.shape,
+                            broadcast_dimensions=())[0].var) if t.shape == () else t
+    return t
+
+
+def _tan_rule(ts, ins, outs, e):
+    return [ts[0] * (1.0 + outs[0] * outs[0])] if ts[0] is not None else [None]
+
+
+def _rem_rule(ts, ins, outs, e):
+    from . import numpy as jnp
+    x, y = ins
+    t = ts[0]
+    if ts[1] is not None:
+        q = x / y
+        t = _sum(t, -ts[1] * (jnp.sign(q) * L.floor(jnp.abs(q))))
+    return [t]
+
+
+EXTRA = {"tan": _tan_rule, "rem": _rem_rule}
+
+
+def _elementwise(e, ins, outs, ts):
+    """sum over the operands with a tangent of the reverse rule applied to that tangent alone."""
+    if e.prim in EXTRA:
+        return EXTRA[e.prim](ts, ins, outs, e)
+    rule = A.RULES.get(e.prim)
+    if rule is None:
+        raise A.ADError(f"no forward-mode rule for `{e.prim}`")
+    acc = [None] * len(e.outvars)
+    for i, t in enumerate(ts):
+        if t is None:
+            continue
+        parts = rule([t], ins, outs, e)
+        acc[0] = _sum(acc[0], parts[i])
+    return acc
+
+
+def _jvp_eqn(e, ins, tins, lanes):
+    """-> (primal outputs, [per output: list of `lanes` tangents or None])."""
+    if e.prim == "while":
+        return _jvp_while(e, ins, tins, lanes)
+    if e.prim == "cond":
+        return _jvp_cond(e, ins, tins, lanes)
+    outs = A._replay(e, ins)
+    if e.prim == "tallymap_emit":
+        tt, tv = tins[0], tins[2]
+        if tt is None:
+            if tv is not None:
+                raise A.ADError("internal: an emit of a perturbed value into a tally without a tangent tally")
+            return outs, [None]
+        if tv is None:
+            return outs, [list(tt)]
+        return outs, [[A._replay(e, [tt[l], ins[1], tv[l]])[0] for l in range(lanes)]]
+    if all(t is None for t in tins):
+        return outs, [None] * len(outs)
+    if e.prim in A.ZERO_D or not any(_isf(o.aval) for o in e.outvars):
+        return outs, [None] * len(outs)
+    if e.prim == "convert_element_type":
+        if not _isf(e.outvars[0].aval):
+            return outs, [None]
+        return outs, [[C.convert(t, e.outvars[0].aval.dtype) for t in tins[0]]]
+    if e.prim in STRUCT:
+        res = []
+        for l in range(lanes):
+            ops = [t[l] if t is not None else _zero(v.aval) for t, v in zip(tins, e.invars)]
+            res.append(A._replay(e, ops))
+        return outs, [[res[l][j] for l in range(lanes)] for j in range(len(outs))]
+    if e.prim == "select_n":
+        pred = ins[0]
+        res = []
+        for l in range(lanes):
+            cases = [t[l] if t is not None else _zero(v.aval) for t, v in zip(tins[1:], e.invars[1:])]
+            res.append(A._replay(e, [pred] + cases)[0])
+        return outs, [res]
+    res = [[] for _ in outs]
+    for l in range(lanes):
+        tl = _elementwise(e, ins, outs, [t[l] if t is not None else None for t in tins])
+        for j, t in enumerate(tl):
+            res[j].append(_fit(t, e.outvars[j].aval) if t is not None else None)
+    return outs, [None if any(x is None for x in r) else r for r in res]
+
+
+def _vars(xs):
+    out = []
+    for x in xs:
+        if C.is_traced(x):
+            out.append(x.var)
+        else:
+            a = np.asarray(x)
+            out.append(C.Lit(a, C.AVal(a.shape, a.dtype)))
+    return out
+
+
+def _flat(tl):
+    return [t for ts in tl if ts is not None for t in ts]
+
+
+def _jvp_while(e, ins, tins, lanes):
+    ncc, nbc = int(e.params["cond_nconsts"]), int(e.params["body_nconsts"])
+    cjx, bjx = e.params["cond_jaxpr"], e.params["body_jaxpr"]
+    cc, bc, init = ins[:ncc], ins[ncc:ncc + nbc], ins[ncc + nbc:]
+    tbc, tinit = tins[ncc:ncc + nbc], tins[ncc + nbc:]
+    bm = [t is not None for t in tbc]
+    cm = [t is not None and _isf(v.aval) for t, v in zip(tinit, e.invars[ncc + nbc:])]
+    if not any(bm) and not any(cm):
+        return A._replay(e, ins), [None] * len(e.outvars)
+    while True:                     # the carries whose tangent can be nonzero: a fixed point over the body
+        _, om = jvp_jaxpr(bjx, bm + cm, lanes)
+        new = [a or b for a, b in zip(cm, om)]
+        if new == cm:
+            break
+        cm = new
+    bj, _ = jvp_jaxpr(bjx, bm + cm, lanes, force_out=cm)
+    nb, nc = nbc, len(init)
+    nbt, nct = sum(bm) * lanes, sum(cm) * lanes
+    iv = bj.invars               # [bc][carries][bc tangents][carry tangents] -> [bc][bc tangents][carries][carry t.]
+    bj = C.Jaxpr(iv[:nb] + iv[nb + nc:nb + nc + nbt] + iv[nb:nb + nc] + iv[nb + nc + nbt:], bj.outvars, bj.eqns)
+    tav = [v.aval.strong() for v, m in zip(e.outvars, cm) if m for _ in range(lanes)]
+    cj = C.Jaxpr(list(cjx.invars) + [C.Var(a) for a in tav], cjx.outvars, cjx.eqns)
+    t0 = []
+    for t, m, v in zip(tinit, cm, e.outvars):
+        if m:
+            t0 += list(t) if t is not None else [_zero(v.aval) for _ in range(lanes)]
+    args = list(cc) + list(bc) + _flat(tbc) + list(init) + t0
+    avals = [v.aval for v in e.outvars] + tav
+    outs = C.bind("while", _vars(args), avals, cond_jaxpr=cj, body_jaxpr=bj, cond_nconsts=ncc,
+                  body_nconsts=nbc + nbt)
+    prim, rest = outs[:nc], outs[nc:]
+    touts, k = [], 0
+    for m in cm:
+        if m:
+            touts.append(rest[k:k + lanes])
+            k += lanes
+        else:
+            touts.append(None)
+    return prim, touts
+
+
+def _jvp_cond(e, ins, tins, lanes):
+    nconsts = int(e.params["nconsts"])
+    branches = e.params["branches"]
+    m = [t is not None for t in tins[1:]]
+    if not any(m):
+        return A._replay(e, ins), [None] * len(e.outvars)
+    om = [False] * len(e.outvars)
+    for br in branches:
+        _, o = jvp_jaxpr(br, m, lanes)
+        om = [a or b for a, b in zip(om, o)]
+    nbr = tuple(jvp_jaxpr(br, m, lanes, force_out=om)[0] for br in branches)
+    tav = [v.aval.strong() for v, x in zip(e.outvars, om) if x for _ in range(lanes)]
+    outs = C.bind("cond", _vars(ins + _flat(tins[1:])), [v.aval for v in e.outvars] + tav, branches=nbr,
+                  nconsts=nconsts)
+    n = len(e.outvars)
+    prim, rest = outs[:n], outs[n:]
+    touts, k = [], 0
+    for x in om:
+        if x:
+            touts.append(rest[k:k + lanes])
+            k += lanes
+        else:
+            touts.append(None)
+    return prim, touts
+
+
+def jvp_jaxpr(jx, tin, lanes=1, force_out=None):
+    """-> (Jaxpr, tout).  Invars: jx.invars, then `lanes` tangents of each invar flagged in tin (invar-major);
+    outvars: jx.outvars, then `lanes` tangents of each outvar flagged in tout (zeros where force_out asks for a
+    tangent the program does not make)."""
+    b = C.Builder()
+    C._STACK.append(b)
+    try:
+        prim = [C.Tracer(b.new_invar(v.aval)) for v in jx.invars]
+        tan = [[C.Tracer(b.new_invar(v.aval.strong())) for _ in range(lanes)] if m else None
+               for v, m in zip(jx.invars, tin)]
+        env = {v.id: t for v, t in zip(jx.invars, prim)}
+        tenv = {v.id: t for v, t in zip(jx.invars, tan) if t is not None}
+        for e in jx.eqns:
+            ins = [A._t(v, env) for v in e.invars]
+            tins = [tenv.get(v.id) if isinstance(v, C.Var) else None for v in e.invars]
+            outs, touts = _jvp_eqn(e, ins, tins, lanes)
+            for o, x, t in zip(e.outvars, outs, touts):
+                env[o.id] = x
+                if t is not None:
+                    tenv[o.id] = t
+        tout = [isinstance(v, C.Var) and v.id in tenv for v in jx.outvars]
+        if force_out is not None:
+            tout = [a or bool(f) for a, f in zip(tout, force_out)]
+        res = []
+        for v in jx.outvars:
+            res.append(_local(b, A._t(v, env), v.aval))
+        for v, m in zip(jx.outvars, tout):
+            if not m:
+                continue
+            ts = tenv.get(v.id) if isinstance(v, C.Var) else None
+            for l in range(lanes):
+                t = ts[l] if ts is not None else _zero(v.aval)
+                res.append(_local(b, t, v.aval))
+    finally:
+        C._STACK.pop()
+    return C.Jaxpr(b.invars, res, b.eqns), tout
+
+
+def _local(b, x, aval):
+    if C.is_traced(x):
+        if x.dtype != aval.dtype and _isf(aval):
+            x = C.convert(x, aval.dtype)
+        return b.local(x.var)
+    a = np.asarray(x, aval.dtype)
+    return C.Lit(np.broadcast_to(a, aval.shape).copy(), aval.strong())
+
+
+def jvp_program(prog, pert_pi, pert_bc, lanes=1):
+    """the jvp ItemProgram of prog (reference _api.py:305-345): invars [tallies][tangent tallies][pi][pi
+    tangents][bc][bc tangents]; outvars [tallies][tangent tallies][ys][tangents of float ys].  pert_pi / pert_bc:
+    per operand, whether it is perturbed (float operands only); `lanes` tangent directions.  Every float tally gets
+    `lanes` tangent tallies named name' (lanes = 1) or name'0, name'1, ... of the same format."""
+    import dataclasses
+
+    from ._api import ItemProgram, check_tallies
+    jx = prog.jaxpr
+    nT, nP, nB = prog.nT, prog.nP, prog.nB
+    tf = [k for k, s in enumerate(prog.tallies) if s.kind in ("sum", "discard") and s.dtype in (C.F32, C.F64)]
+    pav, bav = prog.p_avals(), prog.b_avals()
+    pp = [bool(p) and _isf(a) for p, a in zip(pert_pi, pav)]
+    pb = [bool(p) and _isf(a) for p, a in zip(pert_bc, bav)]
+    tin = [k in tf for k in range(nT)] + pp + pb
+    ny = len(jx.outvars) - nT
+    force = [k in tf for k in range(nT)] + [False] * ny
+    jj, tout = jvp_jaxpr(jx, tin, lanes, force_out=force)
+    iv, ov = jj.invars, jj.outvars
+    n_in = nT + nP + nB
+    prim_in, tan_in = iv[:n_in], iv[n_in:]
+    # tangent invars come invar-major: tallies', pi', bc'
+    ntt, npt = len(tf) * lanes, sum(pp) * lanes
+    t_t, t_p, t_b = tan_in[:ntt], tan_in[ntt:ntt + npt], tan_in[ntt + npt:]
+    inv = prim_in[:nT] + t_t + prim_in[nT:nT + nP] + t_p + prim_in[nT + nP:] + t_b
+    n_out = nT + ny
+    prim_out, tan_out = ov[:n_out], ov[n_out:]
+    tty = [j for j in range(n_out) if tout[j]]
+    if [j for j in tty if j < nT] != tf:
+        raise A.ADError("internal: a float tally without a tangent tally")
+    yt = [j - nT for j in tty if j >= nT]
+    t_tal, t_ys = tan_out[:ntt], tan_out[ntt:]
+    outv = prim_out[:nT] + t_tal + prim_out[nT:] + t_ys
+    out_jx = C.Jaxpr(inv, outv, jj.eqns)
+    tl = list(prog.tallies)
+    for k in tf:
+        s = prog.tallies[k]
+        for l in range(lanes):
+            tl.append(dataclasses.replace(s, name=s.name + ("'" if lanes == 1 else f"'{l}")))
+    check_tallies(out_jx, len(tl), prog.where)
+    q = ItemProgram(out_jx, tuple(tl), nP + npt, nB + len(t_b), prog.trunc, f"{prog.tag}+jvp{lanes}", prog.where)
+    q.tangent_tallies = tf
+    q.tangent_ys = yt
+    q.lanes = lanes
+    q.pert = (tuple(pp), tuple(pb))
+    return q

@@ -47,7 +47,7 @@ def _finish_sub(b, ins, outs, out_avals):
                 ov.append(C.literal(np.asarray(x).astype(a.dtype), a.dtype, weak=a.weak))
     finally:
         C._STACK.pop()
-    cap_locals = [b.env[o.id] for o in b.captured]
+    cap_locals = list(b.cap_local)     # (a value captured through an intermediate builder: not keyed by its id)
     return C.Jaxpr(cap_locals + [t.var for t in ins], ov, b.eqns)
 
 

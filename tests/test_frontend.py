@@ -96,3 +96,52 @@ def test_uniform_normal_avals():
 def test_unknown_option_raises():
     with pytest.raises(ValueError):
         tm.vmap(configs.c1_item, outputs=configs.C1["outputs"], bogus=1)
+
+
+def test_jvp_programs_of_every_config():
+    """the forward-mode program of each config (1 and 3 tangent lanes): a tangent tally of the same format per
+    float tally, tangent operands after the primal ones, linear tally use, and a gfx950 module that compiles."""
+    from tallymap_amd._fwd import jvp_program
+    from tallymap_amd.backend import compile as Cm
+    from tallymap_amd.backend import kernel as K
+    for name in ("c1", "c2", "c3", "c4", "c5"):
+        cfg = configs.SIZED[name](8) if name in configs.SIZED else configs.CONFIGS[name]
+        args = getattr(configs, f"{name}_inputs")(8)
+        axes = cfg["in_axes"]
+        pav = [(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
+        bav = [(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
+        p = _prog(cfg["item"], cfg["outputs"], pav, bav, axes, cfg["max_steps"])
+        pp = [np.issubdtype(d, np.floating) for _, d in pav]
+        pb = [np.issubdtype(d, np.floating) for _, d in bav]
+        for lanes in (1, 3):
+            q = jvp_program(p, pp, pb, lanes)
+            ft = [s for s in p.tallies if s.dtype == np.float32]
+            assert [s.name for s in q.tallies[p.nT:]] == [s.name + ("'" if lanes == 1 else f"'{l}")
+                                                          for s in ft for l in range(lanes)]
+            assert all(t.exact == s.exact and t.shape == s.shape for s in ft for t in q.tallies if
+                       t.name.startswith(s.name + "'"))
+            assert q.nP == p.nP + sum(pp) * lanes and q.nB == p.nB + sum(pb) * lanes
+            assert [v.aval for v in q.jaxpr.invars[:p.nT]] == [v.aval for v in p.jaxpr.invars[:p.nT]]
+            if lanes == 1:
+                src, L = K.build(q)
+                assert L.mode == "step"
+                Cm.code_object(src)
+
+
+def test_jvp_of_a_nested_cond_and_loop():
+    """tangents flow through a cond inside the loop body and through a fori_loop carry."""
+    from tallymap_amd._fwd import jvp_program
+
+    def item(t, x, a):
+        def body(i, c):
+            y = lax.cond(c > 0.5, lambda z: z * a, lambda z: z + a, c)
+            return y * 0.5
+        y = lax.fori_loop(0, 3, body, x)
+        return t.add("h", 0, y), y
+    p = _prog(item, {"h": tm.Sum((1,))}, [((), np.float32)], [((), np.float32)], (0, None))
+    q = jvp_program(p, [False], [True])
+    assert q.tangent_ys == [0]
+    prims = [e.prim for e in q.jaxpr.eqns]
+    assert "while" in prims
+    w = next(e for e in q.jaxpr.eqns if e.prim == "while")
+    assert len(w.outvars) == len(next(e for e in p.jaxpr.eqns if e.prim == "while").outvars) + 1
