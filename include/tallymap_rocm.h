@@ -12,6 +12,8 @@
  *   tm_compile       <- compile.compile_cubin's NVRTC sequence (compile.py:160-173), with hipRTC for gfx950
  *   tm_init          <- compile.py's Drv / dlopen of the driver (shim.cc:44-82): binds the HIP runtime the process
  *                       already uses (no second runtime, no device code in this library)
+ *   tm_launch_aux    <- _records.canon (_records.py:45-74): the Records canonicalisation, here device passes of the
+ *                       program's own module instead of XLA ops
  */
 #ifndef TALLYMAP_ROCM_H
 #define TALLYMAP_ROCM_H
@@ -42,6 +44,13 @@ int tm_register(long long id, const void* image, size_t n, const char* note);
  * Asynchronous: nothing waits for the kernels. */
 int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, int flags, long long n_items,
               int block);
+
+/* Launch the auxiliary entry `name` of program `id` (grid x block threads, the same buffer list and n_items as
+ * tm_launch): the passes that move a Records output's raw records to their canonical slots after tm_launch
+ * (tm_rscan<j>, tm_rtop<j>, tm_rcanon<j>).  Replaces the reference's canonicalisation after each one-pass launch,
+ * done there in XLA ops (_records.py:45-74, canon).  Asynchronous like tm_launch. */
+int tm_launch_aux(long long id, const char* name, void* stream, void* const* bufs, int n, long long n_items,
+                  unsigned grid, int block);
 
 /* out[8]: registers per lane of the item loop (tm_main, or tm_adjoint in a replay adjoint), private (scratch) bytes per lane, static LDS bytes per block, achieved
  * blocks per CU at `block` threads, resident threads on the device, compute units, max threads per block, and the

@@ -7,8 +7,8 @@ replay adjoint (a step-scheduled replay over a tape in HBM, or an ordinary item 
 reverse sweep) through the same path; forward-mode derivatives (jvp, jacfwd) run one fused tangent kernel.
 """
 from . import lax, numpy, random
-from ._api import STATS, Result, Sum, TallyError, UnsupportedError, grad, jacfwd, jvp, vjp, vmap
+from ._api import STATS, Records, Result, Sum, TallyError, UnsupportedError, grad, jacfwd, jvp, vjp, vmap
 from ._tally import Tally
 
 __version__ = "0.1.0"
-__all__ = ["vmap", "vjp", "grad", "jvp", "jacfwd", "Sum", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]
+__all__ = ["vmap", "vjp", "grad", "jvp", "jacfwd", "Sum", "Records", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]

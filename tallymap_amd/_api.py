@@ -54,6 +54,38 @@ class Sum:
     scale: float = 2.0 ** 32
 
 
+class Records:
+    """A Records output (reference _api.py:101-140): each item appends records with
+    ``t = t.append(name, {field: value, ...}, when=...)``.
+
+        Records({"sensor": np.int32, "t": np.float32}, capacity=1 << 20)   (or Records(capacity, fields))
+
+    Result.outputs[name] is {field: array[capacity]}: the concatenation over items, in item order, of each item's
+    records in the order it appended them (record k of item i at slot offset[i] + k, offset the exclusive prefix
+    sum of the per-item counts); slots past the last record are zero.  Result.stats['appended'][name] is the number
+    of records (exact also beyond the capacity) and stats['records_dropped'][name] the number that did not fit.  A
+    call in which any Records output receives more than its capacity (or any item is truncated) makes every float
+    output of the call NaN (records and sums) and every integer record field -1.  Fields are scalars of float32, float64, int32, uint32, int64 or
+    uint64; float fields carry tangents (jvp, jacfwd).  One pass: each append claims a raw slot with one atomic and
+    the same launch moves the records to the canonical slots (reference _records.py)."""
+
+    def __init__(self, fields, capacity=None):
+        if isinstance(fields, (int, np.integer)) and isinstance(capacity, dict):
+            fields, capacity = capacity, fields
+        if not isinstance(fields, dict) or not fields:
+            raise TypeError("tallymap: Records(fields, capacity): fields is a non-empty {name: dtype} dict")
+        if capacity is None:
+            raise ValueError("tallymap: Records needs a capacity on this backend")
+        capacity = int(capacity)
+        if not 0 < capacity <= MAX_ITEMS:
+            raise ValueError(f"tallymap: Records capacity must be in [1, 2^31 - 1], got {capacity}")
+        self.fields = {str(k): np.dtype(v) for k, v in fields.items()}
+        self.capacity = capacity
+
+    def __repr__(self):
+        return f"Records({ {k: v.name for k, v in self.fields.items()} }, capacity={self.capacity})"
+
+
 class Result(collections.namedtuple("Result", "outputs per_item truncated stats")):
     """outputs: {name: summed output}; per_item: per-item results (None if the item returns only its tally);
     truncated: bool[N]; stats: {name: int32 scalar} (reference _api.py:180-189)."""
@@ -85,6 +117,8 @@ class ItemProgram:
     trunc: object = None
     tag: str = "primal"
     where: str = ""
+    records: tuple = ()        # ((name, capacity, ((field, dtype), ...)), ...): the Records outputs
+    counts: tuple = ()         # per Records output: the index among the per-item results of its per-item count
 
     @property
     def nT(self):
@@ -106,7 +140,8 @@ class ItemProgram:
     def digest(self):
         d = self.__dict__.get("_digest")
         if d is None:
-            d = self.__dict__["_digest"] = digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag))
+            d = self.__dict__["_digest"] = digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag,
+                                                                            repr(self.records), self.counts))
         return d
 
 
@@ -131,10 +166,11 @@ def _flow(jx, tin, where, allow_drop=False):
     for e in jx.eqns:
         for j, v in enumerate(e.invars):
             if isinstance(v, C.Var) and v.id in tv:
-                if not ((e.prim == "tallymap_emit" and j == 0) or e.prim in ("while", "cond", "copy")):
+                if not ((e.prim in ("tallymap_emit", "tallymap_claim") and j == 0)
+                        or e.prim in ("while", "cond", "copy")):
                     raise TallyError(f"tallymap: a tally is read by `{e.prim}` in the item function {where}: "
                                      "tallies are write-only (t = t.add(...)), used linearly")
-        if e.prim == "tallymap_emit":
+        if e.prim in ("tallymap_emit", "tallymap_claim"):
             consume(e.invars[0])
             tv.add(e.outvars[0].id)
         elif e.prim == "copy":
@@ -246,10 +282,24 @@ def item_name(fn):
 
 def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None):
     """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves)."""
-    names = sorted(outs_spec)
+    from ._tally import KI, KK, RSEP, rkey
     tspecs = []
-    for n in names:
+    recs = []
+    for n in sorted(outs_spec):
         s = outs_spec[n]
+        if RSEP in n:
+            raise ValueError(f"tallymap: output name {n!r} contains a reserved character")
+        if isinstance(s, Records):
+            fields = tuple(s.fields.items())
+            for f, dt in fields:
+                if dt not in SUM_DTYPES:
+                    raise UnsupportedError(f"tallymap: Records field {n}.{f} of dtype {dt}: supported are "
+                                           f"{', '.join(d.name for d in SUM_DTYPES)}")
+                tspecs.append(TSpec(rkey(n, f), (s.capacity,), dt))
+            tspecs.append(TSpec(rkey(n, KI), (s.capacity,), C.I32))
+            tspecs.append(TSpec(rkey(n, KK), (s.capacity,), C.I32))
+            recs.append((n, s.capacity, fields))
+            continue
         shape = (s.shape,) if isinstance(s.shape, int) else tuple(s.shape)
         dt = np.dtype(s.dtype)
         if dt not in SUM_DTYPES:
@@ -263,6 +313,7 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         if int(np.prod(shape, dtype=np.int64)) > MAX_ITEMS:
             raise ValueError(f"tallymap: output {n!r} has more than 2^31 - 1 cells")
         tspecs.append(TSpec(n, shape, dt, exact, fixed=fixed, scale=scale))
+    names = [s.name for s in tspecs]
     where = item_name(fn)
     tav = [C.AVal((s.S,), s.dtype) for s in tspecs]
     shapes = {s.name: s.shape for s in tspecs}
@@ -276,7 +327,11 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         tin = [C.Tracer(b.new_invar(a)) for a in tav]
         pin = [C.Tracer(b.new_invar(a)) for a in pav]
         bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
-        t = Tally({n: x for n, x in zip(names, tin)}, shapes)
+        rec0 = {}
+        if recs:
+            cid = C.bind("tallymap_item_index", [], [C.AVal((), C.I32)])[0]
+            rec0 = {r: (0, cid) for r, _, _ in recs}
+        t = Tally({n: x for n, x in zip(names, tin)}, shapes, rec0, tuple(recs) or None)
         m = unflatten(ptree, pin) if ptree is not None else pin
         bb = unflatten(btree, bin_) if btree is not None else bin_
         mi, bi = iter(m), iter(bb)
@@ -296,6 +351,15 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
             if not C.is_traced(v):
                 v = C.Tracer(C.bind("copy", [C.literal(v)], [C.literal(v).aval.strong()])[0].var)
             outs.append(b.local(v.var))
+        counts = []
+        for r, _, _ in recs:              # the per-item record counts (hidden per-item results)
+            k = t2._r[r][0]
+            if not C.is_traced(k):
+                k = C.Tracer(C.bind("copy", [C.Lit(int(k), C.AVal((), C.I32))], [C.AVal((), C.I32)])[0].var)
+            elif k.dtype != C.I32:
+                k = C.convert(k, C.I32)
+            counts.append(len(outs) - len(names))
+            outs.append(b.local(k.var))
         trunc = None
         if capctx is not None:
             tr = capctx.trunc
@@ -311,8 +375,29 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     if b.captured:
         raise C.TraceError("tallymap: the item function closes over a traced value of another call")
     check_tallies(jx, len(tspecs), where)
-    prog = ItemProgram(jx, tuple(tspecs), len(pav), len(bav), trunc, "primal", where)
+    prog = ItemProgram(jx, tuple(tspecs), len(pav), len(bav), trunc, "primal", where, tuple(recs), tuple(counts))
     return prog, meta
+
+
+def _split_ys(prog, ys):
+    """the backend's per-item results -> (the item's own results, the truncation flag or None): the hidden
+    per-item record counts are removed."""
+    hidden = set(prog.counts) | ({prog.trunc} if prog.trunc is not None else set())
+    own = [y for j, y in enumerate(ys) if j not in hidden]
+    return own, (ys[prog.trunc] if prog.trunc is not None else None)
+
+
+def _record_outputs(prog, o, res_out, stats):
+    """Records outputs ({field: canonical array}) and their stats from a launch's Outputs."""
+    if not prog.records:
+        return
+    stats["appended"], stats["records_dropped"], stats["records_mismatch"] = {}, {}, {}
+    for j, (r, cap, fields) in enumerate(prog.records):
+        res_out[r] = {f: o.records[r][f] for f, _ in fields}
+        n = o.rcount[j]
+        stats["appended"][r] = n
+        stats["records_dropped"][r] = (n - cap).clamp(min=0)
+        stats["records_mismatch"][r] = 0          # (one pass: no replay whose counts could disagree)
 
 
 def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts):
@@ -343,7 +428,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
         raise ValueError(f"tallymap: schedule must be 'item' or 'step', got {opts['schedule']!r}")
     if backend not in ("auto", "hip", "rocm"):
         raise ValueError(f"tallymap: unknown backend {backend!r}; this package is the ROCm (HIP) kernel backend")
-    outs_spec = {k: (v if isinstance(v, Sum) else Sum(v)) for k, v in outputs.items()}
+    outs_spec = {k: (v if isinstance(v, (Sum, Records)) else Sum(v)) for k, v in outputs.items()}
     names = sorted(outs_spec)
 
     def prepare(args):
@@ -381,13 +466,12 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
         from . import backend as B
         prog, meta, pi, bc, N, _ = prepare(args)
         o = B.run(prog, pi, bc, N, opts)
-        res_out = {n: o.tallies[i].reshape(prog.tallies[i].shape) for i, n in enumerate(names)}
+        tn = [s.name for s in prog.tallies]
+        res_out = {n: o.tallies[tn.index(n)].reshape(prog.tallies[tn.index(n)].shape) for n in names if n in tn}
         stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
-        ys = list(o.ys)
-        trunc = None
-        if prog.trunc is not None:
-            trunc = ys.pop()
+        ys, trunc = _split_ys(prog, list(o.ys))
         stats["n_truncated"] = o.n_truncated
+        _record_outputs(prog, o, res_out, stats)
         per_item = unflatten(meta["ytree"], ys)
         return Result(res_out, per_item, trunc, stats)
 
@@ -512,30 +596,32 @@ def _run_tangents(mapped, args, tans, lanes):
     o = B.run(q, list(pi) + pt, list(bc) + bt, N, mapped._opts)
     names = mapped._names
     nT = prog.nT
-    res_out = {n: o.tallies[i].reshape(prog.tallies[i].shape) for i, n in enumerate(names)}
+    tn = [s.name for s in prog.tallies]
+    res_out = {n: o.tallies[tn.index(n)].reshape(prog.tallies[tn.index(n)].shape) for n in names if n in tn}
     ny = len(prog.y_avals())
-    ys = list(o.ys[:ny])
-    trunc = ys.pop() if prog.trunc is not None else None
+    ys, trunc = _split_ys(prog, list(o.ys[:ny]))
     stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
     stats["n_truncated"] = o.n_truncated
+    _record_outputs(prog, o, res_out, stats)
     primal = Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
     t_tal = [dict() for _ in range(lanes)]
     k = nT
     for slot in q.tangent_tallies:
         for l in range(lanes):
-            if prog.tallies[slot].kind == "sum":
+            if prog.tallies[slot].kind == "sum" and prog.tallies[slot].name in names:
                 t_tal[l][prog.tallies[slot].name] = o.tallies[k].reshape(prog.tallies[slot].shape)
             k += 1
+    for r, cap, fields in prog.records:        # tangents of the float record fields (canonical, like the primal)
+        for l in range(lanes):
+            t_tal[l][r] = {f: o.records[r][f + ("'" if lanes == 1 else f"'{l}")] for f, dt in fields
+                           if dt in (C.F32, C.F64)}
     t_ys = [[None] * ny for _ in range(lanes)]
     m = ny
     for j in q.tangent_ys:
         for l in range(lanes):
             t_ys[l][j] = o.ys[m]
             m += 1
-    if prog.trunc is not None:
-        for l in range(lanes):
-            t_ys[l].pop(prog.trunc)
-    return primal, t_tal, [unflatten(meta["ytree"], t) for t in t_ys], meta
+    return primal, t_tal, [unflatten(meta["ytree"], _split_ys(prog, t)[0]) for t in t_ys], meta
 
 
 def jvp(mapped, primals, tangents):

@@ -305,7 +305,8 @@ def jvp_program(prog, pert_pi, pert_bc, lanes=1):
         for l in range(lanes):
             tl.append(dataclasses.replace(s, name=s.name + ("'" if lanes == 1 else f"'{l}")))
     check_tallies(out_jx, len(tl), prog.where)
-    q = ItemProgram(out_jx, tuple(tl), nP + npt, nB + len(t_b), prog.trunc, f"{prog.tag}+jvp{lanes}", prog.where)
+    q = ItemProgram(out_jx, tuple(tl), nP + npt, nB + len(t_b), prog.trunc, f"{prog.tag}+jvp{lanes}", prog.where,
+                    prog.records, prog.counts)
     q.tangent_tallies = tf
     q.tangent_ys = yt
     q.lanes = lanes

@@ -9,17 +9,31 @@ import numpy as np
 
 from . import _core as C
 
+# A Records output (tallymap.Records, reference _tally.py:190-200, _records.py) is kept as hidden tallies of its
+# capacity C: one per field, plus the keys of each record (KI: the item index, KK: the item's append ordinal).
+# t.append claims the next slot of the launch's raw buffer (`tallymap_claim`: one atomic counter per output) and emits
+# the fields and the keys there; the backend then moves record (i, k) to slot offset[i] + k (the canonical layout).
+RSEP = "\x1f"
+KI, KK = RSEP + "i", RSEP + "k"
+
+
+def rkey(name, field):
+    """the hidden tally of a Records output's field (or key)."""
+    return f"{name}{RSEP}{field}"
+
 
 class Tally:
-    __slots__ = ("_a", "_shapes")
+    __slots__ = ("_a", "_shapes", "_r", "_ri")
 
-    def __init__(self, arrays, shapes):
+    def __init__(self, arrays, shapes, rec=None, rinfo=None):
         self._a = dict(arrays)
         self._shapes = dict(shapes)
+        self._r = dict(rec or {})        # Records name -> (k, cid): the append ordinal and the item index
+        self._ri = rinfo                 # static: ((name, capacity, ((field, dtype), ...)), ...)
 
     @classmethod
-    def _from(cls, a, shapes):
-        return cls(a, shapes)
+    def _from(cls, a, shapes, rec=None, rinfo=None):
+        return cls(a, shapes, rec, rinfo)
 
     def _shapes_key(self):
         return tuple(sorted((n, tuple(s)) for n, s in self._shapes.items()))
@@ -27,13 +41,20 @@ class Tally:
     def _with(self, name, v):
         a = dict(self._a)
         a[name] = v
-        return Tally(a, self._shapes)
+        return Tally(a, self._shapes, self._r, self._ri)
+
+    def _records(self):
+        return {n: (c, f) for n, c, f in (self._ri or ())}
 
     def add(self, name, index, value):
         """tally[name][index] += value.  index: an int (flat index of a 1-D output) or a tuple of ints, one per
         output dimension.  Out-of-range or negative indices are dropped and counted."""
-        if name not in self._a:
-            raise KeyError(f"tallymap: unknown output {name!r} (outputs: {sorted(self._a)})")
+        if name in self._records():
+            raise KeyError(f"tallymap: output {name!r} is a Records output: write it with t.append({name!r}, "
+                           "{field: value, ...})")
+        if name not in self._a or RSEP in name:
+            raise KeyError(f"tallymap: unknown output {name!r} (outputs: "
+                           f"{sorted([n for n in self._a if RSEP not in n] + list(self._records()))})")
         shape = self._shapes[name]
         t = self._a[name]
         if isinstance(index, tuple):
@@ -77,6 +98,65 @@ class Tally:
             vv = C.literal(np.asarray(value).astype(tdt), tdt, weak=False)
         new = C.bind("tallymap_emit", [t.var, fv, vv], [t.aval])[0]
         return self._with(name, new)
+
+    def append(self, name, values, when=True):
+        """Append one record to the Records output `name` (reference _tally.py:302-364): `values` = {field: scalar}
+        with exactly the declared fields; nothing is appended when `when` (a scalar bool) is False.  The output
+        holds the records of every item in (item index, append order) order."""
+        recs = self._records()
+        if name not in recs:
+            raise KeyError(f"tallymap: {name!r} is not a Records output (Records outputs: {sorted(recs)})"
+                           + ("; write a Sum output with t.add" if name in self._a else ""))
+        cap, fields = recs[name]
+        if not isinstance(values, dict) or set(values) != {f for f, _ in fields}:
+            got = sorted(values) if isinstance(values, dict) else type(values).__name__
+            raise TypeError(f"tallymap: t.append({name!r}, ...) takes a dict of exactly the declared fields "
+                            f"{sorted(f for f, _ in fields)}, got {got}")
+        w = when
+        if C.is_traced(w):
+            if w.dtype != C.BOOL or w.shape != ():
+                raise TypeError("tallymap: t.append `when` must be a scalar bool")
+        elif not isinstance(w, (bool, np.bool_)):
+            raise TypeError("tallymap: t.append `when` must be a scalar bool")
+        k, cid = self._r[name]
+        vals = []
+        for f, dt in fields:
+            v = values[f]
+            if C.is_traced(v):
+                if v.shape != ():
+                    raise TypeError(f"tallymap: t.append({name!r}, ...): field {f!r} must be a scalar")
+                if not np.issubdtype(dt, np.inexact) and np.issubdtype(v.dtype, np.inexact):
+                    raise TypeError(f"tallymap: t.append({name!r}, ...): a float value for the integer field {f!r}")
+                vals.append(v if v.dtype == dt else C.convert(v, dt))
+            else:
+                if not np.issubdtype(dt, np.inexact) and isinstance(v, float):
+                    raise TypeError(f"tallymap: t.append({name!r}, ...): a float value for the integer field {f!r}")
+                vals.append(np.asarray(v).astype(dt)[()])
+        wi = C.convert(w, C.I32) if C.is_traced(w) else int(bool(w))
+        k2 = k + wi
+        if not C.is_traced(w) and not w:
+            return self
+        kk = self._a[rkey(name, KK)]
+        kv = k.var if C.is_traced(k) else C.literal(int(k), C.I32, weak=False)
+        wv = w.var if C.is_traced(w) else C.literal(True, C.BOOL, weak=False)
+        idx = [n for n, _, _ in self._ri].index(name)
+        tok, slot = C.bind("tallymap_claim", [kk.var, wv, kv], [kk.aval, C.AVal((), C.I32)], r=idx, capacity=cap)
+        keys = [rkey(name, f) for f, _ in fields] + [rkey(name, KI)]
+        ops = tuple(self._a[key] for key in keys) + (tok,)
+        allv = vals + [cid, k]
+
+        def put(*ts):
+            out = []
+            for t, v, in zip(ts, allv):
+                vv = v.var if C.is_traced(v) else C.literal(np.asarray(v).astype(t.dtype), t.dtype, weak=False)
+                out.append(C.bind("tallymap_emit", [t.var, slot.var, vv], [t.aval])[0])
+            return tuple(out)
+
+        from . import lax as L
+        ts = L.cond(slot >= 0, put, lambda *ts: tuple(ts), *ops)
+        a = dict(self._a)
+        a.update(zip(keys + [rkey(name, KK)], ts))
+        return Tally(a, self._shapes, {**self._r, name: (k2, cid)}, self._ri)
 
 
 def _check_int(i):

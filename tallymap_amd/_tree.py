@@ -20,7 +20,9 @@ def flatten(x):
     from ._tally import Tally
     if isinstance(x, Tally):
         names = tuple(sorted(x._a))
-        return [x._a[n] for n in names], TreeDef("tally", (names, x._shapes_key()), [None] * len(names))
+        rn = tuple(sorted(x._r))
+        leaves = [x._a[n] for n in names] + [v for r in rn for v in x._r[r]]
+        return leaves, TreeDef("tally", (names, x._shapes_key(), rn, x._ri), [None] * len(leaves))
     if isinstance(x, (tuple, list)):
         leaves, kids = [], []
         for c in x:
@@ -55,9 +57,10 @@ def _build(td, it):
     if td is None:
         return next(it)
     if td.kind == "tally":
-        names, shapes = td.meta
+        names, shapes, rn, ri = td.meta
         a = {n: next(it) for n in names}
-        return Tally._from(a, dict(shapes))
+        rec = {r: (next(it), next(it)) for r in rn}
+        return Tally._from(a, dict(shapes), rec, ri)
     if td.kind in ("tuple", "list"):
         xs = [_build(c, it) for c in td.children]
         return tuple(xs) if td.kind == "tuple" else xs

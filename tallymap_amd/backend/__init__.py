@@ -35,6 +35,8 @@ class Outputs:
     stats: object          # int32[5]
     ys: list               # per-item results (the truncation flag last when the program has a cap)
     n_truncated: object    # int32 scalar (None: no cap)
+    records: dict = None   # Records name -> {field (or field' tangent): canonical array}
+    rcount: list = None    # per Records output: records appended (int64 scalar tensor)
 
 
 def torch_dtype(dt):
@@ -102,6 +104,9 @@ def launch(c, ins, N, stream=None):
     arr = (ctypes.c_void_p * len(bufs))(*bufs)
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
     Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), L.n_zero, L.flags, N, c.block))
+    for name, kind, block, cap in (getattr(L, "aux", None) or []) if N > 0 else []:
+        grid = {"items": -(-int(N) // 1024), "one": 1, "cap": min(-(-int(cap) // 256), 4096)}[kind]
+        Cm.check(Cm.lib().tm_launch_aux(c.id, name.encode(), ctypes.c_void_p(s), arr, len(bufs), N, grid, block))
     return outs
 
 
@@ -123,7 +128,12 @@ def run(prog, pi, bc, N, opts):
     stats = res[L.r_stats - base]
     ys = [res[r - base] for r in L.r_ys]
     ntr = res[L.r_ctl - base][2:3].view(__import__("torch").int32)[0] if prog.trunc is not None else None
-    return Outputs(tallies, stats, ys, ntr)
+    recs, rcount = {}, []
+    for ri in getattr(L, "records", None) or []:
+        recs[ri["name"]] = {f: res[rr - base] for f, rr in ri["fields"].items()}
+        b, w = ri["r_ctr"]
+        rcount.append(res[b - base].view(__import__("torch").int64)[w])
+    return Outputs(tallies, stats, ys, ntr, recs, rcount)
 
 
 _LANES = {}
@@ -222,6 +232,9 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
     import torch
 
     from . import reverse as R
+    if getattr(prog, "records", ()):
+        raise Cm.BackendError("tallymap_amd: reverse mode through a program with Records outputs is not supported by "
+                              "this backend yet (forward mode, jvp / jacfwd, is)")
     key = (prog.digest(), tuple(tuple(w) for w in wrt))
     hit = _ADJ.get(key)
     if hit is None:

@@ -590,10 +590,12 @@ def _cond(em, e, ins):
     nco = e.params["nconsts"]
     consts, ops = ins[1:1 + nco], ins[1 + nco:]
     brs = e.params["branches"]
+    # output variables are named now and declared once the branches have shown which outputs are tallies (a tally
+    # output is virtual: declaring its elements would cost one variable per bin)
+    pos, ind = len(em.lines), em.ind
     outs = []
     for o in e.outvars:
-        outs.append(Val([em.declare(o.aval.dtype, None, "c") for _ in range(max(1, o.aval.size))],
-                        o.aval.shape, o.aval.dtype))
+        outs.append(Val([em.fresh("c") for _ in range(max(1, o.aval.size))], o.aval.shape, o.aval.dtype))
     tally_out = {}
     for j, br in enumerate(brs):
         head = f"if ({idx.el[0]} == {j})" if j == 0 else (f"else if ({idx.el[0]} == {j})" if j < len(brs) - 1
@@ -607,4 +609,6 @@ def _cond(em, e, ins):
             for n, a in zip(ov.el, x.el):
                 em.line(f"{n} = {a};")
         em.close()
+    decl = ["  " * ind + f"{ctype(ov.dtype)} {n};" for k, ov in enumerate(outs) if k not in tally_out for n in ov.el]
+    em.lines[pos:pos] = decl
     return [tally_out.get(k, ov) for k, ov in enumerate(outs)]

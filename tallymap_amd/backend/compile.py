@@ -99,6 +99,7 @@ def lib():
                                      ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp)]
             L.tm_register.argtypes = [ll, ctypes.c_char_p, sz, ctypes.c_char_p]
             L.tm_launch.argtypes = [ll, vp, ctypes.POINTER(vp), i, i, i, ll, i]
+            L.tm_launch_aux.argtypes = [ll, ctypes.c_char_p, vp, ctypes.POINTER(vp), i, ll, ctypes.c_uint, i]
             L.tm_kernel_info.argtypes = [ll, i, ctypes.POINTER(ll)]
             L.tm_last_error.restype = ctypes.c_char_p
             L.tm_free.argtypes = [vp]

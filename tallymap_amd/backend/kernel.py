@@ -48,6 +48,10 @@ class Layout:
     mode: str
     priv: list
     zero_words: list       # (buffer index, u32 words) zeroed by tm_zero
+    records: list = dataclasses.field(default_factory=list)
+    # per Records output: dict(name, capacity, r_ctr (its u64 claim counter: result index, word), fields {suffix:
+    # canonical result index}), and aux: the passes (entry name, grid kind, block) run after tm_launch
+    aux: list = dataclasses.field(default_factory=list)
 
 
 def _split(jx):
@@ -80,6 +84,70 @@ def _free_vars(jx):
         for o in e.outvars:
             defined.add(o.id)
     return free
+
+
+def _records_passes(ri, r_rctr, r_out, r_cnt, r_rex, r_rbs, prog, bad):
+    """the three passes that move Records output j's raw records to their canonical slots (replacing the
+    reference's _records.canon, _records.py:45-74): tm_rscan<j> (blocks of 1024 items: the exclusive prefix sum of
+    the per-item counts within the block, and the block's total), tm_rtop<j> (one block: the exclusive prefix sum
+    of the block totals), tm_rcanon<j> (every raw slot s below the number of records: record (i, k) to slot
+    offset[i] + k; when `bad` -- a truncation or any Records output past its capacity (reference _api.py:745-755)
+    -- every float field NaN and every integer field -1 instead)."""
+    j, cap = ri["ctr"], ri["capacity"]
+    cnt, rex, rbs = f"((const i32*)P.p[{r_cnt}])", f"((i64*)P.p[{r_rex}])", f"((i64*)P.p[{r_rbs}])"
+    ctr = f"((const u64*)P.p[{r_rctr}])[{j}]"
+    scan = ("  for (int d = 1; d < 1024; d <<= 1) {\n"
+            "    const i64 x = (int)threadIdx.x >= d ? tm_s[threadIdx.x - d] : 0;\n"
+            "    __syncthreads();\n"
+            "    tm_s[threadIdx.x] += x;\n"
+            "    __syncthreads();\n"
+            "  }\n")
+    out = []
+    out.append(f"extern \"C\" __global__ void __launch_bounds__(1024) tm_rscan{j}(const TmParams P, const i64 n_items) {{\n"
+               "  __shared__ i64 tm_s[1024];\n"
+               "  const i64 i = (i64)blockIdx.x * 1024 + threadIdx.x;\n"
+               f"  const i64 c = i < n_items ? (i64){cnt}[i] : 0;\n"
+               "  tm_s[threadIdx.x] = c;\n"
+               "  __syncthreads();\n" + scan +
+               f"  if (i < n_items) {rex}[i] = tm_s[threadIdx.x] - c;\n"
+               f"  if (threadIdx.x == 1023) {rbs}[blockIdx.x] = tm_s[1023];\n}}")
+    out.append(f"extern \"C\" __global__ void __launch_bounds__(1024) tm_rtop{j}(const TmParams P, const i64 n_items) {{\n"
+               "  __shared__ i64 tm_s[1024];\n"
+               "  const i64 nb = (n_items + 1023) / 1024;\n"
+               "  i64 carry = 0;\n"
+               "  for (i64 base = 0; base < nb; base += 1024) {\n"
+               "    const i64 i = base + threadIdx.x;\n"
+               f"    const i64 v = i < nb ? {rbs}[i] : 0;\n"
+               "    tm_s[threadIdx.x] = v;\n"
+               "    __syncthreads();\n" + scan.replace("\n  ", "\n    ").replace("  for", "    for", 1) +
+               f"    if (i < nb) {rbs}[i] = carry + tm_s[threadIdx.x] - v;\n"
+               "    carry += tm_s[1023];\n"
+               "    __syncthreads();\n"
+               "  }\n}")
+    mv, fill = [], []
+    for f, (k, rr) in ri["fields"].items():
+        ct = ctype(prog.tallies[k].dtype)
+        mv.append(f"(({ct}*)P.p[{rr}])[dst] = ((const {ct}*)P.p[{r_out[k]}])[s];")
+        if prog.tallies[k].dtype in (C.F32, C.F64):
+            fill.append(f"(({ct}*)P.p[{rr}])[s] = ({ct})__builtin_nan(\"\");")
+        else:
+            fill.append(f"(({ct}*)P.p[{rr}])[s] = ({ct})-1;")
+    ki, kk = f"((const i32*)P.p[{r_out[ri['ki']]}])", f"((const i32*)P.p[{r_out[ri['kk']]}])"
+    out.append(f"extern \"C\" __global__ void __launch_bounds__(256) tm_rcanon{j}(const TmParams P, const i64 n_items) {{\n"
+               "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, st = (i64)gridDim.x * blockDim.x;\n"
+               f"  const u64 tot = {ctr};\n"
+               f"  if ({bad}) {{\n"
+               f"    for (i64 s = g; s < {cap}; s += st) {{ {' '.join(fill)} }}\n"
+               "    return;\n"
+               "  }\n"
+               "  for (i64 s = g; s < (i64)tot; s += st) {\n"
+               f"    const i32 cid = {ki}[s], k = {kk}[s];\n"
+               "    if (cid < 0 || (i64)cid >= n_items) continue;\n"
+               f"    const i64 dst = {rex}[cid] + {rbs}[cid >> 10] + k;\n"
+               f"    if (dst < 0 || dst >= {cap}) continue;\n"
+               f"    {' '.join(mv)}\n"
+               "  }\n}")
+    return "\n".join(out)
 
 
 def exact_words(S):
@@ -175,10 +243,25 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     r_out = {k: result(prog.tallies[k].shape, prog.tallies[k].dtype) for k in outs}
     r_scr = {k: result((scratch_words(prog.tallies[k]),), np.uint32) for k in outs
              if prog.tallies[k].exact or prog.tallies[k].fixed}
+    recs = list(getattr(prog, "records", ()) or ())
+    r_rctr = result((2 * len(recs),), np.uint32) if recs else None
+    rec_info = []
+    for j, (rn, cap, _) in enumerate(recs):
+        from .._tally import KI, KK, rkey
+        pre, keys = rkey(rn, ""), (rkey(rn, KI), rkey(rn, KK))
+        fl = {}
+        for k in outs:
+            nm = prog.tallies[k].name
+            if nm.startswith(pre) and nm not in keys:
+                fl[nm[len(pre):]] = (k, result((cap,), prog.tallies[k].dtype))
+        ks = [k for k in outs if prog.tallies[k].name in keys]
+        rec_info.append(dict(name=rn, capacity=cap, ctr=j, fields=fl, ki=ks[0], kk=ks[1], count=prog.counts[j]))
     r_ctl = result((8,), np.uint32)
     r_stats = result((5,), np.int32)
     n_zero = len(res)
     r_ys = [result(a.shape, a.dtype, per_item=True) for a in yav]
+    r_rex = result((), np.int64, per_item=True) if recs else None       # the Records scans' scratch (per item)
+    r_rbs = result((), np.int64, per_item=True) if recs else None
     R = n_in + len(res)
 
     # ------------------------------------------------------------------------------- privatisation plan
@@ -249,6 +332,18 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         em_.close()
         return t
     em.hooks["tallymap_emit"] = emit_rule
+
+    def claim_rule(em_, e, ins):
+        """a Records append's raw slot: the next of the output's counter when `when`, -1 past the capacity."""
+        t, w, _ = ins
+        sl = em_.declare(C.I32, "-1", "sl")
+        em_.open(f"if ({w.el[0]})")
+        em_.line(f"const u64 tm_s = atomicAdd(&((u64*)P.p[{r_rctr}])[{int(e.params['r'])}], 1ull);")
+        em_.line(f"{sl} = tm_s < {int(e.params['capacity'])}ull ? (i32)tm_s : -1;")
+        em_.close()
+        return [t, Val([sl], (), C.I32)]
+    em.hooks["tallymap_claim"] = claim_rule
+    em.hooks["tallymap_item_index"] = lambda em_, e, ins: Val(["((i32)tm_item)"], (), C.I32)
 
     # --------------------------------------------------------------------------------- the item's code
     w = _split(jx) if schedule == "step" else None
@@ -405,6 +500,12 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                            else (s.S * np.dtype(s.dtype).itemsize + 3) // 4))
         if k in r_scr:
             zero_words.append((r_scr[k], scratch_words(s)))
+    if recs:
+        zero_words.append((r_rctr, 2 * len(recs)))
+        for ri in rec_info:
+            for _, (k, rr) in ri["fields"].items():
+                it = np.dtype(prog.tallies[k].dtype).itemsize
+                zero_words.append((rr, ri["capacity"] * it // 4))
     zero_words += [(r_ctl, 8), (r_stats, 5)]
     zl = []
     for b, nw in zero_words:
@@ -429,12 +530,16 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             post.append(_wide_readout(s, f"((const u64*)P.p[{r_scr[k]}])", f"((const i32*)P.p[{r_scr[k]}] + {2 * s.S})",
                                       f"((const u32*)P.p[{r_scr[k]}] + {3 * s.S})", f"P.p[{r_out[k]}]"))
     poison = [k for k in outs if prog.tallies[k].dtype in (C.F32, C.F64)]
-    if prog.trunc is not None and poison:
+    bad = ["TM_CTL[2] != 0u"] if prog.trunc is not None else []
+    # a Records output past its capacity poisons every float output of the call (reference _api.py:120-131)
+    bad += [f"((const u64*)P.p[{r_rctr}])[{ri['ctr']}] > {ri['capacity']}ull" for ri in rec_info]
+    if bad and poison:
         # (the readout and the poison visit a bin from the same thread, in program order)
+        post.append(f"const bool tm_bad = {' || '.join(bad)};")
         for k in poison:
             s = prog.tallies[k]
             ct = ctype(s.dtype)
-            post.append(f"if (TM_CTL[2] != 0u) for (i64 i = g; i < {s.S}; i += st) "
+            post.append(f"if (tm_bad) for (i64 i = g; i < {s.S}; i += st) "
                         f"(({ct}*)P.p[{r_out[k]}])[i] = __builtin_nanf(\"\");")
     if getattr(prog, "poison_ys", False) and prog.trunc is not None:
         # a derived program (the adjoint): every float per-item result is NaN when an item was truncated
@@ -664,6 +769,18 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         cdecl.append(f"  for (int i = threadIdx.x; i < {S}; i += blockDim.x) {nm}[i] = 0ull;")
     body[body.index("//TM_COUNT_DECLS")] = "\n".join(cdecl)
     src.append("\n".join(body))
+    aux = []
+    # any truncation or any Records output past its capacity: every float output NaN, every integer record field -1
+    rbad = " || ".join((["TM_CTL[2] != 0u"] if prog.trunc is not None else [])
+                       + [f"((const u64*)P.p[{r_rctr}])[{ri['ctr']}] > {ri['capacity']}ull" for ri in rec_info])
+    for ri in rec_info:
+        src.append(_records_passes(ri, r_rctr, r_out, r_ys[ri["count"]], r_rex, r_rbs, prog, rbad))
+        j = ri["ctr"]
+        cap = ri["capacity"]
+        aux += [(f"tm_rscan{j}", "items", 1024, cap), (f"tm_rtop{j}", "one", 1024, cap),
+                (f"tm_rcanon{j}", "cap", 256, cap)]
     L = Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_out, r_ctl=r_ctl, r_stats=r_stats, r_ys=r_ys,
-               flags=flags, mode=mode, priv=priv, zero_words=zero_words)
+               flags=flags, mode=mode, priv=priv, zero_words=zero_words,
+               records=[dict(name=ri["name"], capacity=ri["capacity"], r_ctr=(r_rctr, ri["ctr"]),
+                             fields={f: rr for f, (_, rr) in ri["fields"].items()}) for ri in rec_info], aux=aux)
     return "\n".join(src) + "\n", L

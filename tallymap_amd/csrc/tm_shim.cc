@@ -77,6 +77,7 @@ struct Program {
 struct Loaded {
   hipModule_t mod = nullptr;
   hipFunction_t zero = nullptr, main = nullptr, post = nullptr;
+  std::map<std::string, hipFunction_t> aux;     // other entries (the Records passes), looked up on first use
   int cus = 0;
   std::map<int, int> occ;       // block size -> blocks per CU of tm_main
 };
@@ -273,6 +274,35 @@ int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, 
   }
   if ((flags & 2) && L->post && launch1(L->post, 64, 256, s, args, "tm_post")) return 1;
   return 0;
+}
+
+int tm_launch_aux(long long id, const char* name, void* stream, void* const* bufs, int n, long long n_items,
+                  unsigned grid, int block) {
+  if (!g_hip_ok) return fail("tallymap_rocm: tm_init was not called");
+  if (!name || n < 1 || block < 64 || block > 1024 || block % 64 || grid < 1 || grid > (1u << 20))
+    return fail("tallymap_rocm: bad auxiliary launch");
+  if (!strcmp(name, "tm_main") || !strcmp(name, "tm_zero") || !strcmp(name, "tm_post") || !strcmp(name, "tm_adjoint"))
+    return fail("tallymap_rocm: %s is launched by tm_launch", name);
+  std::shared_ptr<Loaded> L;
+  if (loaded(id, &L)) return 1;
+  hipFunction_t f = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = L->aux.find(name);
+    if (it != L->aux.end()) {
+      f = it->second;
+    } else {
+      if (g_rt.hipModuleGetFunction(&f, L->mod, name) != hipSuccess) {
+        (void)g_rt.hipGetLastError();
+        return fail("tallymap_rocm: program %lld has no entry %s", id, name);
+      }
+      L->aux[name] = f;
+    }
+  }
+  std::vector<char> args(sizeof(void*) * n + sizeof(long long));
+  memcpy(args.data(), bufs, sizeof(void*) * n);
+  memcpy(args.data() + sizeof(void*) * n, &n_items, sizeof(long long));
+  return launch1(f, grid, (unsigned)block, static_cast<hipStream_t>(stream), args, name);
 }
 
 int tm_kernel_info(long long id, int block, long long out[8]) {

@@ -145,3 +145,33 @@ def test_jvp_of_a_nested_cond_and_loop():
     assert "while" in prims
     w = next(e for e in q.jaxpr.eqns if e.prim == "while")
     assert len(w.outvars) == len(next(e for e in p.jaxpr.eqns if e.prim == "while").outvars) + 1
+
+
+def test_records_tracing_and_errors():
+    """t.append: hidden field / key tallies of the capacity, a claim per append, the per-item count as a hidden
+    per-item result; wrong fields, a float into an integer field and t.add on a Records output raise."""
+    from tallymap_amd._tally import RSEP
+
+    def item(t, x):
+        def body(i, t):
+            return t.append("r", {"i": i, "v": x * i}, when=x > 0.5)
+        return lax.fori_loop(0, 3, body, t), x
+    p = _prog(item, {"r": tm.Records({"i": np.int32, "v": np.float32}, capacity=128), "h": tm.Sum((2,))},
+              [((), np.float32)], [], (0,))
+    names = [s.name for s in p.tallies]
+    assert names == ["h", "r" + RSEP + "i", "r" + RSEP + "v", "r" + RSEP + RSEP + "i", "r" + RSEP + RSEP + "k"]
+    assert all(s.shape == (128,) for s in p.tallies[1:])
+    assert p.records == (("r", 128, (("i", np.dtype(np.int32)), ("v", np.dtype(np.float32)))),)
+    assert p.counts == (1,) and p.jaxpr.outvars[p.nT + 1].aval.dtype == np.int32
+    w = next(e for e in p.jaxpr.eqns if e.prim == "while")
+    assert any(e.prim == "tallymap_claim" for e in w.params["body_jaxpr"].eqns)
+    out = {"r": tm.Records({"i": np.int32}, capacity=8)}
+    with pytest.raises(TypeError, match="declared fields"):
+        _prog(lambda t, x: t.append("r", {"j": 1}), out, [((), np.float32)], [], (0,))
+    with pytest.raises(TypeError, match="integer field"):
+        _prog(lambda t, x: t.append("r", {"i": x}), out, [((), np.float32)], [], (0,))
+    with pytest.raises(KeyError, match="Records output"):
+        _prog(lambda t, x: t.add("r", 0, 1), out, [((), np.float32)], [], (0,))
+    with pytest.raises(ValueError, match="capacity"):
+        tm.Records({"i": np.int32})
+    assert tm.Records(16, {"i": np.int32}).capacity == 16

@@ -1,0 +1,162 @@
+"""Records outputs on the GPU (tm.Records + t.append, reference _api.py:101-140, _tally.py:302-364, _records.py):
+one pass (a raw slot per append from one atomic counter), then the canonical layout -- record k of item i at
+offset[i] + k -- against a numpy emulation of the same walker (the host threefry of tallymap_amd.random, pinned by
+the oracle tests) record for record, bitwise; overflow, empty outputs, several outputs, jvp tangents."""
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import configs, lax
+from tallymap_amd import numpy as jnp
+from tallymap_amd import random as R
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _np(x):
+    return x.cpu().numpy()
+
+
+def _walker(t, x, key, theta):
+    """the quickstart walker; every step with bin < 8 appends (bin, theta (1 - x)); one more record per item at the
+    end (its step count and final x) into a second output."""
+    def cond(c):
+        return c[1] > 0.05
+
+    def body(c):
+        k, x, t = c
+        u = R.uniform(R.fold_in(key, k))
+        b = (x * 16.0).astype(jnp.int32)
+        t = t.append("steps", {"bin": b, "w": theta * (1.0 - x)}, when=b < 8)
+        return k + 1, x * (0.5 + 0.5 * u), t
+    k, x, t = lax.while_loop(cond, body, (0, x, t))
+    t = t.append("ends", {"k": k, "x": x})
+    t = t.add("hist", jnp.clip((x * 40.0).astype(jnp.int32), 0, 1), 1.0)
+    return t, k
+
+
+def _emulate(xs, keys, theta, M=100):
+    """numpy float32 emulation, all items in lockstep: (steps records (item, ordinal, bin, w), ends (k, x))."""
+    n = len(xs)
+    x = xs.astype(f32).copy()
+    ks = np.zeros(n, np.int32)
+    alive = x > f32(0.05)
+    items, ords, bins, ws = [], [], [], []
+    nord = np.zeros(n, np.int64)
+    step = 0
+    while alive.any() and step < M:
+        idx = np.nonzero(alive)[0]
+        xa = x[idx]
+        u = R._host_uniform(R._host_fold_in(keys[idx], np.full(len(idx), step, np.uint32)), 0.0, 1.0)
+        b = (xa * f32(16.0)).astype(np.int32)
+        w = (f32(theta) * (f32(1.0) - xa)).astype(f32)
+        app = b < 8
+        items.append(idx[app])
+        ords.append(nord[idx[app]].copy())
+        nord[idx[app]] += 1
+        bins.append(b[app])
+        ws.append(w[app])
+        x[idx] = (xa * (f32(0.5) + f32(0.5) * u)).astype(f32)
+        ks[idx] += 1
+        step += 1
+        alive = alive & (x > f32(0.05))
+    items, ords = np.concatenate(items), np.concatenate(ords)
+    order = np.lexsort((ords, items))
+    return (np.concatenate(bins)[order], np.concatenate(ws)[order], items[order]), (ks, x)
+
+
+def _outputs(cap_steps, cap_ends):
+    return {"steps": tm.Records({"bin": np.int32, "w": np.float32}, capacity=cap_steps),
+            "ends": tm.Records({"k": np.int32, "x": np.float32}, capacity=cap_ends),
+            "hist": tm.Sum((2,))}
+
+
+def _bits(a):
+    return np.asarray(a).view(np.uint32)
+
+
+@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(block=64), dict(refill=8)],
+                         ids=["step", "item", "block64", "refill8"])
+def test_records_canonical_layout_bitwise(opts):
+    print(f"case: records walker N=65536 {opts}", flush=True)
+    xs, keys, theta = configs.c1_inputs(1 << 16)
+    (bins, ws, items), (ks, xfin) = _emulate(xs, keys, theta)
+    n_rec = len(bins)
+    f = tm.vmap(_walker, outputs=_outputs(1 << 20, 1 << 17), in_axes=(0, 0, None), max_steps=100, **opts)
+    res = f(xs, keys, theta)
+    _sync()
+    st, en = res.outputs["steps"], res.outputs["ends"]
+    assert int(_np(res.stats["appended"]["steps"])) == n_rec
+    assert int(_np(res.stats["records_dropped"]["steps"])) == 0
+    assert np.array_equal(_np(st["bin"])[:n_rec], bins)
+    assert np.array_equal(_bits(_np(st["w"])[:n_rec]), _bits(ws))
+    assert not _np(st["bin"])[n_rec:].any() and not _np(st["w"])[n_rec:].any()
+    # one end record per item, in item order
+    assert int(_np(res.stats["appended"]["ends"])) == len(xs)
+    assert np.array_equal(_np(en["k"])[:len(xs)], ks)
+    assert np.array_equal(_bits(_np(en["x"])[:len(xs)]), _bits(xfin))
+    assert np.array_equal(_np(res.per_item), ks)
+    assert float(_np(res.outputs["hist"]).sum()) == len(xs)
+
+
+def test_records_overflow_poisons():
+    """more records than the capacity: every float output NaN (records and sums), every integer field -1, the exact
+    number appended and the number dropped reported."""
+    print("case: records overflow", flush=True)
+    xs, keys, theta = configs.c1_inputs(4096)
+    (bins, _, _), _ = _emulate(xs, keys, theta)
+    f = tm.vmap(_walker, outputs=_outputs(1000, 1 << 13), in_axes=(0, 0, None), max_steps=100)
+    res = f(xs, keys, theta)
+    _sync()
+    st = res.outputs["steps"]
+    assert int(_np(res.stats["appended"]["steps"])) == len(bins) > 1000
+    assert int(_np(res.stats["records_dropped"]["steps"])) == len(bins) - 1000
+    assert (_np(st["bin"]) == -1).all() and np.isnan(_np(st["w"])).all()
+    assert np.isnan(_np(res.outputs["hist"])).all()
+    assert np.isnan(_np(res.outputs["ends"]["x"])).all()          # (every float output of the call)
+    assert (_np(res.outputs["ends"]["k"]) == -1).all()              # (and every integer record field)
+    assert int(_np(res.stats["appended"]["ends"])) == 4096
+
+
+def test_records_empty_and_when_false():
+    print("case: records none appended", flush=True)
+
+    def item(t, x):
+        t = t.append("r", {"v": x}, when=x > 2.0)
+        return t.append("r", {"v": x}, when=False)
+    x = np.linspace(0, 1, 5000).astype(f32)
+    res = tm.vmap(item, outputs={"r": tm.Records({"v": np.float32}, capacity=64)}, in_axes=(0,))(x)
+    _sync()
+    assert int(_np(res.stats["appended"]["r"])) == 0
+    assert not _np(res.outputs["r"]["v"]).any()
+
+
+def test_records_jvp_tangents_at_the_same_slots():
+    """d w / d theta = 1 - x: the tangent records sit at the primal's slots and equal w / 2 bitwise (theta = 2)."""
+    print("case: records jvp", flush=True)
+    xs, keys, theta = configs.c1_inputs(1 << 14)
+    f = tm.vmap(_walker, outputs=_outputs(1 << 18, 1 << 15), in_axes=(0, 0, None), max_steps=100)
+    res, tan = tm.jvp(f, (xs, keys, theta), (None, None, f32(1.0)))
+    _sync()
+    n = int(_np(res.stats["appended"]["steps"]))
+    w, wt = _np(res.outputs["steps"]["w"]), _np(tan.outputs["steps"]["w"])
+    assert n > 0 and np.array_equal(_bits(wt[:n]), _bits(w[:n] / f32(2.0))) and not wt[n:].any()
+    assert not _np(tan.outputs["ends"]["x"]).any()             # (x does not depend on theta)
+    ref = f(xs, keys, theta)
+    _sync()
+    assert np.array_equal(_np(ref.outputs["steps"]["bin"]), _np(res.outputs["steps"]["bin"]))
+
+
+def test_records_reverse_mode_refused():
+    print("case: records vjp refused", flush=True)
+    xs, keys, theta = configs.c1_inputs(256)
+    f = tm.vmap(_walker, outputs=_outputs(1 << 12, 1 << 9), in_axes=(0, 0, None), max_steps=100)
+    _, pull = tm.vjp(f, xs, keys, theta, argnums=2)
+    with pytest.raises(Exception, match="Records"):
+        pull({"hist": 1.0})
