@@ -113,6 +113,54 @@ def _cpu_sample(name, inputs, target_s):
         n = min(N, max(n * 2, int(n * target_s / max(dt, 1e-3) / 4)))
 
 
+def _records_walker(t, x, key, theta):
+    """the quickstart walker writing a Records output: (bin, theta (1 - x)) per step instead of a histogram add."""
+    from tallymap_amd import lax
+    from tallymap_amd import numpy as jnp
+    from tallymap_amd import random as R
+
+    def body(c):
+        k, x, t = c
+        u = R.uniform(R.fold_in(key, k))
+        b = (x * 16.0).astype(jnp.int32)
+        t = t.append("steps", {"bin": b, "w": theta * (1.0 - x)}, when=b < 16)
+        return k + 1, x * (0.5 + 0.5 * u), t
+    k, x, t = lax.while_loop(lambda c: c[1] > 0.05, body, (0, x, t))
+    return t, k
+
+
+def bench_records(steps, warmup):
+    """Records throughput: C1's walker over 4,194,304 items appending one record per step (about 33M records,
+    capacity 2^26) -- the one-pass launch plus the canonicalisation passes, HIP events on torch's current stream."""
+    import torch
+
+    import tallymap_amd as tm
+    from tallymap_amd import configs
+    n = 4_194_304
+    xs, keys, theta = configs.c1_inputs(n)
+    dev = [torch.from_numpy(xs).cuda(), torch.from_numpy(keys).cuda(), torch.tensor(theta).cuda()]
+    f = tm.vmap(_records_walker, outputs={"steps": tm.Records({"bin": np.int32, "w": np.float32}, capacity=1 << 26)},
+                in_axes=(0, 0, None), max_steps=100)
+    for _ in range(warmup):
+        f(*dev)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for e in evs:
+        e[0].record(stream)
+        r = f(*dev)
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    nrec = int(r.stats["appended"]["steps"].item())
+    drop, ntr = int(r.stats["records_dropped"]["steps"].item()), int(r.stats["n_truncated"].item())
+    if drop or ntr:
+        raise RuntimeError(f"records bench: {nrec} records, {drop} dropped, {ntr} truncated items")
+    print("bench: records done", file=sys.stderr, flush=True)
+    return {"n_items": n, "records": nrec, "capacity": 1 << 26, "ms": ms, "records_per_s": nrec / (ms * 1e-3),
+            "items_per_s": n / (ms * 1e-3)}
+
+
 def bench_configs(steps, warmup, with_cpu):
     """items/s of configs 1, 3, 4, 5 at their BASELINE sizes, forward and gradient launches timed with HIP events
     on torch's current stream; the oracle on a bounded sample beside each."""
@@ -291,6 +339,7 @@ def main():
                                 "f32_peak": peaks["lds_f32_128"]["adds_per_s"]}
         print("bench: atomics done", file=sys.stderr, flush=True)
         out["configs"] = bench_configs(max(3, a.steps // 4), 1, not a.no_cpu)
+        out["records"] = bench_records(max(3, a.steps // 4), 1)
     print(json.dumps(out))
 
 

@@ -166,11 +166,11 @@ def _flow(jx, tin, where, allow_drop=False):
     for e in jx.eqns:
         for j, v in enumerate(e.invars):
             if isinstance(v, C.Var) and v.id in tv:
-                if not ((e.prim in ("tallymap_emit", "tallymap_claim") and j == 0)
+                if not ((e.prim in ("tallymap_emit", "tallymap_claim", "tallymap_put") and j == 0)
                         or e.prim in ("while", "cond", "copy")):
                     raise TallyError(f"tallymap: a tally is read by `{e.prim}` in the item function {where}: "
                                      "tallies are write-only (t = t.add(...)), used linearly")
-        if e.prim in ("tallymap_emit", "tallymap_claim"):
+        if e.prim in ("tallymap_emit", "tallymap_claim", "tallymap_put"):
             consume(e.invars[0])
             tv.add(e.outvars[0].id)
         elif e.prim == "copy":

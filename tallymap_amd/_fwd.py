@@ -98,13 +98,16 @@ def _jvp_eqn(e, ins, tins, lanes):
     if e.prim == "cond":
         return _jvp_cond(e, ins, tins, lanes)
     outs = A._replay(e, ins)
-    if e.prim == "tallymap_emit":
+    if e.prim in ("tallymap_emit", "tallymap_put"):
         tt, tv = tins[0], tins[2]
         if tt is None:
             if tv is not None:
                 raise A.ADError("internal: an emit of a perturbed value into a tally without a tangent tally")
             return outs, [None]
         if tv is None:
+            if e.prim == "tallymap_put":     # (a Records slot is stored once and never zeroed: store the zero)
+                z = np.zeros((), e.invars[2].aval.dtype)[()]
+                return outs, [[A._replay(e, [tt[l], ins[1], z])[0] for l in range(lanes)]]
             return outs, [list(tt)]
         return outs, [[A._replay(e, [tt[l], ins[1], tv[l]])[0] for l in range(lanes)]]
     if all(t is None for t in tins):

@@ -11,8 +11,9 @@ from . import _core as C
 
 # A Records output (tallymap.Records, reference _tally.py:190-200, _records.py) is kept as hidden tallies of its
 # capacity C: one per field, plus the keys of each record (KI: the item index, KK: the item's append ordinal).
-# t.append claims the next slot of the launch's raw buffer (`tallymap_claim`: one atomic counter per output) and emits
-# the fields and the keys there; the backend then moves record (i, k) to slot offset[i] + k (the canonical layout).
+# t.append claims a slot of the launch's raw buffer (`tallymap_claim`) and stores the fields and the keys there
+# (`tallymap_put`: a plain store, once per slot); the backend then moves record (i, k) to slot offset[i] + k (the
+# canonical layout).
 RSEP = "\x1f"
 KI, KK = RSEP + "i", RSEP + "k"
 
@@ -143,13 +144,13 @@ class Tally:
         tok, slot = C.bind("tallymap_claim", [kk.var, wv, kv], [kk.aval, C.AVal((), C.I32)], r=idx, capacity=cap)
         keys = [rkey(name, f) for f, _ in fields] + [rkey(name, KI)]
         ops = tuple(self._a[key] for key in keys) + (tok,)
-        allv = vals + [cid, k]
+        allv = vals + [cid + 1, k]         # (the raw key of an item is its index + 1: 0 marks an unused raw slot)
 
         def put(*ts):
             out = []
             for t, v, in zip(ts, allv):
                 vv = v.var if C.is_traced(v) else C.literal(np.asarray(v).astype(t.dtype), t.dtype, weak=False)
-                out.append(C.bind("tallymap_emit", [t.var, slot.var, vv], [t.aval])[0])
+                out.append(C.bind("tallymap_put", [t.var, slot.var, vv], [t.aval])[0])
             return tuple(out)
 
         from . import lax as L

@@ -18,6 +18,7 @@ from . import kernel as K
 _KERNELS = collections.OrderedDict()
 _LOCK = threading.Lock()
 KERNEL_CACHE = 256
+RB = 256                   # slots per Records batch (TM_RB in tm_device.h)
 
 
 @dataclasses.dataclass
@@ -97,6 +98,13 @@ def launch(c, ins, N, stream=None):
     for shape, dt, per_item in L.res:
         if per_item == "tape":          # per launched lane (the launcher's persistent grid at this N)
             sh = (_lanes(c, N),) + tuple(shape)
+        elif per_item == ("rraw",):     # a Records raw buffer: the capacity + 255 spare slots per launched wave
+            sh = (int(shape[0]) + (_lanes(c, N) // 64) * (RB - 1) if N > 0 else int(shape[0]),)
+            if sh[0] > 2 ** 31 - 1:
+                raise ValueError(f"tallymap_amd: a Records capacity of {shape[0]} leaves no room for the launch's "
+                                 "batch slack below 2^31 slots")
+        elif per_item == ("rwave",):    # a Records hole list: a count, then a slot range per launched wave
+            sh = (1 + 2 * (_lanes(c, N) // 64),)
         else:
             sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
         outs.append(torch.empty(sh, dtype=torch_dtype(dt), device="cuda"))
@@ -104,8 +112,11 @@ def launch(c, ins, N, stream=None):
     arr = (ctypes.c_void_p * len(bufs))(*bufs)
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
     Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), L.n_zero, L.flags, N, c.block))
-    for name, kind, block, cap in (getattr(L, "aux", None) or []) if N > 0 else []:
-        grid = {"items": -(-int(N) // 1024), "one": 1, "cap": min(-(-int(cap) // 256), 4096)}[kind]
+    for name, kind, block, cap in (getattr(L, "aux", None) or []):
+        if N == 0 and kind != "cap":         # (no item ran: only the canonical outputs are written, as zeros)
+            continue
+        grid = {"items": -(-int(N) // 1024), "one": 1, "cap": min(-(-int(cap) // 256), 4096),
+                "waves": max(1, -(-(_lanes(c, N) // 64) // 256))}[kind]
         Cm.check(Cm.lib().tm_launch_aux(c.id, name.encode(), ctypes.c_void_p(s), arr, len(bufs), N, grid, block))
     return outs
 

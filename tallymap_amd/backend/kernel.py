@@ -49,7 +49,7 @@ class Layout:
     priv: list
     zero_words: list       # (buffer index, u32 words) zeroed by tm_zero
     records: list = dataclasses.field(default_factory=list)
-    # per Records output: dict(name, capacity, r_ctr (its u64 claim counter: result index, word), fields {suffix:
+    # per Records output: dict(name, capacity, r_ctr (its u64 record count: result index, word), fields {suffix:
     # canonical result index}), and aux: the passes (entry name, grid kind, block) run after tm_launch
     aux: list = dataclasses.field(default_factory=list)
 
@@ -87,15 +87,18 @@ def _free_vars(jx):
 
 
 def _records_passes(ri, r_rctr, r_out, r_cnt, r_rex, r_rbs, prog, bad):
-    """the three passes that move Records output j's raw records to their canonical slots (replacing the
-    reference's _records.canon, _records.py:45-74): tm_rscan<j> (blocks of 1024 items: the exclusive prefix sum of
-    the per-item counts within the block, and the block's total), tm_rtop<j> (one block: the exclusive prefix sum
-    of the block totals), tm_rcanon<j> (every raw slot s below the number of records: record (i, k) to slot
-    offset[i] + k; when `bad` -- a truncation or any Records output past its capacity (reference _api.py:745-755)
-    -- every float field NaN and every integer field -1 instead)."""
+    """the passes that move Records output j's raw records to their canonical slots (replacing the reference's
+    _records.canon, _records.py:45-74): tm_rholes<j> (the unused slots of each wave's last batch get key 0),
+    tm_rscan<j> (blocks of 1024 items: the exclusive prefix sum of the per-item counts within the block, and the
+    block's total), tm_rtop<j> (one block: the exclusive prefix sum of the block totals), tm_rcanon<j> (every claimed
+    raw slot with a key: record (i, k) to slot offset[i] + k; the slots past the last record zeroed; when `bad` -- a
+    truncation or any Records output past its capacity (reference _api.py:745-755) -- every float field NaN and
+    every integer field -1 instead)."""
     j, cap = ri["ctr"], ri["capacity"]
     cnt, rex, rbs = f"((const i32*)P.p[{r_cnt}])", f"((i64*)P.p[{r_rex}])", f"((i64*)P.p[{r_rbs}])"
-    ctr = f"((const u64*)P.p[{r_rctr}])[{j}]"
+    slots, tot = f"((const u64*)P.p[{r_rctr}])[{2 * j}]", f"((const u64*)P.p[{r_rctr}])[{2 * j + 1}]"
+    fin = f"((const u64*)P.p[{ri['fin']}])"
+    ki, kk = f"((i32*)P.p[{r_out[ri['ki']]}])", f"((const i32*)P.p[{r_out[ri['kk']]}])"
     scan = ("  for (int d = 1; d < 1024; d <<= 1) {\n"
             "    const i64 x = (int)threadIdx.x >= d ? tm_s[threadIdx.x - d] : 0;\n"
             "    __syncthreads();\n"
@@ -103,6 +106,12 @@ def _records_passes(ri, r_rctr, r_out, r_cnt, r_rex, r_rbs, prog, bad):
             "    __syncthreads();\n"
             "  }\n")
     out = []
+    out.append(f"extern \"C\" __global__ void __launch_bounds__(256) tm_rholes{j}(const TmParams P, const i64 n_items) {{\n"
+               f"  const u64 nw = {fin}[0], rawcap = {cap}ull + nw * (TM_RB - 1ull);\n"
+               "  for (u64 w = (u64)blockIdx.x * blockDim.x + threadIdx.x; w < nw; w += (u64)gridDim.x * blockDim.x) {\n"
+               f"    const u64 s1 = {fin}[2 + 2 * w] < rawcap ? {fin}[2 + 2 * w] : rawcap;\n"
+               f"    for (u64 s = {fin}[1 + 2 * w]; s < s1; ++s) {ki}[s] = 0;\n"
+               "  }\n}")
     out.append(f"extern \"C\" __global__ void __launch_bounds__(1024) tm_rscan{j}(const TmParams P, const i64 n_items) {{\n"
                "  __shared__ i64 tm_s[1024];\n"
                "  const i64 i = (i64)blockIdx.x * 1024 + threadIdx.x;\n"
@@ -124,29 +133,32 @@ def _records_passes(ri, r_rctr, r_out, r_cnt, r_rex, r_rbs, prog, bad):
                "    carry += tm_s[1023];\n"
                "    __syncthreads();\n"
                "  }\n}")
-    mv, fill = [], []
+    mv, fill, zero = [], [], []
     for f, (k, rr) in ri["fields"].items():
         ct = ctype(prog.tallies[k].dtype)
         mv.append(f"(({ct}*)P.p[{rr}])[dst] = ((const {ct}*)P.p[{r_out[k]}])[s];")
+        zero.append(f"(({ct}*)P.p[{rr}])[s] = ({ct})0;")
         if prog.tallies[k].dtype in (C.F32, C.F64):
             fill.append(f"(({ct}*)P.p[{rr}])[s] = ({ct})__builtin_nan(\"\");")
         else:
             fill.append(f"(({ct}*)P.p[{rr}])[s] = ({ct})-1;")
-    ki, kk = f"((const i32*)P.p[{r_out[ri['ki']]}])", f"((const i32*)P.p[{r_out[ri['kk']]}])"
     out.append(f"extern \"C\" __global__ void __launch_bounds__(256) tm_rcanon{j}(const TmParams P, const i64 n_items) {{\n"
                "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, st = (i64)gridDim.x * blockDim.x;\n"
-               f"  const u64 tot = {ctr};\n"
                f"  if ({bad}) {{\n"
                f"    for (i64 s = g; s < {cap}; s += st) {{ {' '.join(fill)} }}\n"
                "    return;\n"
                "  }\n"
-               "  for (i64 s = g; s < (i64)tot; s += st) {\n"
-               f"    const i32 cid = {ki}[s], k = {kk}[s];\n"
-               "    if (cid < 0 || (i64)cid >= n_items) continue;\n"
+               f"  const i64 nslots = (i64){slots}, ntot = (i64){tot};\n"
+               "  for (i64 s = g; s < nslots; s += st) {\n"
+               f"    const i32 key = {ki}[s];\n"
+               "    if (key <= 0 || (i64)key > n_items) continue;\n"
+               f"    const i32 cid = key - 1, k = {kk}[s];\n"
                f"    const i64 dst = {rex}[cid] + {rbs}[cid >> 10] + k;\n"
                f"    if (dst < 0 || dst >= {cap}) continue;\n"
                f"    {' '.join(mv)}\n"
-               "  }\n}")
+               "  }\n"
+               f"  for (i64 s = ntot + g; s < {cap}; s += st) {{ {' '.join(zero)} }}\n"
+               "}")
     return "\n".join(out)
 
 
@@ -240,14 +252,18 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         res.append((tuple(shape), np.dtype(dt), per_item))
         return n_in + len(res) - 1
     outs = prog.out_tallies
-    r_out = {k: result(prog.tallies[k].shape, prog.tallies[k].dtype) for k in outs}
+    from .._tally import KI, KK, RSEP, rkey
+    raw = set()                # the Records outputs' raw tallies: sized per launch (capacity + the waves' batch
+    for rn, _, _ in (getattr(prog, "records", ()) or ()):     # slack), never zeroed, stored to once per slot
+        raw |= {k for k in outs if prog.tallies[k].name.startswith(rkey(rn, ""))}
+    r_out = {k: result(prog.tallies[k].shape, prog.tallies[k].dtype, ("rraw",) if k in raw else False)
+             for k in outs}
     r_scr = {k: result((scratch_words(prog.tallies[k]),), np.uint32) for k in outs
              if prog.tallies[k].exact or prog.tallies[k].fixed}
     recs = list(getattr(prog, "records", ()) or ())
-    r_rctr = result((2 * len(recs),), np.uint32) if recs else None
+    r_rctr = result((4 * len(recs),), np.uint32) if recs else None     # per output: u64 slots claimed, u64 records
     rec_info = []
     for j, (rn, cap, _) in enumerate(recs):
-        from .._tally import KI, KK, rkey
         pre, keys = rkey(rn, ""), (rkey(rn, KI), rkey(rn, KK))
         fl = {}
         for k in outs:
@@ -255,13 +271,16 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             if nm.startswith(pre) and nm not in keys:
                 fl[nm[len(pre):]] = (k, result((cap,), prog.tallies[k].dtype))
         ks = [k for k in outs if prog.tallies[k].name in keys]
-        rec_info.append(dict(name=rn, capacity=cap, ctr=j, fields=fl, ki=ks[0], kk=ks[1], count=prog.counts[j]))
+        rec_info.append(dict(name=rn, capacity=cap, ctr=j, fields=fl, ki=ks[0], kk=ks[1], count=prog.counts[j],
+                             fin=None))
     r_ctl = result((8,), np.uint32)
     r_stats = result((5,), np.int32)
     n_zero = len(res)
     r_ys = [result(a.shape, a.dtype, per_item=True) for a in yav]
     r_rex = result((), np.int64, per_item=True) if recs else None       # the Records scans' scratch (per item)
     r_rbs = result((), np.int64, per_item=True) if recs else None
+    for ri in rec_info:        # per launched wave: the unused slot range [s0, s1) of its last batch (+ a count)
+        ri["fin"] = result((), np.uint64, per_item=("rwave",))
     R = n_in + len(res)
 
     # ------------------------------------------------------------------------------- privatisation plan
@@ -269,6 +288,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     budget = LDS_BYTES
     for k in outs:
         s = prog.tallies[k]
+        if k in raw:
+            continue
         nbytes = s.S * (8 * XW if s.exact else (12 if s.fixed else np.dtype(s.dtype).itemsize))
         if nbytes <= budget:
             budget -= nbytes
@@ -334,15 +355,27 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     em.hooks["tallymap_emit"] = emit_rule
 
     def claim_rule(em_, e, ins):
-        """a Records append's raw slot: the next of the output's counter when `when`, -1 past the capacity."""
+        """a Records append's raw slot (tm_rclaim: the wave's batch), -1 when `when` is false."""
         t, w, _ = ins
-        sl = em_.declare(C.I32, "-1", "sl")
-        em_.open(f"if ({w.el[0]})")
-        em_.line(f"const u64 tm_s = atomicAdd(&((u64*)P.p[{r_rctr}])[{int(e.params['r'])}], 1ull);")
-        em_.line(f"{sl} = tm_s < {int(e.params['capacity'])}ull ? (i32)tm_s : -1;")
-        em_.close()
+        j = int(e.params["r"])
+        sl = em_.bind(f"(i32)tm_rclaim(&((u64*)P.p[{r_rctr}])[{2 * j}], &tm_rbase{j}[threadIdx.x >> 6], "
+                      f"&tm_rleft{j}[threadIdx.x >> 6], &tm_rcnt{j}[threadIdx.x >> 6], {w.el[0]}, tm_rawcap{j})",
+                      C.I32, "sl")
         return [t, Val([sl], (), C.I32)]
     em.hooks["tallymap_claim"] = claim_rule
+
+    def put_rule(em_, e, ins):
+        """a Records field or key stored at its raw slot: a plain store, once per slot (a float adds +0.0 first,
+        so -0.0 is stored as +0.0 like the reference's add into a zeroed buffer)."""
+        t, idx, val = ins
+        k = t.slot
+        s = prog.tallies[k]
+        ct = ctype(s.dtype)
+        v = f"({val.el[0]} + ({ct})0)" if s.dtype in (C.F32, C.F64) else val.el[0]
+        j = next(ri["ctr"] for ri in rec_info if s.name.startswith(rkey(ri["name"], "")))
+        em_.line(f"if ((u64)(u32){idx.el[0]} < tm_rawcap{j}) (({ct}*)P.p[{r_out[k]}])[{idx.el[0]}] = {v};")
+        return t
+    em.hooks["tallymap_put"] = put_rule
     em.hooks["tallymap_item_index"] = lambda em_, e, ins: Val(["((i32)tm_item)"], (), C.I32)
 
     # --------------------------------------------------------------------------------- the item's code
@@ -496,16 +529,14 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     zero_words = []
     for k in outs:
         s = prog.tallies[k]
+        if k in raw:
+            continue
         zero_words.append((r_out[k], s.S * np.dtype(s.dtype).itemsize // 4 if np.dtype(s.dtype).itemsize >= 4
                            else (s.S * np.dtype(s.dtype).itemsize + 3) // 4))
         if k in r_scr:
             zero_words.append((r_scr[k], scratch_words(s)))
     if recs:
-        zero_words.append((r_rctr, 2 * len(recs)))
-        for ri in rec_info:
-            for _, (k, rr) in ri["fields"].items():
-                it = np.dtype(prog.tallies[k].dtype).itemsize
-                zero_words.append((rr, ri["capacity"] * it // 4))
+        zero_words.append((r_rctr, 4 * len(recs)))
     zero_words += [(r_ctl, 8), (r_stats, 5)]
     zl = []
     for b, nw in zero_words:
@@ -529,10 +560,10 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         elif s.fixed:
             post.append(_wide_readout(s, f"((const u64*)P.p[{r_scr[k]}])", f"((const i32*)P.p[{r_scr[k]}] + {2 * s.S})",
                                       f"((const u32*)P.p[{r_scr[k]}] + {3 * s.S})", f"P.p[{r_out[k]}]"))
-    poison = [k for k in outs if prog.tallies[k].dtype in (C.F32, C.F64)]
+    poison = [k for k in outs if prog.tallies[k].dtype in (C.F32, C.F64) and k not in raw]
     bad = ["TM_CTL[2] != 0u"] if prog.trunc is not None else []
     # a Records output past its capacity poisons every float output of the call (reference _api.py:120-131)
-    bad += [f"((const u64*)P.p[{r_rctr}])[{ri['ctr']}] > {ri['capacity']}ull" for ri in rec_info]
+    bad += [f"((const u64*)P.p[{r_rctr}])[{2 * ri['ctr'] + 1}] > {ri['capacity']}ull" for ri in rec_info]
     if bad and poison:
         # (the readout and the poison visit a bin from the same thread, in program order)
         post.append(f"const bool tm_bad = {' || '.join(bad)};")
@@ -563,6 +594,13 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append(f"extern \"C\" __global__ void __launch_bounds__({lb}) {entry}(const TmParams P, "
                 "const i64 n_items) {")
     body.append("  u64* const tm_ctr = (u64*)P.p[%d];" % r_ctl)
+    for ri in rec_info:        # each wave's Records batch state (tm_rclaim) and the raw buffers' length
+        j, w = ri["ctr"], block // 64
+        body.append(f"  __shared__ u64 tm_rbase{j}[{w}], tm_rcnt{j}[{w}];")
+        body.append(f"  __shared__ u32 tm_rleft{j}[{w}];")
+        body.append(f"  if ((threadIdx.x & 63u) == 0u) {{ tm_rbase{j}[threadIdx.x >> 6] = 0ull; "
+                    f"tm_rcnt{j}[threadIdx.x >> 6] = 0ull; tm_rleft{j}[threadIdx.x >> 6] = 0u; }}")
+        body.append(f"  const u64 tm_rawcap{j} = {ri['capacity']}ull + (u64)gridDim.x * {w}ull * (TM_RB - 1ull);")
     for k in priv:
         s = prog.tallies[k]
         if s.exact:
@@ -721,6 +759,17 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         body.append("    }")
     body.append("  }")
     body.append("  if (tm_drop) atomicAdd(&TM_STATS[4], tm_drop);")
+    for ri in rec_info:        # each wave: its records into the exact count, its last batch's unused slots listed
+        j, w, fin = ri["ctr"], block // 64, f"((u64*)P.p[{ri['fin']}])"
+        body.append("  if ((threadIdx.x & 63u) == 0u) {")
+        body.append(f"    const u64 tm_w = (u64)blockIdx.x * {w} + (threadIdx.x >> 6), tm_c = tm_rcnt{j}[threadIdx.x >> 6];")
+        body.append(f"    const u64 tm_b = tm_rbase{j}[threadIdx.x >> 6];")
+        body.append(f"    const u32 tm_l = tm_rleft{j}[threadIdx.x >> 6];")
+        body.append(f"    if (tm_c) atomicAdd(&((u64*)P.p[{r_rctr}])[{2 * j + 1}], tm_c);")
+        body.append(f"    {fin}[1 + 2 * tm_w] = tm_c ? tm_b + (TM_RB - tm_l) : 0ull;")
+        body.append(f"    {fin}[2 + 2 * tm_w] = tm_c ? tm_b + TM_RB : 0ull;")
+        body.append(f"    if (tm_w == 0) {fin}[0] = (u64)gridDim.x * {w};")
+        body.append("  }")
     body.append("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")
     if priv:
         body.append("  __syncthreads();")
@@ -772,15 +821,16 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     aux = []
     # any truncation or any Records output past its capacity: every float output NaN, every integer record field -1
     rbad = " || ".join((["TM_CTL[2] != 0u"] if prog.trunc is not None else [])
-                       + [f"((const u64*)P.p[{r_rctr}])[{ri['ctr']}] > {ri['capacity']}ull" for ri in rec_info])
+                       + [f"((const u64*)P.p[{r_rctr}])[{2 * ri['ctr'] + 1}] > {ri['capacity']}ull"
+                          for ri in rec_info])
     for ri in rec_info:
         src.append(_records_passes(ri, r_rctr, r_out, r_ys[ri["count"]], r_rex, r_rbs, prog, rbad))
         j = ri["ctr"]
         cap = ri["capacity"]
-        aux += [(f"tm_rscan{j}", "items", 1024, cap), (f"tm_rtop{j}", "one", 1024, cap),
-                (f"tm_rcanon{j}", "cap", 256, cap)]
+        aux += [(f"tm_rholes{j}", "waves", 256, cap), (f"tm_rscan{j}", "items", 1024, cap),
+                (f"tm_rtop{j}", "one", 1024, cap), (f"tm_rcanon{j}", "cap", 256, cap)]
     L = Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_out, r_ctl=r_ctl, r_stats=r_stats, r_ys=r_ys,
                flags=flags, mode=mode, priv=priv, zero_words=zero_words,
-               records=[dict(name=ri["name"], capacity=ri["capacity"], r_ctr=(r_rctr, ri["ctr"]),
+               records=[dict(name=ri["name"], capacity=ri["capacity"], r_ctr=(r_rctr, 2 * ri["ctr"] + 1),
                              fields={f: rr for f, (_, rr) in ri["fields"].items()}) for ri in rec_info], aux=aux)
     return "\n".join(src) + "\n", L

@@ -169,6 +169,35 @@ TM_DFN u64 tm_claim(u64* ctr, u32 n) {
   return ((u64)hi << 32) | lo;
 }
 
+// A Records output's slot claim (reference _tally.py:141-160): a wave takes raw slots from a private batch of TM_RB
+// consecutive slots, refilled from the output's slot counter with one atomic per TM_RB slots (one counter hit by
+// every wave of the chip serialises at its L2 channel; per-record or per-append atomics there cost ~30x the item
+// loop).  The batch state (base, slots left, records appended) lives in the wave's LDS words, read by every active
+// lane and written by the first, so lanes that diverged keep one view of it.  The lanes that append take the
+// batch's remaining slots in rank order, then a new batch's: only the last batch of each wave has unused slots.
+// -> the lane's raw slot, or -1 (it does not append, or the slot is past rawcap).
+#define TM_RB 256u
+TM_DFN i64 tm_rclaim(u64* ctr, volatile u64* base_s, volatile u32* left_s, volatile u64* cnt_s, bool when,
+                     u64 rawcap) {
+  const u64 m = tm_ballot(when);
+  if (m == 0ull) return -1;
+  const u32 n = (u32)__builtin_popcountll(m), r = tm_rank(m);
+  const u32 left = *left_s;
+  const u64 base = *base_s;
+  const u64 nb = n > left ? tm_claim(ctr, TM_RB) : 0ull;
+  const u64 s = r < left ? base + (TM_RB - left) + r : nb + (r - left);
+  if (tm_lane() == (int)__builtin_ctzll(tm_ballot(true))) {
+    if (n > left) {
+      *base_s = nb;
+      *left_s = TM_RB - (n - left);
+    } else {
+      *left_s = left - n;
+    }
+    *cnt_s = *cnt_s + n;
+  }
+  return (when && s < rawcap) ? (i64)s : -1;
+}
+
 // f32 atomic adds that keep subnormals (2^-102 = 0x0c800000)
 TM_DFN void tm_cas_addf(float* a, float v) {
   u32* const u = (u32*)a;
