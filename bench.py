@@ -33,7 +33,7 @@ FWD_BYTES_PER_ITEM = 17
 GRAD_BYTES_PER_ITEM = 13
 # HBM bytes per launch at N = 4,194,304 from rocprofv3 counter passes (profiles/c2_random_walk_traffic.md):
 # 2 x FETCH_SIZE + 1 x WRITE_SIZE (KiB), the factors those counters read on a plain 1 GiB device copy
-MEASURED_TRAFFIC = {"forward": 76_430_824, "gradient": 56_952_672}
+MEASURED_TRAFFIC = {"forward": 77_128_984, "gradient": 56_958_568}
 
 
 def cpu_baseline(x0, keys, drift, max_steps, target_s=10.0):
