@@ -4,11 +4,12 @@ An item function of ONE item (its own while loop, its own jax.random draws, resu
 tallies) is traced into a jaxpr-shaped program, lowered to HIP, compiled with hipRTC for gfx950 and launched as
 one persistent wave64 kernel through the C-ABI library libtallymap_rocm.so.  Reverse-mode gradients run the
 replay adjoint (a step-scheduled replay over a tape in HBM, or an ordinary item program when no loop carry needs a
-reverse sweep) through the same path; forward-mode derivatives (jvp, jacfwd) run one fused tangent kernel.
+reverse sweep) through the same path; forward-mode derivatives (jvp, jacfwd) run one fused tangent kernel.  Items
+that spawn children (Queue) run generation by generation, one launch of the same kernel per generation.
 """
 from . import lax, numpy, random
-from ._api import STATS, Records, Result, Sum, TallyError, UnsupportedError, grad, jacfwd, jvp, vjp, vmap
+from ._api import STATS, Queue, Records, Result, Sum, TallyError, UnsupportedError, grad, jacfwd, jvp, vjp, vmap
 from ._tally import Tally
 
 __version__ = "0.1.0"
-__all__ = ["vmap", "vjp", "grad", "jvp", "jacfwd", "Sum", "Records", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]
+__all__ = ["vmap", "vjp", "grad", "jvp", "jacfwd", "Sum", "Queue", "Records", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]

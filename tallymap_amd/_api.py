@@ -86,6 +86,23 @@ class Records:
         return f"Records({ {k: v.name for k, v in self.fields.items()} }, capacity={self.capacity})"
 
 
+@dataclasses.dataclass(frozen=True)
+class Queue:
+    """The spawn queue of `capacity` pending children (reference _api.py:88-96): with vmap(..., spawn=Queue(Q)) an
+    item may call t = t.spawn(child, when=...), a new item with the per-item inputs `child` (the structure of the
+    mapped arguments) that runs the same function on the same broadcast arguments; its per-item result is
+    discarded.  This backend runs the children generation by generation: every launch's children wait in a buffer
+    of Q slots and become the next launch's items.  A child beyond Q in one generation is dropped and counted in
+    stats['children_dropped'], and the call's float outputs are NaN (never a silently truncated shower; integer
+    outputs cannot be NaN and are left as they are).  stats['spawned'] counts the children that ran and
+    stats['children_truncated'] those that hit max_steps (which poisons like a truncated item)."""
+    capacity: int
+
+    def __post_init__(self):
+        if not 0 < int(self.capacity) <= MAX_ITEMS:
+            raise ValueError(f"tallymap: Queue capacity must be in [1, 2^31 - 1], got {self.capacity}")
+
+
 class Result(collections.namedtuple("Result", "outputs per_item truncated stats")):
     """outputs: {name: summed output}; per_item: per-item results (None if the item returns only its tally);
     truncated: bool[N]; stats: {name: int32 scalar} (reference _api.py:180-189)."""
@@ -119,6 +136,7 @@ class ItemProgram:
     where: str = ""
     records: tuple = ()        # ((name, capacity, ((field, dtype), ...)), ...): the Records outputs
     counts: tuple = ()         # per Records output: the index among the per-item results of its per-item count
+    spawn: int = None          # the spawn Queue's capacity (None: the item cannot spawn)
 
     @property
     def nT(self):
@@ -141,11 +159,15 @@ class ItemProgram:
         d = self.__dict__.get("_digest")
         if d is None:
             d = self.__dict__["_digest"] = digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag,
-                                                                            repr(self.records), self.counts))
+                                                                            repr(self.records), self.counts,
+                                                                            self.spawn))
         return d
 
 
 # ----------------------------------------------------------------------------------------- tally checks
+TALLY_OPS = ("tallymap_emit", "tallymap_claim", "tallymap_put", "tallymap_spawn")     # operand 0: the tally threaded
+
+
 def check_tallies(jx, nT, where=""):
     """every tally value is used exactly once, only to thread it: by an emit (its operand 0), as a while / cond
     carry, or as a program output (reference _rewrite.py:41-56).  Raises TallyError."""
@@ -166,11 +188,11 @@ def _flow(jx, tin, where, allow_drop=False):
     for e in jx.eqns:
         for j, v in enumerate(e.invars):
             if isinstance(v, C.Var) and v.id in tv:
-                if not ((e.prim in ("tallymap_emit", "tallymap_claim", "tallymap_put") and j == 0)
+                if not ((e.prim in TALLY_OPS and j == 0)
                         or e.prim in ("while", "cond", "copy")):
                     raise TallyError(f"tallymap: a tally is read by `{e.prim}` in the item function {where}: "
                                      "tallies are write-only (t = t.add(...)), used linearly")
-        if e.prim in ("tallymap_emit", "tallymap_claim", "tallymap_put"):
+        if e.prim in TALLY_OPS:
             consume(e.invars[0])
             tv.add(e.outvars[0].id)
         elif e.prim == "copy":
@@ -280,9 +302,10 @@ def item_name(fn):
     return f"{q} ({code.co_filename}:{code.co_firstlineno})" if code else q
 
 
-def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None):
-    """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves)."""
-    from ._tally import KI, KK, RSEP, rkey
+def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None, spawn=None, ctree=None):
+    """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves);
+    spawn: the Queue capacity (ctree: the structure a spawned child must have)."""
+    from ._tally import KI, KK, QKEY, RSEP, rkey
     tspecs = []
     recs = []
     for n in sorted(outs_spec):
@@ -313,6 +336,10 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         if int(np.prod(shape, dtype=np.int64)) > MAX_ITEMS:
             raise ValueError(f"tallymap: output {n!r} has more than 2^31 - 1 cells")
         tspecs.append(TSpec(n, shape, dt, exact, fixed=fixed, scale=scale))
+    if spawn is not None:
+        if recs:
+            raise UnsupportedError("tallymap: Records outputs together with spawn are not supported by this backend")
+        tspecs.append(TSpec(QKEY, (1,), C.I32, kind="discard"))    # the spawn token (orders t.spawn like an emit)
     names = [s.name for s in tspecs]
     where = item_name(fn)
     tav = [C.AVal((s.S,), s.dtype) for s in tspecs]
@@ -331,7 +358,8 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         if recs:
             cid = C.bind("tallymap_item_index", [], [C.AVal((), C.I32)])[0]
             rec0 = {r: (0, cid) for r, _, _ in recs}
-        t = Tally({n: x for n, x in zip(names, tin)}, shapes, rec0, tuple(recs) or None)
+        rinfo = tuple(recs) + (((QKEY, ctree, tuple(pav)),) if spawn is not None else ())
+        t = Tally({n: x for n, x in zip(names, tin)}, shapes, rec0, rinfo or None)
         m = unflatten(ptree, pin) if ptree is not None else pin
         bb = unflatten(btree, bin_) if btree is not None else bin_
         mi, bi = iter(m), iter(bb)
@@ -375,7 +403,8 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     if b.captured:
         raise C.TraceError("tallymap: the item function closes over a traced value of another call")
     check_tallies(jx, len(tspecs), where)
-    prog = ItemProgram(jx, tuple(tspecs), len(pav), len(bav), trunc, "primal", where, tuple(recs), tuple(counts))
+    prog = ItemProgram(jx, tuple(tspecs), len(pav), len(bav), trunc, "primal", where, tuple(recs), tuple(counts),
+                       int(spawn) if spawn is not None else None)
     return prog, meta
 
 
@@ -385,6 +414,15 @@ def _split_ys(prog, ys):
     hidden = set(prog.counts) | ({prog.trunc} if prog.trunc is not None else set())
     own = [y for j, y in enumerate(ys) if j not in hidden]
     return own, (ys[prog.trunc] if prog.trunc is not None else None)
+
+
+def _truncation(trunc, ntr, N):
+    """Result.truncated and stats['n_truncated']: without max_steps no item is truncated (bool[N] zeros, an int32
+    zero), as in the reference (_api.py:689-693)."""
+    if trunc is not None:
+        return trunc, ntr
+    import torch
+    return torch.zeros((N,), dtype=torch.bool, device="cuda"), torch.zeros((), dtype=torch.int32, device="cuda")
 
 
 def _record_outputs(prog, o, res_out, stats):
@@ -400,7 +438,7 @@ def _record_outputs(prog, o, res_out, stats):
         stats["records_mismatch"][r] = 0          # (one pass: no replay whose counts could disagree)
 
 
-def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts):
+def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="auto", **opts):
     """Map `fn(tally, *args) -> tally | (tally, y)` over the leading axis of the mapped args (reference
     _api.py:428-700).
 
@@ -408,6 +446,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
     in_axes:   0 (mapped) or None (broadcast) per positional argument
     max_steps: cap on every top-level while loop; an item that hits it is flagged in Result.truncated and makes
                every float tally of the call NaN
+    spawn:     tallymap_amd.Queue(capacity) to allow t.spawn(child) (forward calls; run generation by generation)
     backend:   'auto' / 'hip' (the HIP kernel backend; it never falls back)
     opts:      schedule 'step' (default: a lane refills at loop-step granularity) | 'item'; block (threads per
                block, default 256); refill (idle lanes a wave waits for before it claims, default 1); compact
@@ -420,7 +459,10 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
                are accepted for drop-in compatibility and have no meaning on ROCm.
     """
     if fn is None:
-        return lambda f: vmap(f, outputs=outputs, in_axes=in_axes, max_steps=max_steps, backend=backend, **opts)
+        return lambda f: vmap(f, outputs=outputs, in_axes=in_axes, max_steps=max_steps, spawn=spawn, backend=backend,
+                              **opts)
+    if spawn is not None and not isinstance(spawn, Queue):
+        raise TypeError("tallymap: spawn must be tallymap_amd.Queue(capacity)")
     bad = sorted(set(opts) - set(OPTS))
     if bad:
         raise ValueError(f"tallymap: unknown option(s) {bad}; options are " + ", ".join(OPTS))
@@ -450,13 +492,15 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
         pav = [C.AVal(_shape(x)[1:], _np_dtype(x)) for x in pi]
         bav = [C.AVal(_shape(x), _np_dtype(x)) for x in bc]
         key = (tuple(pav), tuple(bav), tuple(axes), str(ptree), str(btree), max_steps,
-               tuple(sorted((n, repr(v)) for n, v in outs_spec.items())))
+               tuple(sorted((n, repr(v)) for n, v in outs_spec.items())), spawn)
         hit = _PROGS.get((id(fn), key))
         if hit is not None and hit[0] is fn:
             _PROGS.move_to_end((id(fn), key))
             prog, meta = hit[1], hit[2]
         else:
-            prog, meta = build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree, btree)
+            ctree = flatten(margs[0] if len(margs) == 1 else margs)[1] if spawn is not None else None
+            prog, meta = build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree, btree,
+                                       spawn.capacity if spawn is not None else None, ctree)
             _PROGS[(id(fn), key)] = (fn, prog, meta)
             while len(_PROGS) > PROG_CACHE:
                 _PROGS.popitem(last=False)
@@ -469,8 +513,10 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, backend="auto", **opts)
         tn = [s.name for s in prog.tallies]
         res_out = {n: o.tallies[tn.index(n)].reshape(prog.tallies[tn.index(n)].shape) for n in names if n in tn}
         stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
+        if prog.spawn is not None:
+            stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
         ys, trunc = _split_ys(prog, list(o.ys))
-        stats["n_truncated"] = o.n_truncated
+        trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
         _record_outputs(prog, o, res_out, stats)
         per_item = unflatten(meta["ytree"], ys)
         return Result(res_out, per_item, trunc, stats)
@@ -517,6 +563,9 @@ def vjp(mapped, *args, argnums=None):
 def _pullback(mapped, args, argnums):
     from . import backend as B
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
+    if prog.spawn is not None:
+        raise UnsupportedError("tallymap: reverse mode through spawn (the tree adjoint) is not supported by this "
+                               "backend")
     an = _argnums(argnums, len(args))
     wrt = _float_args(prog, axes, an)
 
@@ -580,6 +629,8 @@ def _run_tangents(mapped, args, tans, lanes):
     of the float per-item results (None for the others)])."""
     from . import backend as B
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
+    if prog.spawn is not None:
+        raise UnsupportedError("tallymap: forward mode through spawn is not supported by this backend")
     pt, bt, pp, pb = [], [], [], []
     for pos, x in enumerate(axes):
         leaves, _ = flatten(args[pos])
@@ -601,7 +652,7 @@ def _run_tangents(mapped, args, tans, lanes):
     ny = len(prog.y_avals())
     ys, trunc = _split_ys(prog, list(o.ys[:ny]))
     stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
-    stats["n_truncated"] = o.n_truncated
+    trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
     _record_outputs(prog, o, res_out, stats)
     primal = Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
     t_tal = [dict() for _ in range(lanes)]

@@ -16,6 +16,7 @@ from . import _core as C
 # canonical layout).
 RSEP = "\x1f"
 KI, KK = RSEP + "i", RSEP + "k"
+QKEY = RSEP + "q"          # the spawn token: a hidden discard tally that orders t.spawn like an emit
 
 
 def rkey(name, field):
@@ -30,11 +31,14 @@ class Tally:
         self._a = dict(arrays)
         self._shapes = dict(shapes)
         self._r = dict(rec or {})        # Records name -> (k, cid): the append ordinal and the item index
-        self._ri = rinfo                 # static: ((name, capacity, ((field, dtype), ...)), ...)
+        self._ri = rinfo                 # static: ((name, capacity, ((field, dtype), ...)), ...) [+ spawn info]
 
     @classmethod
     def _from(cls, a, shapes, rec=None, rinfo=None):
         return cls(a, shapes, rec, rinfo)
+
+    def _records_info(self):
+        return tuple(r for r in (self._ri or ()) if r[0] != QKEY)
 
     def _shapes_key(self):
         return tuple(sorted((n, tuple(s)) for n, s in self._shapes.items()))
@@ -45,7 +49,13 @@ class Tally:
         return Tally(a, self._shapes, self._r, self._ri)
 
     def _records(self):
-        return {n: (c, f) for n, c, f in (self._ri or ())}
+        return {n: (c, f) for n, c, f in self._records_info()}
+
+    def _spawn_info(self):
+        for r in (self._ri or ()):
+            if r[0] == QKEY:
+                return r[1], r[2]          # (child treedef, child leaf avals)
+        return None
 
     def add(self, name, index, value):
         """tally[name][index] += value.  index: an int (flat index of a 1-D output) or a tuple of ints, one per
@@ -140,7 +150,7 @@ class Tally:
         kk = self._a[rkey(name, KK)]
         kv = k.var if C.is_traced(k) else C.literal(int(k), C.I32, weak=False)
         wv = w.var if C.is_traced(w) else C.literal(True, C.BOOL, weak=False)
-        idx = [n for n, _, _ in self._ri].index(name)
+        idx = [n for n, _, _ in self._records_info()].index(name)
         tok, slot = C.bind("tallymap_claim", [kk.var, wv, kv], [kk.aval, C.AVal((), C.I32)], r=idx, capacity=cap)
         keys = [rkey(name, f) for f, _ in fields] + [rkey(name, KI)]
         ops = tuple(self._a[key] for key in keys) + (tok,)
@@ -158,6 +168,46 @@ class Tally:
         a = dict(self._a)
         a.update(zip(keys + [rkey(name, KK)], ts))
         return Tally(a, self._shapes, {**self._r, name: (k2, cid)}, self._ri)
+
+    def spawn(self, child, when=True):
+        """Append a new item whose per-item inputs are `child` (the structure of the mapped arguments); it runs the
+        same function on the shared broadcast arguments, its own per-item result discarded (reference
+        _tally.py:286-300).  Needs tallymap_amd.vmap(..., spawn=Queue(capacity))."""
+        info = self._spawn_info()
+        if info is None:
+            raise ValueError("tallymap: spawn needs tallymap_amd.vmap(..., spawn=tallymap_amd.Queue(capacity))")
+        tree, avals = info
+        from ._tree import flatten
+        leaves, td = flatten(child)
+        if td != tree or len(leaves) != len(avals):
+            raise TypeError(f"tallymap: spawned child structure {td} != the mapped inputs {tree}")
+        vs = []
+        for x, a in zip(leaves, avals):
+            if C.is_traced(x):
+                if x.shape != a.shape:
+                    raise TypeError(f"tallymap: spawned child leaf of shape {x.shape}, the mapped input is {a.shape}")
+                if x.dtype != a.dtype:
+                    if np.issubdtype(a.dtype, np.integer) and np.issubdtype(x.dtype, np.inexact):
+                        raise TypeError(f"tallymap: a float spawned child leaf for the {a.dtype} mapped input")
+                    x = C.convert(x, a.dtype)
+                vs.append(x.var)
+            else:
+                x = np.asarray(x)
+                if np.issubdtype(a.dtype, np.integer) and np.issubdtype(x.dtype, np.inexact):
+                    raise TypeError(f"tallymap: a float spawned child leaf for the {a.dtype} mapped input")
+                vs.append(C.Lit(np.broadcast_to(x, a.shape).astype(a.dtype), C.AVal(a.shape, a.dtype)))
+        w = when
+        if C.is_traced(w):
+            if w.dtype != C.BOOL or w.shape != ():
+                raise TypeError("tallymap: spawn `when` must be a scalar bool")
+        elif not isinstance(w, (bool, np.bool_)):
+            raise TypeError("tallymap: spawn `when` must be a scalar bool")
+        elif not w:
+            return self
+        wv = w.var if C.is_traced(w) else C.literal(True, C.BOOL, weak=False)
+        tok = self._a[QKEY]
+        new = C.bind("tallymap_spawn", [tok.var, wv] + vs, [tok.aval])[0]
+        return self._with(QKEY, new)
 
 
 def _check_int(i):

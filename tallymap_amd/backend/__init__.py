@@ -90,8 +90,13 @@ def compiled(prog, opts, adjoint=None):
 
 def launch(c, ins, N, stream=None):
     """allocate c's results and queue its kernels -> the result tensors (in layout order)."""
-    import ctypes
+    outs = _alloc(c, N)
+    _queue(c, ins, outs, N, c.layout.n_zero, c.layout.flags, stream)
+    return outs
 
+
+def _alloc(c, N):
+    """c's result tensors for a launch over N items (uninitialised: tm_zero clears what must start at zero)."""
     import torch
     L = c.layout
     outs = []
@@ -108,17 +113,26 @@ def launch(c, ins, N, stream=None):
         else:
             sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
         outs.append(torch.empty(sh, dtype=torch_dtype(dt), device="cuda"))
+    return outs
+
+
+def _queue(c, ins, outs, N, n_zero, flags, stream=None):
+    """queue c's kernels over N items on `stream` (default: torch's current one): tm_zero when n_zero, tm_main
+    when N > 0, tm_post when flags & 2, then the auxiliary passes of the layout."""
+    import ctypes
+
+    import torch
+    L = c.layout
     bufs = [t.data_ptr() for t in ins] + [t.data_ptr() for t in outs]
     arr = (ctypes.c_void_p * len(bufs))(*bufs)
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
-    Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), L.n_zero, L.flags, N, c.block))
+    Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), n_zero, flags, N, c.block))
     for name, kind, block, cap in (getattr(L, "aux", None) or []):
         if N == 0 and kind != "cap":         # (no item ran: only the canonical outputs are written, as zeros)
             continue
         grid = {"items": -(-int(N) // 1024), "one": 1, "cap": min(-(-int(cap) // 256), 4096),
                 "waves": max(1, -(-(_lanes(c, N) // 64) // 256))}[kind]
         Cm.check(Cm.lib().tm_launch_aux(c.id, name.encode(), ctypes.c_void_p(s), arr, len(bufs), N, grid, block))
-    return outs
 
 
 def run(prog, pi, bc, N, opts):
@@ -132,6 +146,8 @@ def run(prog, pi, bc, N, opts):
     for x, a in zip(ins[prog.nP:], prog.b_avals()):
         if tuple(x.shape) != tuple(a.shape):
             raise ValueError(f"tallymap_amd: broadcast operand of shape {tuple(x.shape)}, expected {a.shape}")
+    if getattr(prog, "spawn", None) is not None:
+        return _run_spawn(c, prog, ins, N)
     res = launch(c, ins, N)
     L = c.layout
     base = L.n_in
@@ -145,6 +161,58 @@ def run(prog, pi, bc, N, opts):
         b, w = ri["r_ctr"]
         rcount.append(res[b - base].view(__import__("torch").int64)[w])
     return Outputs(tallies, stats, ys, ntr, recs, rcount)
+
+
+def _run_spawn(c, prog, ins, N):
+    """a spawning program, generation by generation (the reference's one-launch ticket ring, backends/kernel/
+    kernel.py:1006-1040, made a host loop of ordinary launches: no wave ever waits for another).  Generation 0 runs
+    the N items with tm_zero; each launch's children (their per-item operands in the Q-row buffers of the layout,
+    the ticket counter in ctl words 4-5) are the next launch's items, without tm_zero, so the tallies and stats
+    accumulate; tickets past Q are dropped children.  The loop ends at the first generation that spawns nothing
+    (one device-to-host read of ctl per generation); the host then writes stats spawned / children_dropped /
+    children_truncated and tm_post runs once (a dropped or truncated child poisons the float tallies there)."""
+    import torch
+    L = c.layout
+    base = L.n_in
+    Q = int(prog.spawn)
+    outs = _alloc(c, N)
+    ctl = outs[L.r_ctl - base].view(torch.int32)
+    cur = [outs[r - base] for r in L.r_q]          # the buffers the last launch's children were written to
+    spare, ys_scr = None, None
+    _queue(c, ins, outs, N, L.n_zero, 0)
+    spawned = dropped = 0
+    ntr_roots = None
+    while True:
+        w = ctl.cpu().numpy().view(np.uint32)
+        if ntr_roots is None:
+            ntr_roots = int(w[2])
+        cnt = int(w[4]) | (int(w[5]) << 32)
+        if cnt == 0:
+            break
+        n = min(cnt, Q)
+        spawned += n
+        dropped += cnt - n
+        if spare is None:
+            spare = [torch.empty_like(t) for t in cur]
+            ys_scr = {r: torch.empty((Q,) + tuple(outs[r - base].shape[1:]), dtype=outs[r - base].dtype,
+                                     device="cuda") for r in L.r_ys}
+        ctl[0:2].zero_()                               # the item claim counter
+        ctl[4:6].zero_()                               # the ticket counter
+        gen = list(outs)
+        for r, t in zip(L.r_q, spare):
+            gen[r - base] = t
+        for r, t in ys_scr.items():                    # (a child's own per-item result is discarded)
+            gen[r - base] = t
+        _queue(c, cur + list(ins[prog.nP:]), gen, n, 0, 0)
+        cur, spare = spare, cur
+    big = 2 ** 31 - 1
+    ctr = int(w[2]) - ntr_roots
+    outs[L.r_stats - base][0:3].copy_(torch.tensor([min(spawned, big), min(dropped, big), ctr], dtype=torch.int32))
+    _queue(c, ins, outs, 0, 0, L.flags)
+    tallies = [outs[L.r_out[k] - base] for k in prog.out_tallies]
+    ys = [outs[r - base] for r in L.r_ys]
+    ntr = torch.tensor(ntr_roots, dtype=torch.int32, device="cuda") if prog.trunc is not None else None
+    return Outputs(tallies, outs[L.r_stats - base], ys, ntr, {}, [])
 
 
 _LANES = {}

@@ -52,6 +52,8 @@ class Layout:
     # per Records output: dict(name, capacity, r_ctr (its u64 record count: result index, word), fields {suffix:
     # canonical result index}), and aux: the passes (entry name, grid kind, block) run after tm_launch
     aux: list = dataclasses.field(default_factory=list)
+    # spawn: the next generation's per-item operand buffers (result indices, one per per-item operand, Q rows)
+    r_q: list = dataclasses.field(default_factory=list)
 
 
 def _split(jx):
@@ -277,6 +279,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     r_stats = result((5,), np.int32)
     n_zero = len(res)
     r_ys = [result(a.shape, a.dtype, per_item=True) for a in yav]
+    Q = getattr(prog, "spawn", None)
+    r_q = [result((Q,) + tuple(a.shape), a.dtype) for a in pav] if Q is not None else []
     r_rex = result((), np.int64, per_item=True) if recs else None       # the Records scans' scratch (per item)
     r_rbs = result((), np.int64, per_item=True) if recs else None
     for ri in rec_info:        # per launched wave: the unused slot range [s0, s1) of its last batch (+ a count)
@@ -377,6 +381,23 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         return t
     em.hooks["tallymap_put"] = put_rule
     em.hooks["tallymap_item_index"] = lambda em_, e, ins: Val(["((i32)tm_item)"], (), C.I32)
+
+    def spawn_rule(em_, e, ins):
+        """a spawned child: a ticket of the next generation's buffer (tm_qclaim: one counter atomic per wave at this
+        point), its per-item operands stored in that row when the ticket is below the capacity Q (the host counts
+        the tickets past Q as dropped children).  The counter is ctl words 4-5."""
+        t, w, leaves = ins[0], ins[1], ins[2:]
+        if Q is None or len(leaves) != nP:
+            raise RuntimeError("internal: a spawn in a program without a queue of its per-item operands")
+        tq = em_.bind(f"tm_qclaim(tm_ctr + 2, {w.el[0]})", C.I64, "tq")
+        em_.open(f"if ((u64){tq} < {int(Q)}ull)")
+        for i, (lv, a) in enumerate(zip(leaves, pav)):
+            ct, n = ctype(a.dtype), max(1, a.size)
+            for el in range(n):
+                em_.line(f"(({ct}*)P.p[{r_q[i]}])[{tq} * {n} + {el}] = {lv.el[el]};")
+        em_.close()
+        return t
+    em.hooks["tallymap_spawn"] = spawn_rule
 
     # --------------------------------------------------------------------------------- the item's code
     w = _split(jx) if schedule == "step" else None
@@ -564,6 +585,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     bad = ["TM_CTL[2] != 0u"] if prog.trunc is not None else []
     # a Records output past its capacity poisons every float output of the call (reference _api.py:120-131)
     bad += [f"((const u64*)P.p[{r_rctr}])[{2 * ri['ctr'] + 1}] > {ri['capacity']}ull" for ri in rec_info]
+    if Q is not None:          # a dropped child (set by the host from the generations' ticket counts)
+        bad.append("TM_STATS[1] != 0")
     if bad and poison:
         # (the readout and the poison visit a bin from the same thread, in program order)
         post.append(f"const bool tm_bad = {' || '.join(bad)};")
@@ -830,7 +853,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         aux += [(f"tm_rholes{j}", "waves", 256, cap), (f"tm_rscan{j}", "items", 1024, cap),
                 (f"tm_rtop{j}", "one", 1024, cap), (f"tm_rcanon{j}", "cap", 256, cap)]
     L = Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_out, r_ctl=r_ctl, r_stats=r_stats, r_ys=r_ys,
-               flags=flags, mode=mode, priv=priv, zero_words=zero_words,
+               flags=flags, mode=mode, priv=priv, zero_words=zero_words, r_q=r_q,
                records=[dict(name=ri["name"], capacity=ri["capacity"], r_ctr=(r_rctr, 2 * ri["ctr"] + 1),
                              fields={f: rr for f, (_, rr) in ri["fields"].items()}) for ri in rec_info], aux=aux)
     return "\n".join(src) + "\n", L

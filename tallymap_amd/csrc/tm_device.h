@@ -169,6 +169,15 @@ TM_DFN u64 tm_claim(u64* ctr, u32 n) {
   return ((u64)hi << 32) | lo;
 }
 
+// A spawned child's row in the next generation's buffer (reference _tally.py:284-300): the lanes that spawn at this
+// point take consecutive tickets with one counter atomic per wave -> the lane's ticket, or -1 (it does not spawn).
+TM_DFN i64 tm_qclaim(u64* ctr, bool when) {
+  const u64 m = tm_ballot(when);
+  if (m == 0ull) return -1;
+  const u64 b = tm_claim(ctr, (u32)__builtin_popcountll(m));
+  return when ? (i64)(b + tm_rank(m)) : -1;
+}
+
 // A Records output's slot claim (reference _tally.py:141-160): a wave takes raw slots from a private batch of TM_RB
 // consecutive slots, refilled from the output's slot counter with one atomic per TM_RB slots (one counter hit by
 // every wave of the chip serialises at its L2 channel; per-record or per-append atomics there cost ~30x the item

@@ -175,3 +175,44 @@ def test_records_tracing_and_errors():
     with pytest.raises(ValueError, match="capacity"):
         tm.Records({"i": np.int32})
     assert tm.Records(16, {"i": np.int32}).capacity == 16
+
+
+def test_spawn_tracing_and_errors():
+    """t.spawn: a hidden token tally threaded like an emit, one `tallymap_spawn` per spawn with the child's leaves
+    (converted to the mapped inputs' dtypes); the generated kernel claims tickets per wave and bounds them by the
+    capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input, Records
+    with spawn and the derivative paths through spawn raise (reference edge.py:183-188)."""
+    from tallymap_amd._tally import QKEY
+    from tallymap_amd.backend import kernel as K
+
+    def item(t, g, x):
+        def body(i, t):
+            return t.spawn((g + 1, x * 0.5), when=g < 2)
+        return lax.fori_loop(0, 2, body, t.add("h", 0, x))
+    f = tm.vmap(item, outputs={"h": tm.Sum((2,))}, spawn=tm.Queue(100))
+    g0, xs = np.zeros(10, np.int32), np.ones(10, np.float32)
+    p = f._prepare((g0, xs))[0]
+    assert p.spawn == 100 and [s.name for s in p.tallies] == ["h", QKEY] and p.tallies[1].kind == "discard"
+    w = next(e for e in p.jaxpr.eqns if e.prim == "while")
+    sp = [e for e in w.params["body_jaxpr"].eqns if e.prim == "tallymap_spawn"]
+    assert len(sp) == 1 and [v.aval.dtype for v in sp[0].invars[2:]] == [np.int32, np.float32]
+    src, L = K.build(p)
+    assert "tm_qclaim(tm_ctr + 2," in src and "< 100ull" in src and len(L.r_q) == 2
+    assert "TM_STATS[1] != 0" in src                 # a dropped child poisons the float outputs
+    with pytest.raises(ValueError, match="Queue"):
+        tm.vmap(lambda t, x: t.spawn(x), outputs={"h": tm.Sum((1,))})._prepare((xs,))
+    with pytest.raises(TypeError, match="structure"):
+        tm.vmap(lambda t, g, x: t.spawn(x), outputs={"h": tm.Sum((1,))}, spawn=tm.Queue(8))._prepare((g0, xs))
+    with pytest.raises(TypeError, match="float spawned child"):
+        tm.vmap(lambda t, g, x: t.spawn((x, x)), outputs={"h": tm.Sum((1,))}, spawn=tm.Queue(8))._prepare((g0, xs))
+    with pytest.raises(tm.UnsupportedError, match="Records"):
+        tm.vmap(lambda t, x: t.append("r", {"v": x}).spawn(x), outputs={"r": tm.Records({"v": np.float32}, 8)},
+                spawn=tm.Queue(8))._prepare((xs,))
+    with pytest.raises(tm.UnsupportedError, match="spawn"):
+        tm.grad(f)(g0, xs)
+    with pytest.raises(tm.UnsupportedError, match="spawn"):
+        tm.jvp(f, (g0, xs), (None, xs))
+    with pytest.raises(TypeError, match="Queue"):
+        tm.vmap(item, outputs={"h": tm.Sum((2,))}, spawn=100)
+    with pytest.raises(ValueError, match="capacity"):
+        tm.Queue(0)

@@ -1,0 +1,241 @@
+"""Spawned children on the GPU (tm.Queue + t.spawn, reference _api.py:88-96, _tally.py:284-300, backends/kernel/
+kernel.py:1006-1040), run generation by generation: the cascade of the reference's own spawn test (edge.py:960-995)
+against its closed form bitwise (exact tallies: every child's value is the root's times a power of two), a
+branching shower against a numpy emulation of the same tree (the host threefry of tallymap_amd.random, pinned by
+the oracle tests) bitwise, the queue rule (a dropped child poisons the float outputs), truncated children."""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import lax
+from tallymap_amd import numpy as jnp
+from tallymap_amd import random as R
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+NB = 8
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _np(x):
+    return x.cpu().numpy() if hasattr(x, "cpu") else np.asarray(x)
+
+
+def _cascade(t, gen, x):
+    """every item adds x into bin gen; below generation 3 it spawns two children, x / 2 and x / 4."""
+    t = t.add("Q", gen, x)
+    t = t.add("n", 0, 1)
+    t = t.spawn((gen + 1, x * 0.5), when=gen < 3)
+    t = t.spawn((gen + 1, x * 0.25), when=gen < 3)
+    return t
+
+
+def _cascade_inputs(n):
+    return np.zeros(n, np.int32), np.random.default_rng(1).uniform(0.0, 1.0, n).astype(f32)
+
+
+def _cascade_want(xs):
+    """bin g holds (3/4)^g sum(xs) exactly (x / 2 + x / 4 per parent, both exact in float32): the exact sum's
+    correctly rounded float32 (Fraction arithmetic, no rounding before the last step)."""
+    s = sum(Fraction(float(x)) for x in xs)
+    return np.array([float(s * Fraction(3, 4) ** g) if g < 4 else 0.0 for g in range(NB)], f32)
+
+
+@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(block=64)], ids=["step", "item", "block64"])
+def test_spawn_cascade_exact_closed_form(opts):
+    print(f"case: spawn cascade exact N=4096 {opts}", flush=True)
+    g0, xs = _cascade_inputs(4096)
+    f = tm.vmap(_cascade, outputs={"Q": tm.Sum((NB,), fixed_point=True), "n": tm.Sum((1,), np.int32)},
+                spawn=tm.Queue(1 << 16), **opts)
+    res = f(g0, xs)
+    _sync()
+    st = {k: int(_np(v)) for k, v in res.stats.items()}
+    assert st["spawned"] == 4096 * 14 and st["children_dropped"] == 0 and st["children_truncated"] == 0, st
+    assert set(res.stats) == {"fixed_point_overflow", "dropped_emits", "spawned", "children_dropped",
+                              "children_truncated", "n_truncated"}
+    assert np.array_equal(_np(res.outputs["Q"]).view(np.uint32), _cascade_want(xs).view(np.uint32))
+    assert int(_np(res.outputs["n"])[0]) == 4096 * 15
+
+
+def test_spawn_cascade_float_sum():
+    """the plain float32 tally (atomic adds in any order): within 1e-5 of the float64 sum."""
+    print("case: spawn cascade f32 N=65536", flush=True)
+    g0, xs = _cascade_inputs(65_536)
+    res = tm.vmap(_cascade, outputs={"Q": tm.Sum((NB,)), "n": tm.Sum((1,), np.int32)}, spawn=tm.Queue(1 << 20))(g0, xs)
+    _sync()
+    want = _cascade_want(xs).astype(np.float64)
+    got = _np(res.outputs["Q"]).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + 1e-30), (got, want)
+
+
+def test_spawn_small_queue_drops_and_poisons():
+    """Queue(16): each generation keeps its first 16 children (generation 0 spawns 2N, generations 1 and 2 spawn
+    32 each from their 16 items); the rest are dropped and counted, the float output is NaN, the integer one is
+    left alone (it counts the N roots and the 48 children that ran).  The reference's rule holds: spawned +
+    dropped <= the tree's N * 14 children."""
+    print("case: spawn Queue(16) drops", flush=True)
+    n = 1000
+    g0, xs = _cascade_inputs(n)
+    res = tm.vmap(_cascade, outputs={"Q": tm.Sum((NB,)), "n": tm.Sum((1,), np.int32)}, spawn=tm.Queue(16))(g0, xs)
+    _sync()
+    sp, dr = int(_np(res.stats["spawned"])), int(_np(res.stats["children_dropped"]))
+    assert (sp, dr) == (48, 2 * n - 16 + 32) and sp + dr <= n * 14
+    assert np.isnan(_np(res.outputs["Q"])).all()
+    assert int(_np(res.outputs["n"])[0]) == n + 48
+
+
+def _looper(t, gen, x):
+    k, t = lax.while_loop(lambda c: c[0] < 100, lambda c: (c[0] + 1, c[1]), (0, t))
+    t = t.add("Q", 0, x)
+    return t.spawn((gen + 1, x), when=gen < 1)
+
+
+def test_spawn_children_truncated():
+    """max_steps=5 truncates every root and every child: n_truncated counts the roots, children_truncated the
+    children, and the float output is NaN (reference edge.py:991-996)."""
+    print("case: spawn children truncated", flush=True)
+    g0, xs = _cascade_inputs(777)
+    res = tm.vmap(_looper, outputs={"Q": tm.Sum((NB,))}, spawn=tm.Queue(1 << 10), max_steps=5)(g0, xs)
+    _sync()
+    assert int(_np(res.stats["children_truncated"])) == 777 and int(_np(res.stats["n_truncated"])) == 777
+    assert int(_np(res.stats["spawned"])) == 777
+    assert np.isnan(_np(res.outputs["Q"])).all() and _np(res.truncated).all()
+
+
+def test_spawn_never_taken_equals_plain_call():
+    """a spawn whose `when` is never true: the same outputs, bitwise, as the program without spawn."""
+    print("case: spawn never taken", flush=True)
+    g0, xs = _cascade_inputs(50_000)
+    g0 = g0 + 3
+    out = {"Q": tm.Sum((NB,), fixed_point=True), "n": tm.Sum((1,), np.int32)}
+    a = tm.vmap(_cascade, outputs=out, spawn=tm.Queue(64))(g0, xs)
+
+    def plain(t, gen, x):
+        return t.add("Q", gen, x).add("n", 0, 1)
+    b = tm.vmap(plain, outputs=out)(g0, xs)
+    _sync()
+    assert int(_np(a.stats["spawned"])) == 0
+    assert np.array_equal(_np(a.outputs["Q"]).view(np.uint32), _np(b.outputs["Q"]).view(np.uint32))
+    assert np.array_equal(_np(a.outputs["n"]), _np(b.outputs["n"]))
+
+
+# ------------------------------------------------------------------------------------------------ the shower
+NZ, DEPTH = 16, 6
+TH = (f32(0.2), f32(0.6))
+
+
+def _particle(t, p, theta):
+    """a particle deposits theta[0] of its energy per step along z and, with probability 0.35 per step below
+    generation DEPTH, splits off a child carrying theta[1] x (0.5 .. 1) of what is left; it returns its step
+    count and remaining energy."""
+    def body(c):
+        s, n, t = c
+        k = R.fold_in(s["key"], n)
+        u = R.uniform(k, (3,))
+        z = s["z"] + u[0] * 0.5
+        dep = s["E"] * theta[0]
+        t = t.add("dep", jnp.clip(jnp.floor(z * 2.0).astype(jnp.int32), 0, NZ - 1), dep)
+        split = (u[1] < 0.35) & (s["g"] < DEPTH)
+        ec = (s["E"] - dep) * theta[1] * (0.5 + 0.5 * u[2])
+        t = t.spawn(dict(E=ec, z=z, key=R.fold_in(k, 1), g=s["g"] + 1), when=split)
+        e = s["E"] - dep - jnp.where(split, ec, 0.0)
+        return dict(E=e, z=z, key=s["key"], g=s["g"]), n + 1, t
+    s, n, t = lax.while_loop(lambda c: (c[0]["E"] > 1e-3) & (c[1] < 40), body, (p, 0, t))
+    t = t.add("count", s["g"], 1)
+    return t, (n, s["E"])
+
+
+def _roots(n):
+    E = np.linspace(1.0, 2.0, n, dtype=f32)
+    keys = R._host_split(np.array([0, 7], np.uint32), n)
+    return dict(E=E, z=np.zeros(n, f32), key=keys, g=np.zeros(n, np.int32))
+
+
+def _emulate_shower(roots, theta):
+    """numpy float32, generation by generation, each generation's items in lockstep -> (dep exact-sum terms per
+    bin, count per generation, children, the roots' (n, E))."""
+    dep_terms = [[] for _ in range(NZ)]
+    count = np.zeros(NZ, np.int64)
+    gen = {k: np.asarray(v).copy() for k, v in roots.items()}
+    children = 0
+    root_out = None
+    while len(gen["E"]):
+        m = len(gen["E"])
+        E, z, key, g = gen["E"].astype(f32), gen["z"].astype(f32), gen["key"], gen["g"]
+        n = np.zeros(m, np.int32)
+        kids = {k: [] for k in gen}
+        alive = (E > f32(1e-3)) & (n < 40)
+        while alive.any():
+            i = np.nonzero(alive)[0]
+            k = R._host_fold_in(key[i], n[i].astype(np.uint32))
+            u = R._host_uniform(k, 0.0, 1.0, (3,))
+            zi = (z[i] + u[:, 0] * f32(0.5)).astype(f32)
+            dep = (E[i] * theta[0]).astype(f32)
+            b = np.clip(np.floor(zi * f32(2.0)).astype(np.int32), 0, NZ - 1)
+            for bb, d in zip(b, dep):
+                dep_terms[bb].append(d)
+            split = (u[:, 1] < f32(0.35)) & (g[i] < DEPTH)
+            ec = ((E[i] - dep) * theta[1] * (f32(0.5) + f32(0.5) * u[:, 2])).astype(f32)
+            kids["E"].append(ec[split])
+            kids["z"].append(zi[split])
+            kids["key"].append(R._host_fold_in(k[split], np.ones(int(split.sum()), np.uint32)))
+            kids["g"].append(g[i][split] + 1)
+            E[i] = (E[i] - dep - np.where(split, ec, f32(0.0))).astype(f32)
+            z[i] = zi
+            n[i] += 1
+            alive = (E > f32(1e-3)) & (n < 40)
+        np.add.at(count, g, 1)
+        if root_out is None:
+            root_out = (n.copy(), E.copy())
+        gen = {k: (np.concatenate(v) if v else np.zeros((0,) + gen[k].shape[1:], gen[k].dtype)) for k, v in kids.items()}
+        children += len(gen["E"])
+    return dep_terms, count, children, root_out
+
+
+@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(refill=8)], ids=["step", "item", "refill8"])
+def test_spawn_shower_against_emulation(opts):
+    """the exact deposit profile (each bin the correctly rounded sum of its deposits), the particles per
+    generation, the children count and the roots' own results, bitwise against the numpy emulation of the tree."""
+    print(f"case: spawn shower N=2048 {opts}", flush=True)
+    roots = _roots(2048)
+    theta = np.array(TH, f32)
+    dep_terms, count, children, (n_r, e_r) = _emulate_shower(roots, theta)
+    f = tm.vmap(_particle, outputs={"dep": tm.Sum((NZ,), fixed_point=True), "count": tm.Sum((NZ,), np.int32)},
+                in_axes=(0, None), spawn=tm.Queue(1 << 16), **opts)
+    res = f(roots, theta)
+    _sync()
+    from oracle import exact as X
+    want = np.array([X.exact_sum(np.array(d, f32))[0] if d else f32(0) for d in dep_terms], f32)
+    assert children > 2048 and int(_np(res.stats["spawned"])) == children
+    assert int(_np(res.stats["children_dropped"])) == 0
+    assert np.array_equal(_np(res.outputs["count"]), count.astype(np.int32))
+    assert np.array_equal(_np(res.outputs["dep"]).view(np.uint32), want.view(np.uint32))
+    n_got, e_got = res.per_item
+    assert np.array_equal(_np(n_got), n_r) and np.array_equal(_np(e_got).view(np.uint32), e_r.view(np.uint32))
+
+
+def test_spawn_shower_large_float_sum():
+    """2^20 roots, about 67 million particles and 10^9 deposits in all: the float32 deposit profile against the
+    exact profile (the same call with fixed_point=True), the particle counts equal.  The tolerance is 1e-4, not
+    the 1e-5 of the smaller calls: each bin's float32 sum runs in LDS per workgroup over ~10^5 deposits (as the
+    reference's shared-memory float32 accumulators do, backends/kernel/kernel.py:959-963), whose rounding is
+    ~sqrt(10^5) x 2^-24 = 2e-5 relative."""
+    print("case: spawn shower N=1048576", flush=True)
+    roots = _roots(1 << 20)
+    theta = np.array(TH, f32)
+    outs = {"dep": tm.Sum((NZ,)), "count": tm.Sum((NZ,), np.int32)}
+    a = tm.vmap(_particle, outputs=outs, in_axes=(0, None), spawn=tm.Queue(1 << 25))(roots, theta)
+    b = tm.vmap(_particle, outputs=dict(outs, dep=tm.Sum((NZ,), fixed_point=True)), in_axes=(0, None),
+                spawn=tm.Queue(1 << 25))(roots, theta)
+    _sync()
+    assert int(_np(a.stats["spawned"])) == int(_np(b.stats["spawned"])) > (1 << 20)
+    assert int(_np(a.stats["children_dropped"])) == 0
+    assert np.array_equal(_np(a.outputs["count"]), _np(b.outputs["count"]))
+    x, y = _np(a.outputs["dep"]).astype(np.float64), _np(b.outputs["dep"]).astype(np.float64)
+    assert np.all(np.abs(x - y) <= 1e-4 * np.abs(y) + 1e-30), (x, y)
