@@ -416,6 +416,13 @@ def _split_ys(prog, ys):
     return own, (ys[prog.trunc] if prog.trunc is not None else None)
 
 
+def _sum_outputs(prog, o, names):
+    """{name: the summed output} of the user's outputs among a launch's tallies (in prog.out_tallies order)."""
+    tn = [s.name for s in prog.tallies]
+    at = {slot: i for i, slot in enumerate(prog.out_tallies)}
+    return {n: o.tallies[at[tn.index(n)]].reshape(prog.tallies[tn.index(n)].shape) for n in names if n in tn}
+
+
 def _truncation(trunc, ntr, N):
     """Result.truncated and stats['n_truncated']: without max_steps no item is truncated (bool[N] zeros, an int32
     zero), as in the reference (_api.py:689-693)."""
@@ -510,8 +517,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
         from . import backend as B
         prog, meta, pi, bc, N, _ = prepare(args)
         o = B.run(prog, pi, bc, N, opts)
-        tn = [s.name for s in prog.tallies]
-        res_out = {n: o.tallies[tn.index(n)].reshape(prog.tallies[tn.index(n)].shape) for n in names if n in tn}
+        res_out = _sum_outputs(prog, o, names)
         stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
         if prog.spawn is not None:
             stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
@@ -629,17 +635,21 @@ def _run_tangents(mapped, args, tans, lanes):
     of the float per-item results (None for the others)])."""
     from . import backend as B
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
-    if prog.spawn is not None:
-        raise UnsupportedError("tallymap: forward mode through spawn is not supported by this backend")
     pt, bt, pp, pb = [], [], [], []
     for pos, x in enumerate(axes):
         leaves, _ = flatten(args[pos])
         tl = tans[pos]
         for j, leaf in enumerate(leaves):
             dt = _np_dtype(leaf)
-            on = tl is not None and np.issubdtype(dt, np.floating)
+            isf = np.issubdtype(dt, np.floating)
+            # (a spawning program carries a tangent of every float per-item operand: its children's tangents)
+            on = isf and (tl is not None or (x == 0 and prog.spawn is not None))
             (pp if x == 0 else pb).append(on)
-            if on:
+            if on and tl is None:
+                import torch
+                z = torch.zeros(_shape(leaf), dtype=B.torch_dtype(dt), device="cuda")
+                pt += [z] * lanes
+            elif on:
                 for t in tl:
                     tleaves, _ = flatten(t)
                     (pt if x == 0 else bt).append(tleaves[j])
@@ -647,20 +657,22 @@ def _run_tangents(mapped, args, tans, lanes):
     o = B.run(q, list(pi) + pt, list(bc) + bt, N, mapped._opts)
     names = mapped._names
     nT = prog.nT
-    tn = [s.name for s in prog.tallies]
-    res_out = {n: o.tallies[tn.index(n)].reshape(prog.tallies[tn.index(n)].shape) for n in names if n in tn}
+    res_out = _sum_outputs(prog, o, names)
     ny = len(prog.y_avals())
     ys, trunc = _split_ys(prog, list(o.ys[:ny]))
     stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
+    if prog.spawn is not None:
+        stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
     trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
     _record_outputs(prog, o, res_out, stats)
     primal = Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
     t_tal = [dict() for _ in range(lanes)]
+    at = {slot: i for i, slot in enumerate(q.out_tallies)}     # (the launch returns the "sum" tallies only)
     k = nT
     for slot in q.tangent_tallies:
         for l in range(lanes):
             if prog.tallies[slot].kind == "sum" and prog.tallies[slot].name in names:
-                t_tal[l][prog.tallies[slot].name] = o.tallies[k].reshape(prog.tallies[slot].shape)
+                t_tal[l][prog.tallies[slot].name] = o.tallies[at[k]].reshape(prog.tallies[slot].shape)
             k += 1
     for r, cap, fields in prog.records:        # tangents of the float record fields (canonical, like the primal)
         for l in range(lanes):

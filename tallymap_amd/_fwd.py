@@ -14,6 +14,9 @@ variables, loop carries and tangent tallies, all advanced in the same pass over 
     dropped there too); every float tally has a tangent tally, of the same format (exact, fixed point, plain);
   * while: carries are extended by the tangents of the carries that become active (a fixed point over the body);
     the cond ignores them.  cond: every branch gets the same tangent inputs and returns the union of tangents;
+  * a spawn `t.spawn(child)` stores the child's tangents with it (every float per-item operand of a spawning
+    program has tangent operands, zero for a root whose input is not perturbed), so a child starts from the tangent
+    its parent gave it (reference _primitive.py:469-471, 712-714);
   * comparisons, integer arithmetic, threefry, floor / ceil / round / sign and stop_gradient have no tangent.
 """
 import numpy as np
@@ -97,6 +100,16 @@ def _jvp_eqn(e, ins, tins, lanes):
         return _jvp_while(e, ins, tins, lanes)
     if e.prim == "cond":
         return _jvp_cond(e, ins, tins, lanes)
+    if e.prim == "tallymap_spawn":
+        # the child's operands, then `lanes` tangents of each float one (invar-major, as the program's per-item
+        # tangent operands are ordered)
+        extra = []
+        for v, t in zip(e.invars[2:], tins[2:]):
+            if _isf(v.aval):
+                extra += [_fit(t[l], v.aval) if t is not None else _zero(v.aval) for l in range(lanes)]
+        vs = [x.var if C.is_traced(x) else C.Lit(np.asarray(x), C.AVal(np.shape(x), np.asarray(x).dtype))
+              for x in list(ins) + extra]
+        return C.bind("tallymap_spawn", vs, [e.outvars[0].aval]), [None]
     outs = A._replay(e, ins)
     if e.prim in ("tallymap_emit", "tallymap_put"):
         tt, tv = tins[0], tins[2]
@@ -281,6 +294,8 @@ def jvp_program(prog, pert_pi, pert_bc, lanes=1):
     tf = [k for k, s in enumerate(prog.tallies) if s.kind in ("sum", "discard") and s.dtype in (C.F32, C.F64)]
     pav, bav = prog.p_avals(), prog.b_avals()
     pp = [bool(p) and _isf(a) for p, a in zip(pert_pi, pav)]
+    if prog.spawn is not None and pp != [_isf(a) for a in pav]:
+        raise A.ADError("internal: a spawning program's jvp needs a tangent of every float per-item operand")
     pb = [bool(p) and _isf(a) for p, a in zip(pert_bc, bav)]
     tin = [k in tf for k in range(nT)] + pp + pb
     ny = len(jx.outvars) - nT
@@ -309,7 +324,7 @@ def jvp_program(prog, pert_pi, pert_bc, lanes=1):
             tl.append(dataclasses.replace(s, name=s.name + ("'" if lanes == 1 else f"'{l}")))
     check_tallies(out_jx, len(tl), prog.where)
     q = ItemProgram(out_jx, tuple(tl), nP + npt, nB + len(t_b), prog.trunc, f"{prog.tag}+jvp{lanes}", prog.where,
-                    prog.records, prog.counts)
+                    prog.records, prog.counts, prog.spawn)
     q.tangent_tallies = tf
     q.tangent_ys = yt
     q.lanes = lanes

@@ -181,7 +181,8 @@ def test_spawn_tracing_and_errors():
     """t.spawn: a hidden token tally threaded like an emit, one `tallymap_spawn` per spawn with the child's leaves
     (converted to the mapped inputs' dtypes); the generated kernel claims tickets per wave and bounds them by the
     capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input, Records
-    with spawn and the derivative paths through spawn raise (reference edge.py:183-188)."""
+    with spawn and reverse mode through spawn raise (reference edge.py:183-188); the jvp program's spawn stores
+    the child's tangents with it."""
     from tallymap_amd._tally import QKEY
     from tallymap_amd.backend import kernel as K
 
@@ -210,8 +211,11 @@ def test_spawn_tracing_and_errors():
                 spawn=tm.Queue(8))._prepare((xs,))
     with pytest.raises(tm.UnsupportedError, match="spawn"):
         tm.grad(f)(g0, xs)
-    with pytest.raises(tm.UnsupportedError, match="spawn"):
-        tm.jvp(f, (g0, xs), (None, xs))
+    from tallymap_amd._api import _jvp_prog
+    q = _jvp_prog(p, (False, True), (), 2)       # two tangent lanes: the child stores x' of each lane
+    w = next(e for e in q.jaxpr.eqns if e.prim == "while")
+    sp = [e for e in w.params["body_jaxpr"].eqns if e.prim == "tallymap_spawn"]
+    assert q.spawn == 100 and q.nP == 4 and len(sp) == 1 and len(sp[0].invars) == 2 + 4
     with pytest.raises(TypeError, match="Queue"):
         tm.vmap(item, outputs={"h": tm.Sum((2,))}, spawn=100)
     with pytest.raises(ValueError, match="capacity"):
