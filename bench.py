@@ -161,6 +161,70 @@ def bench_records(steps, warmup):
             "items_per_s": n / (ms * 1e-3)}
 
 
+SHOWER_NZ, SHOWER_DEPTH = 16, 6
+
+
+def _shower_particle(t, p, theta):
+    """a branching shower (the reference's examples/shower_toy.py workload, with a uniform step length): a particle
+    deposits theta[0] of its energy per step along z and, with probability 0.35 per step below generation 6,
+    splits off a child with theta[1] x U(0.5, 1) of what is left."""
+    from tallymap_amd import lax
+    from tallymap_amd import numpy as jnp
+    from tallymap_amd import random as R
+
+    def body(c):
+        s, n, t = c
+        k = R.fold_in(s["key"], n)
+        u = R.uniform(k, (3,))
+        z = s["z"] + u[0] * 0.5
+        dep = s["E"] * theta[0]
+        t = t.add("dep", jnp.clip(jnp.floor(z * 2.0).astype(jnp.int32), 0, SHOWER_NZ - 1), dep)
+        split = (u[1] < 0.35) & (s["g"] < SHOWER_DEPTH)
+        ec = (s["E"] - dep) * theta[1] * (0.5 + 0.5 * u[2])
+        t = t.spawn(dict(E=ec, z=z, key=R.fold_in(k, 1), g=s["g"] + 1), when=split)
+        e = s["E"] - dep - jnp.where(split, ec, 0.0)
+        return dict(E=e, z=z, key=s["key"], g=s["g"]), n + 1, t
+    s, n, t = lax.while_loop(lambda c: (c[0]["E"] > 1e-3) & (c[1] < 40), body, (p, 0, t))
+    return t.add("count", s["g"], 1)
+
+
+def bench_spawn(steps, warmup):
+    """spawn throughput: the shower from 1,048,576 roots (about 67M particles in 7 generations, Queue 2^25): one
+    call is a launch per generation with a device-to-host read of the ticket count between them; timed with HIP
+    events on torch's current stream around the whole call (the host's generation loop included)."""
+    import torch
+
+    import tallymap_amd as tm
+    from tallymap_amd import random as R
+    n = 1 << 20
+    roots = dict(E=torch.linspace(1.0, 2.0, n, dtype=torch.float32, device="cuda"),
+                 z=torch.zeros(n, dtype=torch.float32, device="cuda"),
+                 key=torch.from_numpy(R._host_split(np.array([0, 7], np.uint32), n).view(np.int32)).cuda()
+                 .view(torch.uint32), g=torch.zeros(n, dtype=torch.int32, device="cuda"))
+    theta = torch.tensor([0.2, 0.6], dtype=torch.float32, device="cuda")
+    f = tm.vmap(_shower_particle, outputs={"dep": tm.Sum((SHOWER_NZ,)), "count": tm.Sum((SHOWER_NZ,), np.int32)},
+                in_axes=(0, None), spawn=tm.Queue(1 << 25))
+    for _ in range(warmup):
+        f(roots, theta)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for e in evs:
+        e[0].record(stream)
+        r = f(roots, theta)
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    sp, dr = int(r.stats["spawned"].item()), int(r.stats["children_dropped"].item())
+    count = r.outputs["count"].cpu().numpy()
+    if dr or int(count.sum()) != n + sp:
+        raise RuntimeError(f"spawn bench: {sp} spawned, {dr} dropped, {int(count.sum())} particles counted")
+    gens = int(np.count_nonzero(count))
+    print("bench: spawn done", file=sys.stderr, flush=True)
+    return {"roots": n, "children": sp, "generations": gens, "queue": 1 << 25, "ms": ms,
+            "particles_per_s": (n + sp) / (ms * 1e-3)}
+
+
 def bench_configs(steps, warmup, with_cpu):
     """items/s of configs 1, 3, 4, 5 at their BASELINE sizes, forward and gradient launches timed with HIP events
     on torch's current stream; the oracle on a bounded sample beside each."""
@@ -340,6 +404,7 @@ def main():
         print("bench: atomics done", file=sys.stderr, flush=True)
         out["configs"] = bench_configs(max(3, a.steps // 4), 1, not a.no_cpu)
         out["records"] = bench_records(max(3, a.steps // 4), 1)
+        out["spawn"] = bench_spawn(max(3, a.steps // 4), 1)
     print(json.dumps(out))
 
 

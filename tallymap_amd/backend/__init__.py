@@ -167,7 +167,7 @@ def _run_spawn(c, prog, ins, N):
     """a spawning program, generation by generation (the reference's one-launch ticket ring, backends/kernel/
     kernel.py:1006-1040, made a host loop of ordinary launches: no wave ever waits for another).  Generation 0 runs
     the N items with tm_zero; each launch's children (their per-item operands in the Q-row buffers of the layout,
-    the ticket counter in ctl words 4-5) are the next launch's items, without tm_zero, so the tallies and stats
+    the ticket counter in ctl words 32-33) are the next launch's items, without tm_zero, so the tallies and stats
     accumulate; tickets past Q are dropped children.  The loop ends at the first generation that spawns nothing
     (one device-to-host read of ctl per generation); the host then writes stats spawned / children_dropped /
     children_truncated and tm_post runs once (a dropped or truncated child poisons the float tallies there)."""
@@ -186,7 +186,7 @@ def _run_spawn(c, prog, ins, N):
         w = ctl.cpu().numpy().view(np.uint32)
         if ntr_roots is None:
             ntr_roots = int(w[2])
-        cnt = int(w[4]) | (int(w[5]) << 32)
+        cnt = int(w[32]) | (int(w[33]) << 32)
         if cnt == 0:
             break
         n = min(cnt, Q)
@@ -197,7 +197,7 @@ def _run_spawn(c, prog, ins, N):
             ys_scr = {r: torch.empty((Q,) + tuple(outs[r - base].shape[1:]), dtype=outs[r - base].dtype,
                                      device="cuda") for r in L.r_ys}
         ctl[0:2].zero_()                               # the item claim counter
-        ctl[4:6].zero_()                               # the ticket counter
+        ctl[32:34].zero_()                             # the ticket counter
         gen = list(outs)
         for r, t in zip(L.r_q, spare):
             gen[r - base] = t

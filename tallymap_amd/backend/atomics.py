@@ -9,6 +9,8 @@ patterns) one flush of its block's bins.  The patterns are the ones the generate
   glb_f32_dist    global_atomic_add_f32, every add to its own address (per-item tallies: C4, C5)
   glb_f32_128     global_atomic_add_f32 onto 128 addresses (an unprivatised small tally)
   glb_f32_1       global_atomic_add_f32 onto 1 address (full contention)
+  glb_claim_1     one returning u64 add per wave onto 1 address (tm_claim: the item, Records-batch and spawn-ticket
+                  claims); its rate is claims (wave instructions) per second
 
 The adds are of 1.0 (f32) or 1 (u64), so the totals are checkable: `run` returns adds per second and whether the
 buffer holds exactly the number of adds issued.
@@ -17,7 +19,7 @@ import numpy as np
 
 from . import compile as Cm
 
-PATTERNS = ("lds_f32_128", "lds_u64_128", "glb_f32_dist", "glb_f32_128", "glb_f32_1")
+PATTERNS = ("lds_f32_128", "lds_u64_128", "glb_f32_dist", "glb_f32_128", "glb_f32_1", "glb_claim_1")
 
 
 def source(pattern, per):
@@ -61,6 +63,12 @@ def source(pattern, per):
         body = f"""
   for (u32 k = 0; k < {per}u; ++k) atomicAdd(&((float*)P.p[0])[0], 1.0f);"""
         nw = "128"                                  # the whole buffer (bins 1..127 stay 0)
+    elif pattern == "glb_claim_1":
+        body = f"""
+  u64 acc = 0ull;
+  for (u32 k = 0; k < {per}u; ++k) acc += tm_claim((u64*)P.p[0], 1u);
+  if (acc == ~0ull) ((u64*)P.p[0])[1] = acc;        // (never: keeps the claims' results live)"""
+        nw = "256"
     else:
         raise ValueError(pattern)
     main = ("extern \"C\" __global__ void __launch_bounds__(256) tm_main(const TmParams P, const i64 n_items) {"
@@ -68,7 +76,7 @@ def source(pattern, per):
     return "\n".join(head + [zero % nw, main])
 
 
-PER = {"glb_f32_1": 16}       # one address: f32 counts stay exact below 2^24
+PER = {"glb_f32_1": 16, "glb_claim_1": 256}       # one address: f32 counts stay exact below 2^24
 
 
 def run(pattern, per=None, reps=5):
@@ -87,11 +95,11 @@ def run(pattern, per=None, reps=5):
     Cm.check(Cm.lib().tm_register(kid, img, len(img), f"atomics {pattern}".encode()))
     c = Compiled(kid, None, 256, src, pattern)
     lanes = kernel_info(c)["resident_threads"]
-    adds = lanes * per
+    adds = (lanes // 64 if pattern == "glb_claim_1" else lanes) * per
     n_items = lanes                 # sizes the grid: ceil(lanes / 256) blocks, the persistent grid
     if pattern == "glb_f32_dist":
         buf = torch.empty(adds, dtype=torch.float32, device="cuda")
-    elif pattern == "lds_u64_128":
+    elif pattern in ("lds_u64_128", "glb_claim_1"):
         buf = torch.empty(128, dtype=torch.int64, device="cuda")
     else:
         buf = torch.empty(128, dtype=torch.float32, device="cuda")

@@ -31,6 +31,9 @@ BLOCK = 256
 LDS_BYTES = 32768          # privatised tallies per block (MI355X: 160 KB LDS per CU)
 XW = 5                     # int64 words per exact bin
 CHUNK = 64
+RESERVE = 4                # chunks a wave reserves per claim while far from the end (short items)
+CLAIM_NS = 50              # reserve when a chunk lasted less than this many ns per resident wave (claims from every
+                           # wave at that pace would take a quarter of the counter's ~83M claims/s)
 COMPACT = 16               # iterations between the tail-phase repacks of a workgroup's live items                 # items per wave claim
 BCAST_REG = 16             # broadcast operands up to this many elements are loaded into registers
 
@@ -275,12 +278,21 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         ks = [k for k in outs if prog.tallies[k].name in keys]
         rec_info.append(dict(name=rn, capacity=cap, ctr=j, fields=fl, ki=ks[0], kk=ks[1], count=prog.counts[j],
                              fin=None))
-    r_ctl = result((8,), np.uint32)
+    Q = getattr(prog, "spawn", None)
+    # ctl: the item claim counter (words 0-1), truncations (word 2); a spawning program's ticket counter sits at
+    # words 32-33, on its own 128-byte line (two counters that every wave hits serialise on a shared line)
+    n_ctl = 64 if Q is not None else 8
+    r_ctl = result((n_ctl,), np.uint32)
     r_stats = result((5,), np.int32)
     n_zero = len(res)
     r_ys = [result(a.shape, a.dtype, per_item=True) for a in yav]
-    Q = getattr(prog, "spawn", None)
     r_q = [result((Q,) + tuple(a.shape), a.dtype) for a in pav] if Q is not None else []
+    q_words, q_off = 0, []     # a child's operands as u32 words (the LDS staging layout)
+    for a in pav:
+        q_off.append(q_words)
+        q_words += max(1, a.size) * (2 if a.dtype.itemsize == 8 else 1)
+    # children staged per wave in LDS and flushed with one ticket claim per QS children (0: a claim per spawn point)
+    QS = (128 if q_words <= 16 else 64 if q_words <= 48 else 0) if Q is not None else 0
     r_rex = result((), np.int64, per_item=True) if recs else None       # the Records scans' scratch (per item)
     r_rbs = result((), np.int64, per_item=True) if recs else None
     for ri in rec_info:        # per launched wave: the unused slot range [s0, s1) of its last batch (+ a count)
@@ -383,20 +395,82 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     em.hooks["tallymap_item_index"] = lambda em_, e, ins: Val(["((i32)tm_item)"], (), C.I32)
 
     def spawn_rule(em_, e, ins):
-        """a spawned child: a ticket of the next generation's buffer (tm_qclaim: one counter atomic per wave at this
-        point), its per-item operands stored in that row when the ticket is below the capacity Q (the host counts
-        the tickets past Q as dropped children).  The counter is ctl words 4-5."""
+        """a spawned child.  Staged (QS > 0): the spawning lanes write the child's operands as words into their
+        wave's LDS staging rows (rank order after the wave's count); a wave whose rows would overflow first
+        flushes them (_qflush_lines: one ticket claim for all of them, then rows stored to the next generation's
+        buffer), and each wave flushes what is left when it exits.  Direct (QS = 0): one ticket claim per wave at
+        this point (tm_qclaim) and the row stored at once.  Tickets past the capacity Q are not stored (the host
+        counts them as dropped children)."""
         t, w, leaves = ins[0], ins[1], ins[2:]
         if Q is None or len(leaves) != nP:
             raise RuntimeError("internal: a spawn in a program without a queue of its per-item operands")
-        tq = em_.bind(f"tm_qclaim(tm_ctr + 2, {w.el[0]})", C.I64, "tq")
-        em_.open(f"if ((u64){tq} < {int(Q)}ull)")
+        if not QS:
+            tq = em_.bind(f"tm_qclaim(tm_qctr, {w.el[0]})", C.I64, "tq")
+            em_.open(f"if ((u64){tq} < {int(Q)}ull)")
+            for i, (lv, a) in enumerate(zip(leaves, pav)):
+                ct, n = ctype(a.dtype), max(1, a.size)
+                for el in range(n):
+                    em_.line(f"(({ct}*)P.p[{r_q[i]}])[{tq} * {n} + {el}] = {lv.el[el]};")
+            em_.close()
+            return t
+        wv = em_.bind(w.el[0], C.BOOL, "sw")
+        m, nn, q = em_.fresh("sm"), em_.fresh("sn"), em_.fresh("sq")
+        em_.line(f"const u64 {m} = tm_ballot({wv});")
+        em_.open(f"if ({m} != 0ull)")
+        em_.line(f"const u32 {nn} = (u32)__builtin_popcountll({m});")
+        em_.line(f"u32 {q} = tm_qn[threadIdx.x >> 6];")
+        em_.open(f"if ({q} + {nn} > {QS}u)")
+        for ln in _qflush_lines(q):
+            em_.line(ln)
+        em_.line(f"{q} = 0u;")
+        em_.close()
+        em_.open(f"if ({wv})")
+        d = em_.fresh("sd")
+        em_.line(f"volatile u32* const {d} = tm_qs + ({q} + tm_rank({m})) * {q_words}u;")
         for i, (lv, a) in enumerate(zip(leaves, pav)):
-            ct, n = ctype(a.dtype), max(1, a.size)
-            for el in range(n):
-                em_.line(f"(({ct}*)P.p[{r_q[i]}])[{tq} * {n} + {el}] = {lv.el[el]};")
+            for el in range(max(1, a.size)):
+                o = q_off[i] + el * (2 if a.dtype.itemsize == 8 else 1)
+                v = lv.el[el]
+                if a.dtype.itemsize == 8:
+                    b = em_.bind(f"__builtin_bit_cast(u64, ({ctype(a.dtype)})({v}))", C.U64, "sb")
+                    em_.line(f"{d}[{o}] = (u32){b}; {d}[{o + 1}] = (u32)({b} >> 32);")
+                elif a.dtype.itemsize == 4:
+                    em_.line(f"{d}[{o}] = __builtin_bit_cast(u32, ({ctype(a.dtype)})({v}));")
+                else:
+                    em_.line(f"{d}[{o}] = (u32)({v});")
+        em_.close()
+        em_.line("__builtin_amdgcn_wave_barrier();")
+        em_.line(f"if (tm_lane() == (int)__builtin_ctzll(tm_ballot(true))) tm_qn[threadIdx.x >> 6] = {q} + {nn};")
         em_.close()
         return t
+
+    def _qflush_lines(cnt):
+        """store the wave's `cnt` staged children to the next generation's buffer with the lanes that are active:
+        one ticket claim for all of them, the rows spread over the lanes."""
+        rd = []
+        for i, a in enumerate(pav):
+            ct, n = ctype(a.dtype), max(1, a.size)
+            for el in range(n):
+                o = q_off[i] + el * (2 if a.dtype.itemsize == 8 else 1)
+                if a.dtype.itemsize == 8:
+                    v = f"__builtin_bit_cast({ct}, (u64)tm_fs[{o}] | ((u64)tm_fs[{o + 1}] << 32))"
+                elif a.dtype.itemsize == 4:
+                    v = f"__builtin_bit_cast({ct}, tm_fs[{o}])"
+                elif a.dtype == C.BOOL:
+                    v = f"(tm_fs[{o}] != 0u)"
+                else:
+                    v = f"({ct})tm_fs[{o}]"
+                rd.append(f"      (({ct}*)P.p[{r_q[i]}])[tm_ft * {n} + {el}] = {v};")
+        return ([ "{",
+                 f"  const u64 tm_fb = tm_claim(tm_qctr, {cnt});",
+                  "  const u64 tm_fa = tm_ballot(true);",
+                  "  const u32 tm_fna = (u32)__builtin_popcountll(tm_fa);",
+                  "  __builtin_amdgcn_wave_barrier();",
+                 f"  for (u32 tm_fe = tm_rank(tm_fa); tm_fe < {cnt}; tm_fe += tm_fna) {{",
+                  "    const u64 tm_ft = tm_fb + tm_fe;",
+                 f"    if (tm_ft < {int(Q)}ull) {{",
+                 f"      const volatile u32* const tm_fs = tm_qs + tm_fe * {q_words}u;"]
+                + rd + ["    }", "  }", "  __builtin_amdgcn_wave_barrier();", "}"])
     em.hooks["tallymap_spawn"] = spawn_rule
 
     # --------------------------------------------------------------------------------- the item's code
@@ -558,7 +632,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             zero_words.append((r_scr[k], scratch_words(s)))
     if recs:
         zero_words.append((r_rctr, 4 * len(recs)))
-    zero_words += [(r_ctl, 8), (r_stats, 5)]
+    zero_words += [(r_ctl, n_ctl), (r_stats, 5)]
     zl = []
     for b, nw in zero_words:
         zl.append(f"  for (i64 i = g; i < {nw}; i += s) ((u32*)P.p[{b}])[i] = 0u;")
@@ -624,6 +698,14 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         body.append(f"  if ((threadIdx.x & 63u) == 0u) {{ tm_rbase{j}[threadIdx.x >> 6] = 0ull; "
                     f"tm_rcnt{j}[threadIdx.x >> 6] = 0ull; tm_rleft{j}[threadIdx.x >> 6] = 0u; }}")
         body.append(f"  const u64 tm_rawcap{j} = {ri['capacity']}ull + (u64)gridDim.x * {w}ull * (TM_RB - 1ull);")
+    if Q is not None:          # the spawn ticket counter; each wave's staging rows and their count
+        body.append("  u64* const tm_qctr = tm_ctr + 16;")
+        if QS:
+            body.append(f"  __shared__ u32 tm_qst[{(block // 64) * QS * q_words}];")
+            body.append(f"  __shared__ u32 tm_qnv[{block // 64}];")
+            body.append("  volatile u32* const tm_qn = tm_qnv;")
+            body.append(f"  volatile u32* const tm_qs = tm_qst + (threadIdx.x >> 6) * {QS * q_words}u;")
+            body.append("  if ((threadIdx.x & 63u) == 0u) tm_qn[threadIdx.x >> 6] = 0u;")
     for k in priv:
         s = prog.tallies[k]
         if s.exact:
@@ -667,6 +749,9 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append("  i64 tm_item = 0;")
     body.append("  u32 tm_loc = 0;")
     body.append("  u64 tm_cb = 0, tm_cur = 0, tm_end = 0;     // the wave's chunk: base, next unassigned, end")
+    body.append("  u64 tm_rv = 0, tm_re = 0;                  // the wave's reservation of chunks: next, end")
+    body.append("  u64 tm_t0 = 0;                             // the real-time counter at the wave's last claim")
+    body.append("  u32 tm_rc = 1u;                            // chunks in the wave's last reservation")
     body.append("  i32 tm_drop = 0;")
     body.append("  u32 tm_ntr = 0;")
     body += decls
@@ -686,13 +771,30 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                     "tm_ballot(tm_live) == 0ull)) {")
     else:
         body.append("      if (tm_need != 0ull) {")
+    # one counter that every wave hits serves ~83M claims/s on MI355X, which short items at 64 per claim reach.  A
+    # wave that used up its last reservation in less than CLAIM_NS ns per resident wave per chunk (the pace at
+    # which the waves together would take a quarter of the counter's rate) reserves RESERVE chunks per claim while
+    # more than that many items per resident wave remain past its last claim; long items, and every wave's first
+    # claim, take single chunks, so their tail balances as before.  The pace is read from the 100 MHz real-time
+    # counter at claims only.
+    resv = chunk * RESERVE
     body.append("        if (tm_cur >= tm_end) {")
-    body.append(f"          const u64 tm_b = tm_claim(tm_ctr, {chunk}u);")
+    body.append("          if (tm_rv >= tm_re) {")
+    body.append("            const u64 tm_now = __builtin_amdgcn_s_memrealtime();")
+    body.append(f"            const u64 tm_wv = (u64)gridDim.x * {wpb}u;")
+    body.append(f"            const bool tm_big = tm_t0 != 0ull && (tm_now - tm_t0) * 10ull < tm_wv * tm_rc * {CLAIM_NS}ull "
+                f"&& (u64)n_items > tm_re + tm_wv * {resv}ull;")
+    body.append(f"            tm_rc = tm_big ? {RESERVE}u : 1u;")
+    body.append("            tm_t0 = tm_now;")
+    body.append(f"            tm_rv = tm_claim(tm_ctr, tm_rc * {chunk}u);")
+    body.append(f"            tm_re = tm_rv + tm_rc * {chunk}u < (u64)n_items ? tm_rv + tm_rc * {chunk}u : (u64)n_items;")
+    body.append("          }")
+    body.append("          const u64 tm_b = tm_rv;")
     body.append("          if (tm_b >= (u64)n_items) {")
     body.append("            tm_more = false;")
     body.append("          } else {")
-    body.append(f"            tm_cb = tm_b; tm_cur = tm_b; tm_end = tm_b + {chunk}u < (u64)n_items ? tm_b + {chunk}u "
-                ": (u64)n_items;")
+    body.append(f"            tm_cb = tm_b; tm_cur = tm_b; tm_end = tm_b + {chunk}u < tm_re ? tm_b + {chunk}u : tm_re;")
+    body.append("            tm_rv = tm_end;")
     if W:
         body.append(f"            for (u32 q = (u32)tm_lane(); q < {chunk}u; q += 64u) {{")
         body.append("              const u64 t = tm_cb + q;")
@@ -781,6 +883,13 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         body.append("      --tm_it;")
         body.append("    }")
     body.append("  }")
+    if QS:                     # the wave's staged children that are left
+        body.append("  {")
+        body.append("    const u32 tm_sq = tm_qn[threadIdx.x >> 6];")
+        body.append("    if (tm_sq != 0u) {")
+        body += ["      " + ln for ln in _qflush_lines("tm_sq")]
+        body.append("    }")
+        body.append("  }")
     body.append("  if (tm_drop) atomicAdd(&TM_STATS[4], tm_drop);")
     for ri in rec_info:        # each wave: its records into the exact count, its last batch's unused slots listed
         j, w, fin = ri["ctr"], block // 64, f"((u64*)P.p[{ri['fin']}])"

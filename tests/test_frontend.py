@@ -179,8 +179,8 @@ def test_records_tracing_and_errors():
 
 def test_spawn_tracing_and_errors():
     """t.spawn: a hidden token tally threaded like an emit, one `tallymap_spawn` per spawn with the child's leaves
-    (converted to the mapped inputs' dtypes); the generated kernel claims tickets per wave and bounds them by the
-    capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input, Records
+    (converted to the mapped inputs' dtypes); the generated kernel stages children per wave, claims their tickets
+    per flush and bounds them by the capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input, Records
     with spawn and reverse mode through spawn raise (reference edge.py:183-188); the jvp program's spawn stores
     the child's tangents with it."""
     from tallymap_amd._tally import QKEY
@@ -198,7 +198,9 @@ def test_spawn_tracing_and_errors():
     sp = [e for e in w.params["body_jaxpr"].eqns if e.prim == "tallymap_spawn"]
     assert len(sp) == 1 and [v.aval.dtype for v in sp[0].invars[2:]] == [np.int32, np.float32]
     src, L = K.build(p)
-    assert "tm_qclaim(tm_ctr + 2," in src and "< 100ull" in src and len(L.r_q) == 2
+    # children staged per wave in LDS, one ticket claim per flush, rows past the capacity not stored
+    assert "tm_claim(tm_qctr, " in src and "tm_ft < 100ull" in src and "tm_qclaim" not in src.split("tm_main")[1]
+    assert len(L.r_q) == 2
     assert "TM_STATS[1] != 0" in src                 # a dropped child poisons the float outputs
     with pytest.raises(ValueError, match="Queue"):
         tm.vmap(lambda t, x: t.spawn(x), outputs={"h": tm.Sum((1,))})._prepare((xs,))
