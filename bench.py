@@ -301,7 +301,15 @@ def main():
     ap.add_argument("--traffic-bytes", type=float, default=None,
                     help="HBM bytes per dominant-kernel launch (default: the rocprofv3 measurement of this kernel at "
                          "the default N, null at other N)")
+    ap.add_argument("--section", choices=("configs", "records", "spawn"), default=None,
+                    help="run only this section and print its JSON object (for profiling one workload)")
     a = ap.parse_args()
+    if a.section:
+        steps = max(3, a.steps // 4)
+        run = {"configs": lambda: bench_configs(steps, 1, not a.no_cpu), "records": lambda: bench_records(steps, 1),
+               "spawn": lambda: bench_spawn(steps, 1)}[a.section]
+        print(json.dumps({a.section: run()}))
+        return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {a.gpus}): items shard contiguously over "
               "GPUs with one all-reduce of the tallies, which is designed but not built", file=sys.stderr)
