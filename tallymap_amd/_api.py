@@ -137,6 +137,9 @@ class ItemProgram:
     records: tuple = ()        # ((name, capacity, ((field, dtype), ...)), ...): the Records outputs
     counts: tuple = ()         # per Records output: the index among the per-item results of its per-item count
     spawn: int = None          # the spawn Queue's capacity (None: the item cannot spawn)
+    spawn_mode: str = None     # the tree adjoint's programs: 'record' (children also store parent and ordinal) or
+                               # 'adjoint' (spawns emit into the child-slot tally; per-item operand `off` last)
+    qcount: int = None         # 'record': the index among the per-item results of the item's spawn count
 
     @property
     def nT(self):
@@ -160,7 +163,7 @@ class ItemProgram:
         if d is None:
             d = self.__dict__["_digest"] = digest(self.jaxpr, self.tallies, (self.nP, self.nB, self.trunc, self.tag,
                                                                             repr(self.records), self.counts,
-                                                                            self.spawn))
+                                                                            self.spawn, self.spawn_mode, self.qcount))
         return d
 
 
@@ -302,10 +305,12 @@ def item_name(fn):
     return f"{q} ({code.co_filename}:{code.co_firstlineno})" if code else q
 
 
-def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None, spawn=None, ctree=None):
+def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None, spawn=None, ctree=None,
+                  spawn_mode=None):
     """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves);
-    spawn: the Queue capacity (ctree: the structure a spawned child must have)."""
-    from ._tally import KI, KK, QKEY, RSEP, rkey
+    spawn: the Queue capacity (ctree: the structure a spawned child must have); spawn_mode: None, or one of the
+    tree adjoint's programs, 'record' / 'adjoint' (Tally.spawn)."""
+    from ._tally import KI, KK, QF, QKEY, RSEP, rkey
     tspecs = []
     recs = []
     for n in sorted(outs_spec):
@@ -340,6 +345,12 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         if recs:
             raise UnsupportedError("tallymap: Records outputs together with spawn are not supported by this backend")
         tspecs.append(TSpec(QKEY, (1,), C.I32, kind="discard"))    # the spawn token (orders t.spawn like an emit)
+        nf = sum(a.size for a in pav if a.dtype in (C.F32, C.F64))
+        if spawn_mode == "adjoint" and nf:
+            if int(spawn) * nf > MAX_ITEMS:
+                raise UnsupportedError("tallymap: reverse mode through spawn needs Queue capacity x the float "
+                                       "elements of a child below 2^31")
+            tspecs.append(TSpec(QF, (int(spawn) * nf,), C.F32))     # the child slots of the tree adjoint
     names = [s.name for s in tspecs]
     where = item_name(fn)
     tav = [C.AVal((s.S,), s.dtype) for s in tspecs]
@@ -353,12 +364,17 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     try:
         tin = [C.Tracer(b.new_invar(a)) for a in tav]
         pin = [C.Tracer(b.new_invar(a)) for a in pav]
+        off = C.Tracer(b.new_invar(C.AVal((), C.I32))) if spawn_mode == "adjoint" else None
         bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
         rec0 = {}
         if recs:
             cid = C.bind("tallymap_item_index", [], [C.AVal((), C.I32)])[0]
             rec0 = {r: (0, cid) for r, _, _ in recs}
-        rinfo = tuple(recs) + (((QKEY, ctree, tuple(pav)),) if spawn is not None else ())
+        if spawn_mode == "record":
+            rec0[QKEY] = (0, C.bind("tallymap_item_index", [], [C.AVal((), C.I32)])[0])
+        elif spawn_mode == "adjoint":
+            rec0[QKEY] = (0, off)
+        rinfo = tuple(recs) + (((QKEY, ctree, tuple(pav), spawn_mode),) if spawn is not None else ())
         t = Tally({n: x for n, x in zip(names, tin)}, shapes, rec0, rinfo or None)
         m = unflatten(ptree, pin) if ptree is not None else pin
         bb = unflatten(btree, bin_) if btree is not None else bin_
@@ -388,6 +404,15 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
                 k = C.convert(k, C.I32)
             counts.append(len(outs) - len(names))
             outs.append(b.local(k.var))
+        qcount = None
+        if spawn_mode == "record":        # the item's spawn count (hidden per-item result: its children)
+            k = t2._r[QKEY][0]
+            if not C.is_traced(k):
+                k = C.Tracer(C.bind("copy", [C.Lit(int(k), C.AVal((), C.I32))], [C.AVal((), C.I32)])[0].var)
+            elif k.dtype != C.I32:
+                k = C.convert(k, C.I32)
+            qcount = len(outs) - len(names)
+            outs.append(b.local(k.var))
         trunc = None
         if capctx is not None:
             tr = capctx.trunc
@@ -403,8 +428,9 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     if b.captured:
         raise C.TraceError("tallymap: the item function closes over a traced value of another call")
     check_tallies(jx, len(tspecs), where)
-    prog = ItemProgram(jx, tuple(tspecs), len(pav), len(bav), trunc, "primal", where, tuple(recs), tuple(counts),
-                       int(spawn) if spawn is not None else None)
+    prog = ItemProgram(jx, tuple(tspecs), len(pav) + (spawn_mode == "adjoint"), len(bav), trunc,
+                       "primal" if spawn_mode is None else f"spawn_{spawn_mode}", where, tuple(recs), tuple(counts),
+                       int(spawn) if spawn is not None and spawn_mode != "adjoint" else None, spawn_mode, qcount)
     return prog, meta
 
 
@@ -412,6 +438,7 @@ def _split_ys(prog, ys):
     """the backend's per-item results -> (the item's own results, the truncation flag or None): the hidden
     per-item record counts are removed."""
     hidden = set(prog.counts) | ({prog.trunc} if prog.trunc is not None else set())
+    hidden |= {prog.qcount} if getattr(prog, "qcount", None) is not None else set()
     own = [y for j, y in enumerate(ys) if j not in hidden]
     return own, (ys[prog.trunc] if prog.trunc is not None else None)
 
@@ -480,7 +507,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
     outs_spec = {k: (v if isinstance(v, (Sum, Records)) else Sum(v)) for k, v in outputs.items()}
     names = sorted(outs_spec)
 
-    def prepare(args):
+    def prepare(args, spawn_mode=None):
         axes = in_axes if isinstance(in_axes, (tuple, list)) else (in_axes,) * len(args)
         if len(axes) != len(args) or any(a not in (0, None) for a in axes):
             raise ValueError("tallymap: in_axes must be 0/None or a tuple of 0/None per positional argument")
@@ -499,7 +526,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
         pav = [C.AVal(_shape(x)[1:], _np_dtype(x)) for x in pi]
         bav = [C.AVal(_shape(x), _np_dtype(x)) for x in bc]
         key = (tuple(pav), tuple(bav), tuple(axes), str(ptree), str(btree), max_steps,
-               tuple(sorted((n, repr(v)) for n, v in outs_spec.items())), spawn)
+               tuple(sorted((n, repr(v)) for n, v in outs_spec.items())), spawn, spawn_mode)
         hit = _PROGS.get((id(fn), key))
         if hit is not None and hit[0] is fn:
             _PROGS.move_to_end((id(fn), key))
@@ -507,7 +534,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
         else:
             ctree = flatten(margs[0] if len(margs) == 1 else margs)[1] if spawn is not None else None
             prog, meta = build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree, btree,
-                                       spawn.capacity if spawn is not None else None, ctree)
+                                       spawn.capacity if spawn is not None else None, ctree, spawn_mode)
             _PROGS[(id(fn), key)] = (fn, prog, meta)
             while len(_PROGS) > PROG_CACHE:
                 _PROGS.popitem(last=False)
@@ -570,8 +597,7 @@ def _pullback(mapped, args, argnums):
     from . import backend as B
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     if prog.spawn is not None:
-        raise UnsupportedError("tallymap: reverse mode through spawn (the tree adjoint) is not supported by this "
-                               "backend")
+        return _tree_pullback(mapped, args, argnums)
     an = _argnums(argnums, len(args))
     wrt = _float_args(prog, axes, an)
 
@@ -596,6 +622,76 @@ def _pullback(mapped, args, argnums):
                     out.append(next(gp) if p in wrt[0] else None)
                 else:
                     g = next(gb) if b in wrt[1] else None
+                    out.append(g.reshape(np.shape(args[pos])) if g is not None else None)
+            p += x == 0
+            b += x is None
+        return tuple(out) if len(out) != 1 else out[0]
+    return pullback
+
+
+def _tree_pullback(mapped, args, argnums):
+    """reverse mode through spawn: the tree adjoint (reference _reverse_spawn.py).  The recording forward runs the
+    generations with each child's parent and ordinal and keeps them in canonical order (item i's children at
+    off[i] + ordinal).  The adjoint program is the item with every spawn an EMIT of the child's float operands into
+    a child-slot tally at (off + ordinal) x floats + element, so the cotangent of a child's initial state reaches
+    its parent as the cotangent of that emitted value, at the spawn step, inside the ordinary replay adjoint.  One
+    adjoint launch per generation, deepest first: generation g's child-slot cotangents are generation g + 1's
+    per-item operand cotangents; broadcast cotangents are summed over the generations, the roots' per-item operand
+    cotangents are the per-item arguments'.  A dropped child (incomplete tree) makes every cotangent NaN."""
+    import torch
+
+    from . import backend as B
+    from ._tally import QF
+    rprog, meta, pi, bc, N, axes = mapped._prepare(args, "record")
+    aprog = mapped._prepare(args, "adjoint")[0]
+    an = _argnums(argnums, len(args))
+    want = _float_args(rprog, axes, an)
+    pav = rprog.p_avals()
+    fpi = tuple(j for j, a in enumerate(pav) if a.dtype in (C.F32, C.F64))
+    if any(pav[j].dtype == C.F64 for j in fpi):
+        raise UnsupportedError("tallymap: reverse mode through spawn with float64 per-item operands")
+    wrt = (fpi, want[1])
+    o = B.run(rprog, pi, bc, N, mapped._opts)
+    gens = o.generations
+    Q = int(rprog.spawn)
+    nf = sum(max(1, pav[j].size) for j in fpi)
+    an_slots = {s.name: k for k, s in enumerate(aprog.tallies)}
+    qf = an_slots.get(QF)
+
+    def pullback(ct_outputs=None, ct_per_item=None):
+        cts = {an_slots[n]: v for n, v in (ct_outputs or {}).items() if n in an_slots}
+        cys = {}
+        if ct_per_item is not None:
+            yl, _ = flatten(ct_per_item)
+            cys = {j: x for j, x in enumerate(yl) if x is not None}
+        nan = gens is None
+        runs = gens if gens is not None else [(list(pi), torch.zeros((N,), dtype=torch.int32, device="cuda"), N)]
+        ct_next, g_bc, g_root = None, None, None
+        for g in reversed(range(len(runs))):
+            ops, off, n = runs[g]
+            ct = dict(cts)
+            if qf is not None:
+                ct[qf] = ct_next if ct_next is not None else 0.0
+            gp, gb, _ = B.run_vjp(aprog, wrt, list(ops) + [off], bc, n, ct, cys if g == 0 else {}, mapped._opts)
+            g_bc = gb if g_bc is None else [a + b for a, b in zip(g_bc, gb)]
+            if g == 0:
+                g_root = gp
+            elif nf:
+                flat = torch.cat([x.reshape(n, -1).float() for x in gp], 1).reshape(-1)
+                ct_next = torch.zeros((Q * nf,), dtype=torch.float32, device="cuda")
+                ct_next[:n * nf] = flat
+        if nan:
+            g_root = [torch.full_like(x, float("nan")) for x in g_root]
+            g_bc = [torch.full_like(x, float("nan")) for x in g_bc]
+        out = []
+        gp, gb = dict(zip(fpi, g_root)), iter(g_bc)
+        p = b = 0
+        for pos, x in enumerate(axes):
+            if pos in an:
+                if x == 0:
+                    out.append(gp.get(p) if p in want[0] else None)
+                else:
+                    g = next(gb) if b in want[1] else None
                     out.append(g.reshape(np.shape(args[pos])) if g is not None else None)
             p += x == 0
             b += x is None

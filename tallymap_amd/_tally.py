@@ -17,6 +17,7 @@ from . import _core as C
 RSEP = "\x1f"
 KI, KK = RSEP + "i", RSEP + "k"
 QKEY = RSEP + "q"          # the spawn token: a hidden discard tally that orders t.spawn like an emit
+QF = RSEP + "qf"           # the tree adjoint's child-slot tally: a child's float operands, emitted at its slot
 
 
 def rkey(name, field):
@@ -54,7 +55,7 @@ class Tally:
     def _spawn_info(self):
         for r in (self._ri or ()):
             if r[0] == QKEY:
-                return r[1], r[2]          # (child treedef, child leaf avals)
+                return r[1], r[2], r[3]    # (child treedef, child leaf avals, mode: None | 'record' | 'adjoint')
         return None
 
     def add(self, name, index, value):
@@ -176,7 +177,7 @@ class Tally:
         info = self._spawn_info()
         if info is None:
             raise ValueError("tallymap: spawn needs tallymap_amd.vmap(..., spawn=tallymap_amd.Queue(capacity))")
-        tree, avals = info
+        tree, avals, mode = info
         from ._tree import flatten
         leaves, td = flatten(child)
         if td != tree or len(leaves) != len(avals):
@@ -206,8 +207,43 @@ class Tally:
             return self
         wv = w.var if C.is_traced(w) else C.literal(True, C.BOOL, weak=False)
         tok = self._a[QKEY]
-        new = C.bind("tallymap_spawn", [tok.var, wv] + vs, [tok.aval])[0]
-        return self._with(QKEY, new)
+        if mode is None:
+            new = C.bind("tallymap_spawn", [tok.var, wv] + vs, [tok.aval])[0]
+            return self._with(QKEY, new)
+        # the tree adjoint's two programs carry the item's spawn count k (its children's ordinals)
+        k, ref = self._r[QKEY]
+        wi = C.convert(w, C.I32) if C.is_traced(w) else 1
+        if mode == "record":
+            # the recording forward: the child also stores its parent (the item index) and its ordinal k
+            kv = k.var if C.is_traced(k) else C.literal(int(k), C.I32, weak=False)
+            new = C.bind("tallymap_spawn", [tok.var, wv] + vs + [ref.var, kv], [tok.aval])[0]
+            a = dict(self._a)
+            a[QKEY] = new
+            return Tally(a, self._shapes, {**self._r, QKEY: (k + wi, ref)}, self._ri)
+        # the adjoint program: the child's float operands are EMITTED into the child-slot tally at its slot
+        # (ref = the item's first child slot, an operand), so the replay adjoint hands each one the cotangent of
+        # the child's initial state at the spawn step (reference _reverse_spawn.py:1-10)
+        a = dict(self._a)
+        nf = sum(int(np.prod(av.shape, dtype=np.int64)) for av in avals if np.issubdtype(av.dtype, np.floating))
+        if nf:
+            from . import numpy as jnp
+            base = (ref + k) * nf
+            e = 0
+            t = a[QF]
+            for x, av in zip(leaves, avals):
+                if not np.issubdtype(av.dtype, np.floating):
+                    continue
+                n = int(np.prod(av.shape, dtype=np.int64))
+                for j in range(n):
+                    if C.is_traced(x):
+                        xe = x if x.dtype == av.dtype else C.convert(x, av.dtype)
+                        for i in np.unravel_index(j, av.shape) if av.shape else ():
+                            xe = xe[int(i)]
+                        idx = jnp.where(w, base + e, -1) if C.is_traced(w) else base + e
+                        t = C.Tracer(C.bind("tallymap_emit", [t.var, idx.var, xe.var], [t.aval])[0].var)
+                    e += 1
+            a[QF] = t
+        return Tally(a, self._shapes, {**self._r, QKEY: (k + wi, ref)}, self._ri)
 
 
 def _check_int(i):

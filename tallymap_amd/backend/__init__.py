@@ -170,11 +170,18 @@ def _run_spawn(c, prog, ins, N):
     the ticket counter in ctl words 32-33) are the next launch's items, without tm_zero, so the tallies and stats
     accumulate; tickets past Q are dropped children.  The loop ends at the first generation that spawns nothing
     (one device-to-host read of ctl per generation); the host then writes stats spawned / children_dropped /
-    children_truncated and tm_post runs once (a dropped or truncated child poisons the float tallies there)."""
+    children_truncated and tm_post runs once (a dropped or truncated child poisons the float tallies there).
+
+    The tree adjoint's recording forward (prog.spawn_mode 'record': children also store their parent and ordinal)
+    puts every generation in canonical order -- the children of item i at off[i] .. off[i] + count[i] - 1, off the
+    exclusive prefix sum of the items' spawn counts -- and keeps it: Outputs.generations = [(per-item operands,
+    off int32[n], n)] from the roots down, or None when a child was dropped (the tree is incomplete)."""
     import torch
     L = c.layout
     base = L.n_in
     Q = int(prog.spawn)
+    nP = prog.nP
+    rec = getattr(prog, "spawn_mode", None) == "record"
     outs = _alloc(c, N)
     ctl = outs[L.r_ctl - base].view(torch.int32)
     cur = [outs[r - base] for r in L.r_q]          # the buffers the last launch's children were written to
@@ -182,20 +189,37 @@ def _run_spawn(c, prog, ins, N):
     _queue(c, ins, outs, N, L.n_zero, 0)
     spawned = dropped = 0
     ntr_roots = None
+    gens, ops, n_cur = [], list(ins[:nP]), N      # (the operands and size of the generation just launched)
     while True:
         w = ctl.cpu().numpy().view(np.uint32)
         if ntr_roots is None:
             ntr_roots = int(w[2])
         cnt = int(w[32]) | (int(w[33]) << 32)
+        if rec and gens is not None:
+            counts = (outs[L.r_ys[prog.qcount] - base] if not gens else ys_scr[L.r_ys[prog.qcount]])[:n_cur].long()
+            off = torch.cumsum(counts, 0) - counts
+            gens.append((ops, off.to(torch.int32), n_cur))
         if cnt == 0:
             break
         n = min(cnt, Q)
         spawned += n
         dropped += cnt - n
+        if cnt > Q:
+            gens = None                                # a dropped child: no complete tree to differentiate
         if spare is None:
             spare = [torch.empty_like(t) for t in cur]
             ys_scr = {r: torch.empty((Q,) + tuple(outs[r - base].shape[1:]), dtype=outs[r - base].dtype,
                                      device="cuda") for r in L.r_ys}
+        if rec and gens is not None:                   # the children in canonical (parent, ordinal) order
+            dest = off[cur[nP][:n].long()] + cur[nP + 1][:n].long()
+            ops = []
+            for t in cur[:nP]:
+                z = torch.empty((n,) + tuple(t.shape[1:]), dtype=t.dtype, device="cuda")
+                sv = {torch.uint32: torch.int32, torch.uint64: torch.int64}.get(t.dtype)   # (no index_put for
+                (z.view(sv) if sv else z)[dest] = (t.view(sv) if sv else t)[:n]          # unsigned words)
+                ops.append(z)
+        else:
+            ops = cur[:nP]
         ctl[0:2].zero_()                               # the item claim counter
         ctl[32:34].zero_()                             # the ticket counter
         gen = list(outs)
@@ -203,7 +227,8 @@ def _run_spawn(c, prog, ins, N):
             gen[r - base] = t
         for r, t in ys_scr.items():                    # (a child's own per-item result is discarded)
             gen[r - base] = t
-        _queue(c, cur + list(ins[prog.nP:]), gen, n, 0, 0)
+        _queue(c, list(ops) + list(ins[nP:]), gen, n, 0, 0)
+        n_cur = n
         cur, spare = spare, cur
     big = 2 ** 31 - 1
     ctr = int(w[2]) - ntr_roots
@@ -212,7 +237,9 @@ def _run_spawn(c, prog, ins, N):
     tallies = [outs[L.r_out[k] - base] for k in prog.out_tallies]
     ys = [outs[r - base] for r in L.r_ys]
     ntr = torch.tensor(ntr_roots, dtype=torch.int32, device="cuda") if prog.trunc is not None else None
-    return Outputs(tallies, outs[L.r_stats - base], ys, ntr, {}, [])
+    o = Outputs(tallies, outs[L.r_stats - base], ys, ntr, {}, [])
+    o.generations = gens if rec else None
+    return o
 
 
 _LANES = {}

@@ -286,9 +286,12 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     r_stats = result((5,), np.int32)
     n_zero = len(res)
     r_ys = [result(a.shape, a.dtype, per_item=True) for a in yav]
-    r_q = [result((Q,) + tuple(a.shape), a.dtype) for a in pav] if Q is not None else []
+    # the queue's columns: the child's per-item operands, then (recording forward of the tree adjoint) its parent
+    # (the item index) and its ordinal among the parent's children
+    qav = list(pav) + ([C.AVal((), C.I32)] * 2 if getattr(prog, "spawn_mode", None) == "record" else [])
+    r_q = [result((Q,) + tuple(a.shape), a.dtype) for a in qav] if Q is not None else []
     q_words, q_off = 0, []     # a child's operands as u32 words (the LDS staging layout)
-    for a in pav:
+    for a in qav:
         q_off.append(q_words)
         q_words += max(1, a.size) * (2 if a.dtype.itemsize == 8 else 1)
     # children staged per wave in LDS and flushed with one ticket claim per QS children (0: a claim per spawn point)
@@ -402,12 +405,12 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         this point (tm_qclaim) and the row stored at once.  Tickets past the capacity Q are not stored (the host
         counts them as dropped children)."""
         t, w, leaves = ins[0], ins[1], ins[2:]
-        if Q is None or len(leaves) != nP:
+        if Q is None or len(leaves) != len(qav):
             raise RuntimeError("internal: a spawn in a program without a queue of its per-item operands")
         if not QS:
             tq = em_.bind(f"tm_qclaim(tm_qctr, {w.el[0]})", C.I64, "tq")
             em_.open(f"if ((u64){tq} < {int(Q)}ull)")
-            for i, (lv, a) in enumerate(zip(leaves, pav)):
+            for i, (lv, a) in enumerate(zip(leaves, qav)):
                 ct, n = ctype(a.dtype), max(1, a.size)
                 for el in range(n):
                     em_.line(f"(({ct}*)P.p[{r_q[i]}])[{tq} * {n} + {el}] = {lv.el[el]};")
@@ -427,7 +430,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         em_.open(f"if ({wv})")
         d = em_.fresh("sd")
         em_.line(f"volatile u32* const {d} = tm_qs + ({q} + tm_rank({m})) * {q_words}u;")
-        for i, (lv, a) in enumerate(zip(leaves, pav)):
+        for i, (lv, a) in enumerate(zip(leaves, qav)):
             for el in range(max(1, a.size)):
                 o = q_off[i] + el * (2 if a.dtype.itemsize == 8 else 1)
                 v = lv.el[el]
@@ -448,7 +451,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         """store the wave's `cnt` staged children to the next generation's buffer with the lanes that are active:
         one ticket claim for all of them, the rows spread over the lanes."""
         rd = []
-        for i, a in enumerate(pav):
+        for i, a in enumerate(qav):
             ct, n = ctype(a.dtype), max(1, a.size)
             for el in range(n):
                 o = q_off[i] + el * (2 if a.dtype.itemsize == 8 else 1)

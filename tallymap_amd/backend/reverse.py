@@ -91,11 +91,19 @@ def split(prog):
     jx = prog.jaxpr
     nT = prog.nT
     ws = [i for i, e in enumerate(jx.eqns) if e.prim == "while"]
-    if len(ws) != 1:
-        raise ReverseError(f"reverse mode needs exactly one top-level while loop in the item (found {len(ws)})")
-    w = ws[0]
-    we = jx.eqns[w]
-    pre_e, post_e = jx.eqns[:w], jx.eqns[w + 1:]
+    if len(ws) > 1:
+        raise ReverseError(f"reverse mode needs at most one top-level while loop in the item (found {len(ws)})")
+    if ws:
+        w = ws[0]
+        we = jx.eqns[w]
+        pre_e, post_e = jx.eqns[:w], jx.eqns[w + 1:]
+    else:
+        # an item without a loop: all of it is PRE, followed by a loop that never runs (its carries are the tallies
+        # riding through), so the adjoint is the forward-only one
+        we = C.Eqn("while", [], [], {"cond_nconsts": 0, "body_nconsts": 0,
+                                     "cond_jaxpr": C.Jaxpr([], [C.Lit(False, C.AVal((), C.BOOL))], []),
+                                     "body_jaxpr": C.Jaxpr([], [], [])})
+        pre_e, post_e = list(jx.eqns), []
     nc, nb = we.params["cond_nconsts"], we.params["body_nconsts"]
     cc, bc, init = we.invars[:nc], we.invars[nc:nc + nb], we.invars[nc + nb:]
     # the slot of each tally value defined before the loop
@@ -291,7 +299,9 @@ def forward_only_program(adj, pl):
             vj = AD.eval_jaxpr(body_vjp, bcv + cars, ct_read)
             g = [gi + vj[k] for k, gi in enumerate(g)]
             return (AD.eval_jaxpr(sp.body, bcv + cars), g)
-        cars_f, g = L.while_loop(cond_f, body_f, (cars0, g0)) if sp.ncar else (cars0, g0)
+        never = (not sp.cond.eqns and isinstance(sp.cond.outvars[0], C.Lit)
+                 and not bool(sp.cond.outvars[0].val))          # (the loop split() adds to a loop-free item)
+        cars_f, g = L.while_loop(cond_f, body_f, (cars0, g0)) if sp.ncar and not never else (cars0, g0)
         cars_f = list(cars_f)
         post_outs = AD.eval_jaxpr(sp.post, Pv + cars_f)
         post_cts = []

@@ -180,9 +180,9 @@ def test_records_tracing_and_errors():
 def test_spawn_tracing_and_errors():
     """t.spawn: a hidden token tally threaded like an emit, one `tallymap_spawn` per spawn with the child's leaves
     (converted to the mapped inputs' dtypes); the generated kernel stages children per wave, claims their tickets
-    per flush and bounds them by the capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input, Records
-    with spawn and reverse mode through spawn raise (reference edge.py:183-188); the jvp program's spawn stores
-    the child's tangents with it."""
+    per flush and bounds them by the capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input and Records
+    with spawn raise (reference edge.py:183-188); the jvp program's spawn stores the child's tangents with it; the
+    tree adjoint's recording and adjoint programs have the extra columns and operands they need."""
     from tallymap_amd._tally import QKEY
     from tallymap_amd.backend import kernel as K
 
@@ -211,8 +211,15 @@ def test_spawn_tracing_and_errors():
     with pytest.raises(tm.UnsupportedError, match="Records"):
         tm.vmap(lambda t, x: t.append("r", {"v": x}).spawn(x), outputs={"r": tm.Records({"v": np.float32}, 8)},
                 spawn=tm.Queue(8))._prepare((xs,))
-    with pytest.raises(tm.UnsupportedError, match="spawn"):
-        tm.grad(f)(g0, xs)
+    # the tree adjoint's programs: the recording forward stores (parent, ordinal) with each child and returns the
+    # item's spawn count; the adjoint program takes its first child slot and emits the child's float operands
+    r = f._prepare((g0, xs), "record")[0]
+    assert r.spawn_mode == "record" and r.qcount == 0 and len(K.build(r)[1].r_q) == 4
+    a = f._prepare((g0, xs), "adjoint")[0]
+    from tallymap_amd._tally import QF
+    assert a.spawn is None and a.nP == 3 and a.p_avals()[2].dtype == np.int32
+    assert [s.shape for s in a.tallies if s.name == QF] == [(100,)]
+    assert not any(e.prim == "tallymap_spawn" for e in C.walk_eqns(a.jaxpr))
     from tallymap_amd._api import _jvp_prog
     q = _jvp_prog(p, (False, True), (), 2)       # two tangent lanes: the child stores x' of each lane
     w = next(e for e in q.jaxpr.eqns if e.prim == "while")
