@@ -191,7 +191,8 @@ def _shower_particle(t, p, theta):
 def bench_spawn(steps, warmup):
     """spawn throughput: the shower from 1,048,576 roots (about 67M particles in 7 generations, Queue 2^25): one
     call is a launch per generation with a device-to-host read of the ticket count between them; timed with HIP
-    events on torch's current stream around the whole call (the host's generation loop included)."""
+    events on torch's current stream around the whole call (the host's generation loop included).  Then the tree
+    adjoint's gradient w.r.t. theta, timed the same way (recording forward + one adjoint launch per generation)."""
     import torch
 
     import tallymap_amd as tm
@@ -220,9 +221,25 @@ def bench_spawn(steps, warmup):
     if dr or int(count.sum()) != n + sp:
         raise RuntimeError(f"spawn bench: {sp} spawned, {dr} dropped, {int(count.sum())} particles counted")
     gens = int(np.count_nonzero(count))
+    # the tree adjoint: d <w, dep> / d theta (the recording forward, then one replay-adjoint launch per
+    # generation, deepest first)
+    w = torch.linspace(1.0, 2.0, SHOWER_NZ, dtype=torch.float32, device="cuda")
+    g = tm.grad(f, weights={"dep": w}, argnums=1)
+    g(roots, theta)
+    torch.cuda.synchronize()
+    gev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for e in gev:
+        e[0].record(stream)
+        gr = g(roots, theta)
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    gms = float(np.mean([e[0].elapsed_time(e[1]) for e in gev]))
+    if not bool(torch.isfinite(gr).all()):
+        raise RuntimeError(f"spawn bench: tree adjoint gradient {gr.tolist()}")
     print("bench: spawn done", file=sys.stderr, flush=True)
     return {"roots": n, "children": sp, "generations": gens, "queue": 1 << 25, "ms": ms,
-            "particles_per_s": (n + sp) / (ms * 1e-3)}
+            "particles_per_s": (n + sp) / (ms * 1e-3), "grad_ms": gms,
+            "grad_particles_per_s": (n + sp) / (gms * 1e-3)}
 
 
 def bench_configs(steps, warmup, with_cpu):
