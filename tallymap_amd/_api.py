@@ -310,7 +310,7 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves);
     spawn: the Queue capacity (ctree: the structure a spawned child must have); spawn_mode: None, or one of the
     tree adjoint's programs, 'record' / 'adjoint' (Tally.spawn)."""
-    from ._tally import KI, KK, QF, QKEY, RSEP, rkey
+    from ._tally import KI, KK, QF, QKEY, RADJ, RSEP, rkey
     tspecs = []
     recs = []
     for n in sorted(outs_spec):
@@ -323,9 +323,16 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
                 if dt not in SUM_DTYPES:
                     raise UnsupportedError(f"tallymap: Records field {n}.{f} of dtype {dt}: supported are "
                                            f"{', '.join(d.name for d in SUM_DTYPES)}")
+                if spawn_mode == "adjoint":            # (the adjoint program: float fields at canonical slots)
+                    if dt == C.F64:
+                        raise UnsupportedError(f"tallymap: reverse mode through the float64 Records field {n}.{f}")
+                    if dt == C.F32:
+                        tspecs.append(TSpec(rkey(n, f), (s.capacity,), dt))
+                    continue
                 tspecs.append(TSpec(rkey(n, f), (s.capacity,), dt))
-            tspecs.append(TSpec(rkey(n, KI), (s.capacity,), C.I32))
-            tspecs.append(TSpec(rkey(n, KK), (s.capacity,), C.I32))
+            if spawn_mode != "adjoint":
+                tspecs.append(TSpec(rkey(n, KI), (s.capacity,), C.I32))
+                tspecs.append(TSpec(rkey(n, KK), (s.capacity,), C.I32))
             recs.append((n, s.capacity, fields))
             continue
         shape = (s.shape,) if isinstance(s.shape, int) else tuple(s.shape)
@@ -364,17 +371,22 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     try:
         tin = [C.Tracer(b.new_invar(a)) for a in tav]
         pin = [C.Tracer(b.new_invar(a)) for a in pav]
-        off = C.Tracer(b.new_invar(C.AVal((), C.I32))) if spawn_mode == "adjoint" else None
+        off = C.Tracer(b.new_invar(C.AVal((), C.I32))) if spawn_mode == "adjoint" and spawn is not None else None
+        # (the Records adjoint program: each item's canonical offset per Records output, one operand each)
+        roff = [C.Tracer(b.new_invar(C.AVal((), C.I32))) for _ in recs] if spawn_mode == "adjoint" else []
         bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
         rec0 = {}
-        if recs:
+        if roff:
+            rec0 = {r: (0, o) for (r, _, _), o in zip(recs, roff)}
+        elif recs:
             cid = C.bind("tallymap_item_index", [], [C.AVal((), C.I32)])[0]
             rec0 = {r: (0, cid) for r, _, _ in recs}
-        if spawn_mode == "record":
+        if spawn_mode == "record" and spawn is not None:
             rec0[QKEY] = (0, C.bind("tallymap_item_index", [], [C.AVal((), C.I32)])[0])
-        elif spawn_mode == "adjoint":
+        elif spawn_mode == "adjoint" and spawn is not None:
             rec0[QKEY] = (0, off)
         rinfo = tuple(recs) + (((QKEY, ctree, tuple(pav), spawn_mode),) if spawn is not None else ())
+        rinfo += ((RADJ, None, None),) if roff else ()
         t = Tally({n: x for n, x in zip(names, tin)}, shapes, rec0, rinfo or None)
         m = unflatten(ptree, pin) if ptree is not None else pin
         bb = unflatten(btree, bin_) if btree is not None else bin_
@@ -396,7 +408,7 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
                 v = C.Tracer(C.bind("copy", [C.literal(v)], [C.literal(v).aval.strong()])[0].var)
             outs.append(b.local(v.var))
         counts = []
-        for r, _, _ in recs:              # the per-item record counts (hidden per-item results)
+        for r, _, _ in (recs if not roff else ()):      # the per-item record counts (hidden per-item results)
             k = t2._r[r][0]
             if not C.is_traced(k):
                 k = C.Tracer(C.bind("copy", [C.Lit(int(k), C.AVal((), C.I32))], [C.AVal((), C.I32)])[0].var)
@@ -428,8 +440,9 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     if b.captured:
         raise C.TraceError("tallymap: the item function closes over a traced value of another call")
     check_tallies(jx, len(tspecs), where)
-    prog = ItemProgram(jx, tuple(tspecs), len(pav) + (spawn_mode == "adjoint"), len(bav), trunc,
-                       "primal" if spawn_mode is None else f"spawn_{spawn_mode}", where, tuple(recs), tuple(counts),
+    prog = ItemProgram(jx, tuple(tspecs), len(pav) + (off is not None) + len(roff), len(bav), trunc,
+                       "primal" if spawn_mode is None else f"spawn_{spawn_mode}", where,
+                       tuple(recs) if not roff else (), tuple(counts),
                        int(spawn) if spawn is not None and spawn_mode != "adjoint" else None, spawn_mode, qcount)
     return prog, meta
 
@@ -595,24 +608,46 @@ def vjp(mapped, *args, argnums=None):
 
 def _pullback(mapped, args, argnums):
     from . import backend as B
+    from ._tally import RSEP
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     if prog.spawn is not None:
         return _tree_pullback(mapped, args, argnums)
     an = _argnums(argnums, len(args))
-    wrt = _float_args(prog, axes, an)
+    vprog, extra, bad = prog, [], False
+    if prog.records:
+        # reverse mode through Records (the reference's fill twin, _api.py:856-870): the forward gives each item's
+        # record count, hence its canonical offset per output; the adjoint program emits every float field at its
+        # record's slot, so the records' cotangents reach the appended values
+        import torch
+        vprog = mapped._prepare(args, "adjoint")[0]
+        o = B.run(prog, pi, bc, N, mapped._opts)
+        for j, (r, cap, _) in enumerate(prog.records):
+            c = o.ys[prog.counts[j]].long()
+            extra.append((torch.cumsum(c, 0) - c).clamp(max=cap).to(torch.int32))
+            bad = bad or bool((o.rcount[j] > cap).item())     # (an output past its capacity: NaN, as the forward)
+    wrt = _float_args(vprog, axes, an)
 
     def pullback(ct_outputs=None, ct_per_item=None):
         cts = {}
-        for k, s in enumerate(prog.tallies):
-            if ct_outputs and s.name in ct_outputs:
+        for k, s in enumerate(vprog.tallies):
+            if not ct_outputs:
+                break
+            if s.name in ct_outputs:
                 cts[k] = ct_outputs[s.name]
+            elif RSEP in s.name:                     # a Records field: ct_outputs[name][field]
+                r, f = s.name.split(RSEP, 1)
+                if isinstance(ct_outputs.get(r), dict) and f in ct_outputs[r]:
+                    cts[k] = ct_outputs[r][f]
         cys = {}
         if ct_per_item is not None:
             yl, _ = flatten(ct_per_item)
             for j, x in enumerate(yl):
                 if x is not None:
                     cys[j] = x
-        g_pi, g_bc, ntr = B.run_vjp(prog, wrt, pi, bc, N, cts, cys, mapped._opts)
+        g_pi, g_bc, ntr = B.run_vjp(vprog, wrt, list(pi) + extra, bc, N, cts, cys, mapped._opts)
+        if bad:
+            g_pi = [x.float().fill_(float("nan")) for x in g_pi]
+            g_bc = [x.float().fill_(float("nan")) for x in g_bc]
         out = []
         gp, gb = iter(g_pi), iter(g_bc)
         p = b = 0

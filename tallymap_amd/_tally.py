@@ -18,6 +18,7 @@ RSEP = "\x1f"
 KI, KK = RSEP + "i", RSEP + "k"
 QKEY = RSEP + "q"          # the spawn token: a hidden discard tally that orders t.spawn like an emit
 QF = RSEP + "qf"           # the tree adjoint's child-slot tally: a child's float operands, emitted at its slot
+RADJ = RSEP + "radj"       # (in the records info) the Records adjoint program: appends emit at canonical slots
 
 
 def rkey(name, field):
@@ -39,7 +40,7 @@ class Tally:
         return cls(a, shapes, rec, rinfo)
 
     def _records_info(self):
-        return tuple(r for r in (self._ri or ()) if r[0] != QKEY)
+        return tuple(r for r in (self._ri or ()) if not r[0].startswith(RSEP))
 
     def _shapes_key(self):
         return tuple(sorted((n, tuple(s)) for n, s in self._shapes.items()))
@@ -148,6 +149,20 @@ class Tally:
         k2 = k + wi
         if not C.is_traced(w) and not w:
             return self
+        if any(r[0] == RADJ for r in (self._ri or ())):
+            # the Records adjoint program: record (i, k) of the forward sits at canonical slot off[i] + k (cid holds
+            # off[i], an operand); each float field is EMITTED there into a float tally of the capacity, so the
+            # replay adjoint hands the field the cotangent of its record (reference _api.py:856-870, the fill twin)
+            from . import numpy as jnp
+            a = dict(self._a)
+            slot = cid + k
+            idx = jnp.where(w, slot, -1) if C.is_traced(w) else slot
+            for (f, dt), v in zip(fields, vals):
+                if dt not in (C.F32, C.F64) or not C.is_traced(v):
+                    continue
+                t = a[rkey(name, f)]
+                a[rkey(name, f)] = C.Tracer(C.bind("tallymap_emit", [t.var, idx.var, v.var], [t.aval])[0].var)
+            return Tally(a, self._shapes, {**self._r, name: (k2, cid)}, self._ri)
         kk = self._a[rkey(name, KK)]
         kv = k.var if C.is_traced(k) else C.literal(int(k), C.I32, weak=False)
         wv = w.var if C.is_traced(w) else C.literal(True, C.BOOL, weak=False)
