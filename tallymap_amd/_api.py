@@ -308,11 +308,17 @@ def item_name(fn):
 def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=None, spawn=None, ctree=None,
                   spawn_mode=None):
     """trace `fn(tally, *args)` into an ItemProgram.  pav / bav: per-item / broadcast operand avals (leaves);
-    spawn: the Queue capacity (ctree: the structure a spawned child must have); spawn_mode: None, or one of the
-    tree adjoint's programs, 'record' / 'adjoint' (Tally.spawn)."""
+    spawn: the Queue capacity (ctree: the structure a spawned child must have); spawn_mode: None, or a derived
+    program: 'record' (the recording forward of a spawning item: children store parent and ordinal; Records appends
+    are only counted), 'adjoint' (spawns and Records appends emit their float values at canonical slots, the
+    offsets being per-item operands) or 'fill' (Records with spawn: every field emitted at its canonical slot, the
+    Sums discarded, spawns inert)."""
     from ._tally import KI, KK, QF, QKEY, RADJ, RSEP, rkey
     tspecs = []
     recs = []
+    # how appends run: one pass (claimed raw slots), only counted, or emitted at canonical offsets (operands)
+    rmode = ({None: None, "record": "count" if spawn is not None else None, "adjoint": "adjoint", "fill": "fill"}
+             [spawn_mode])
     for n in sorted(outs_spec):
         s = outs_spec[n]
         if RSEP in n:
@@ -323,14 +329,15 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
                 if dt not in SUM_DTYPES:
                     raise UnsupportedError(f"tallymap: Records field {n}.{f} of dtype {dt}: supported are "
                                            f"{', '.join(d.name for d in SUM_DTYPES)}")
-                if spawn_mode == "adjoint":            # (the adjoint program: float fields at canonical slots)
+                if rmode == "adjoint":                 # (the adjoint program: float fields at canonical slots)
                     if dt == C.F64:
                         raise UnsupportedError(f"tallymap: reverse mode through the float64 Records field {n}.{f}")
                     if dt == C.F32:
                         tspecs.append(TSpec(rkey(n, f), (s.capacity,), dt))
                     continue
-                tspecs.append(TSpec(rkey(n, f), (s.capacity,), dt))
-            if spawn_mode != "adjoint":
+                if rmode != "count":
+                    tspecs.append(TSpec(rkey(n, f), (s.capacity,), dt))
+            if rmode is None:
                 tspecs.append(TSpec(rkey(n, KI), (s.capacity,), C.I32))
                 tspecs.append(TSpec(rkey(n, KK), (s.capacity,), C.I32))
             recs.append((n, s.capacity, fields))
@@ -347,10 +354,9 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
             raise ValueError(f"tallymap: Sum output {n!r}: scale must be finite and positive, got {s.scale!r}")
         if int(np.prod(shape, dtype=np.int64)) > MAX_ITEMS:
             raise ValueError(f"tallymap: output {n!r} has more than 2^31 - 1 cells")
-        tspecs.append(TSpec(n, shape, dt, exact, fixed=fixed, scale=scale))
+        tspecs.append(TSpec(n, shape, dt, exact, fixed=fixed, scale=scale,
+                            kind="discard" if spawn_mode == "fill" else "sum"))
     if spawn is not None:
-        if recs:
-            raise UnsupportedError("tallymap: Records outputs together with spawn are not supported by this backend")
         tspecs.append(TSpec(QKEY, (1,), C.I32, kind="discard"))    # the spawn token (orders t.spawn like an emit)
         nf = sum(a.size for a in pav if a.dtype in (C.F32, C.F64))
         if spawn_mode == "adjoint" and nf:
@@ -373,7 +379,7 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         pin = [C.Tracer(b.new_invar(a)) for a in pav]
         off = C.Tracer(b.new_invar(C.AVal((), C.I32))) if spawn_mode == "adjoint" and spawn is not None else None
         # (the Records adjoint program: each item's canonical offset per Records output, one operand each)
-        roff = [C.Tracer(b.new_invar(C.AVal((), C.I32))) for _ in recs] if spawn_mode == "adjoint" else []
+        roff = [C.Tracer(b.new_invar(C.AVal((), C.I32))) for _ in recs] if rmode in ("adjoint", "fill") else []
         bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
         rec0 = {}
         if roff:
@@ -386,7 +392,7 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         elif spawn_mode == "adjoint" and spawn is not None:
             rec0[QKEY] = (0, off)
         rinfo = tuple(recs) + (((QKEY, ctree, tuple(pav), spawn_mode),) if spawn is not None else ())
-        rinfo += ((RADJ, None, None),) if roff else ()
+        rinfo += ((RADJ, rmode, None),) if rmode is not None and recs else ()
         t = Tally({n: x for n, x in zip(names, tin)}, shapes, rec0, rinfo or None)
         m = unflatten(ptree, pin) if ptree is not None else pin
         bb = unflatten(btree, bin_) if btree is not None else bin_
@@ -442,9 +448,67 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     check_tallies(jx, len(tspecs), where)
     prog = ItemProgram(jx, tuple(tspecs), len(pav) + (off is not None) + len(roff), len(bav), trunc,
                        "primal" if spawn_mode is None else f"spawn_{spawn_mode}", where,
-                       tuple(recs) if not roff else (), tuple(counts),
-                       int(spawn) if spawn is not None and spawn_mode != "adjoint" else None, spawn_mode, qcount)
+                       tuple(recs) if rmode is None else (), tuple(counts),
+                       int(spawn) if spawn is not None and spawn_mode not in ("adjoint", "fill") else None,
+                       spawn_mode, qcount)
     return prog, meta
+
+
+def _records_spawn(prepare, opts, names, args):
+    """Records outputs of a spawning call (reference _api.py:817-890), in two passes.  The recording forward runs
+    the tree (the Sums, the stats, each item's record counts, every generation in canonical order); record k of
+    node m sits at offset[m] + k, the nodes numbered roots first, then generation by generation (a parent's
+    children consecutive, by ordinal: the reference's _tree_order), offset the exclusive prefix sum of the nodes'
+    counts.  The fill pass runs the known generations again with every append EMITTED at its slot into zeroed
+    tallies of the capacity (0 + v = v).  A Records output past its capacity, a dropped child or a truncated item
+    or child makes every float output NaN and every integer record field -1."""
+    import torch
+
+    from . import backend as B
+    prog, meta, pi, bc, N, _ = prepare(args, "record")
+    fprog = prepare(args, "fill")[0]
+    o = B.run(prog, pi, bc, N, opts)
+    res_out = _sum_outputs(prog, o, names)
+    stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
+    stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
+    ys, trunc = _split_ys(prog, list(o.ys))
+    trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
+    recs = list(prepare(args)[0].records)      # (name, capacity, fields) of each Records output
+    allc = [torch.cat([gc[j].long() for gc in o.gen_counts]) for j in range(len(recs))]
+    appended = [c.sum() for c in allc]
+    over = any(bool((a > cap).item()) for a, (_, cap, _) in zip(appended, recs))
+    bad = over or bool((o.stats[ST["children_dropped"]] != 0).item()) or (
+        prog.trunc is not None and bool(((o.stats[ST["children_truncated"]] != 0)
+                                         | (stats["n_truncated"] != 0)).item()))
+    stats["appended"], stats["records_dropped"], stats["records_mismatch"] = {}, {}, {}
+    for (r, cap, _), a in zip(recs, appended):
+        stats["appended"][r], stats["records_dropped"][r] = a, (a - cap).clamp(min=0)
+        stats["records_mismatch"][r] = 0
+    rt = {}
+    if o.generations is not None and not over:
+        sizes = [n for _, _, n in o.generations]
+        offs = [(torch.cumsum(c, 0) - c).clamp(max=cap).to(torch.int32).split(sizes)
+                for c, (_, cap, _) in zip(allc, recs)]
+        gens = [(list(ops) + [offs[j][g] for j in range(len(recs))], n)
+                for g, (ops, _, n) in enumerate(o.generations)]
+        fo = B.run_generations(fprog, gens, bc, opts)
+        rt = {fprog.tallies[k].name: t for k, t in zip(fprog.out_tallies, fo.tallies)}
+    from ._tally import rkey
+    for r, cap, fields in recs:
+        res_out[r] = {}
+        for f, dt in fields:
+            t = rt.get(rkey(r, f))
+            if t is None:
+                t = torch.zeros((cap,), dtype=B.torch_dtype(dt), device="cuda")
+            if bad:
+                t = t.fill_(float("nan")) if dt in (C.F32, C.F64) else t.fill_(-1)
+            res_out[r][f] = t
+    if over:                                   # (a Records output past its capacity poisons every float Sum too)
+        for n in list(res_out):
+            v = res_out[n]
+            if not isinstance(v, dict) and v.dtype in (torch.float32, torch.float64):
+                v.fill_(float("nan"))
+    return Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
 
 
 def _split_ys(prog, ys):
@@ -556,6 +620,8 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
     def mapped(*args):
         from . import backend as B
         prog, meta, pi, bc, N, _ = prepare(args)
+        if prog.records and prog.spawn is not None:
+            return _records_spawn(prepare, opts, names, args)
         o = B.run(prog, pi, bc, N, opts)
         res_out = _sum_outputs(prog, o, names)
         stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
@@ -689,25 +755,44 @@ def _tree_pullback(mapped, args, argnums):
     o = B.run(rprog, pi, bc, N, mapped._opts)
     gens = o.generations
     Q = int(rprog.spawn)
+    # Records outputs of the call: their appends emit at the canonical node order's offsets (per generation)
+    recs = list(mapped._prepare(args)[0].records)
+    roffs, over = [[] for _ in (gens or ())], False
+    if recs and gens is not None:
+        sizes = [n for _, _, n in gens]
+        for j, (_, cap, _) in enumerate(recs):
+            c = torch.cat([gc[j].long() for gc in o.gen_counts])
+            over = over or bool((c.sum() > cap).item())
+            for g, x in enumerate((torch.cumsum(c, 0) - c).clamp(max=cap).to(torch.int32).split(sizes)):
+                roffs[g].append(x)
     nf = sum(max(1, pav[j].size) for j in fpi)
     an_slots = {s.name: k for k, s in enumerate(aprog.tallies)}
     qf = an_slots.get(QF)
 
     def pullback(ct_outputs=None, ct_per_item=None):
+        from ._tally import RSEP
         cts = {an_slots[n]: v for n, v in (ct_outputs or {}).items() if n in an_slots}
+        for n, k in an_slots.items():             # a Records field: ct_outputs[name][field]
+            if RSEP in n and not n.startswith(RSEP):
+                r, f = n.split(RSEP, 1)
+                if isinstance((ct_outputs or {}).get(r), dict) and f in ct_outputs[r]:
+                    cts[k] = ct_outputs[r][f]
         cys = {}
         if ct_per_item is not None:
             yl, _ = flatten(ct_per_item)
             cys = {j: x for j, x in enumerate(yl) if x is not None}
-        nan = gens is None
-        runs = gens if gens is not None else [(list(pi), torch.zeros((N,), dtype=torch.int32, device="cuda"), N)]
+        nan = gens is None or over
+        z = torch.zeros((N,), dtype=torch.int32, device="cuda")
+        runs = gens if gens is not None else [(list(pi), z, N)]
         ct_next, g_bc, g_root = None, None, None
         for g in reversed(range(len(runs))):
             ops, off, n = runs[g]
             ct = dict(cts)
             if qf is not None:
                 ct[qf] = ct_next if ct_next is not None else 0.0
-            gp, gb, _ = B.run_vjp(aprog, wrt, list(ops) + [off], bc, n, ct, cys if g == 0 else {}, mapped._opts)
+            ro = roffs[g] if gens is not None else [z] * len(recs)
+            gp, gb, _ = B.run_vjp(aprog, wrt, list(ops) + [off] + ro, bc, n, ct, cys if g == 0 else {},
+                                  mapped._opts)
             g_bc = gb if g_bc is None else [a + b for a, b in zip(g_bc, gb)]
             if g == 0:
                 g_root = gp
@@ -766,6 +851,9 @@ def _run_tangents(mapped, args, tans, lanes):
     of the float per-item results (None for the others)])."""
     from . import backend as B
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
+    if prog.records and prog.spawn is not None:
+        raise UnsupportedError("tallymap: forward mode through Records outputs of a spawning call is not supported "
+                               "by this backend")
     pt, bt, pp, pb = [], [], [], []
     for pos, x in enumerate(axes):
         leaves, _ = flatten(args[pos])

@@ -18,7 +18,8 @@ RSEP = "\x1f"
 KI, KK = RSEP + "i", RSEP + "k"
 QKEY = RSEP + "q"          # the spawn token: a hidden discard tally that orders t.spawn like an emit
 QF = RSEP + "qf"           # the tree adjoint's child-slot tally: a child's float operands, emitted at its slot
-RADJ = RSEP + "radj"       # (in the records info) the Records adjoint program: appends emit at canonical slots
+RADJ = RSEP + "radj"       # (in the records info) how appends run: 'count' (only the ordinal), 'fill' (every field
+                           # emitted at its canonical slot), 'adjoint' (float fields emitted there)
 
 
 def rkey(name, field):
@@ -149,19 +150,23 @@ class Tally:
         k2 = k + wi
         if not C.is_traced(w) and not w:
             return self
-        if any(r[0] == RADJ for r in (self._ri or ())):
-            # the Records adjoint program: record (i, k) of the forward sits at canonical slot off[i] + k (cid holds
-            # off[i], an operand); each float field is EMITTED there into a float tally of the capacity, so the
-            # replay adjoint hands the field the cotangent of its record (reference _api.py:856-870, the fill twin)
+        rmode = next((r[1] for r in (self._ri or ()) if r[0] == RADJ), None)
+        if rmode == "count":           # (the count pass of Records with spawn: only the item's ordinal advances)
+            return Tally(self._a, self._shapes, {**self._r, name: (k2, cid)}, self._ri)
+        if rmode is not None:
+            # record (i, k) sits at canonical slot off[i] + k (cid holds off[i], an operand).  'fill' EMITS every
+            # field there into a zeroed tally of the capacity (0 + v = v: the reference's fill pass, _api.py:856-870);
+            # 'adjoint' emits the float fields, so the replay adjoint hands each the cotangent of its record
             from . import numpy as jnp
             a = dict(self._a)
             slot = cid + k
             idx = jnp.where(w, slot, -1) if C.is_traced(w) else slot
             for (f, dt), v in zip(fields, vals):
-                if dt not in (C.F32, C.F64) or not C.is_traced(v):
+                if rmode == "adjoint" and (dt not in (C.F32, C.F64) or not C.is_traced(v)):
                     continue
                 t = a[rkey(name, f)]
-                a[rkey(name, f)] = C.Tracer(C.bind("tallymap_emit", [t.var, idx.var, v.var], [t.aval])[0].var)
+                vv = v.var if C.is_traced(v) else C.literal(np.asarray(v).astype(dt), dt, weak=False)
+                a[rkey(name, f)] = C.Tracer(C.bind("tallymap_emit", [t.var, idx.var, vv], [t.aval])[0].var)
             return Tally(a, self._shapes, {**self._r, name: (k2, cid)}, self._ri)
         kk = self._a[rkey(name, KK)]
         kv = k.var if C.is_traced(k) else C.literal(int(k), C.I32, weak=False)
@@ -225,6 +230,8 @@ class Tally:
         if mode is None:
             new = C.bind("tallymap_spawn", [tok.var, wv] + vs, [tok.aval])[0]
             return self._with(QKEY, new)
+        if mode == "fill":             # (the fill pass of Records with spawn runs known generations: no spawn)
+            return self
         # the tree adjoint's two programs carry the item's spawn count k (its children's ordinals)
         k, ref = self._r[QKEY]
         wi = C.convert(w, C.I32) if C.is_traced(w) else 1

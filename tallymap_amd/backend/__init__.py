@@ -175,7 +175,8 @@ def _run_spawn(c, prog, ins, N):
     The tree adjoint's recording forward (prog.spawn_mode 'record': children also store their parent and ordinal)
     puts every generation in canonical order -- the children of item i at off[i] .. off[i] + count[i] - 1, off the
     exclusive prefix sum of the items' spawn counts -- and keeps it: Outputs.generations = [(per-item operands,
-    off int32[n], n)] from the roots down, or None when a child was dropped (the tree is incomplete)."""
+    off int32[n], n)] from the roots down, or None when a child was dropped (the tree is incomplete), and
+    Outputs.gen_counts = per generation, the items' Records counts (prog.counts; kept also after a drop)."""
     import torch
     L = c.layout
     base = L.n_in
@@ -190,11 +191,15 @@ def _run_spawn(c, prog, ins, N):
     spawned = dropped = 0
     ntr_roots = None
     gens, ops, n_cur = [], list(ins[:nP]), N      # (the operands and size of the generation just launched)
+    gcounts = []
     while True:
         w = ctl.cpu().numpy().view(np.uint32)
         if ntr_roots is None:
             ntr_roots = int(w[2])
         cnt = int(w[32]) | (int(w[33]) << 32)
+        if rec and prog.counts:                        # (the launch's per-item results: outs, or the scratch)
+            src = (lambda r: outs[r - base]) if not gcounts else (lambda r: ys_scr[r])
+            gcounts.append([src(L.r_ys[j])[:n_cur].clone() for j in prog.counts])
         if rec and gens is not None:
             counts = (outs[L.r_ys[prog.qcount] - base] if not gens else ys_scr[L.r_ys[prog.qcount]])[:n_cur].long()
             off = torch.cumsum(counts, 0) - counts
@@ -239,7 +244,33 @@ def _run_spawn(c, prog, ins, N):
     ntr = torch.tensor(ntr_roots, dtype=torch.int32, device="cuda") if prog.trunc is not None else None
     o = Outputs(tallies, outs[L.r_stats - base], ys, ntr, {}, [])
     o.generations = gens if rec else None
+    o.gen_counts = gcounts if rec else None
     return o
+
+
+def run_generations(prog, gens, bc, opts):
+    """an ordinary (not spawning) program over known generations -- gens = [(per-item operands, n)] -- as one
+    accumulating launch sequence: tm_zero before the first, tm_post after the last (the fill pass of Records with
+    spawn).  -> Outputs (per-item results of the first generation)."""
+    import torch
+    c = compiled(prog, opts)
+    L = c.layout
+    base = L.n_in
+    if getattr(L, "aux", None):
+        raise Cm.BackendError("internal: run_generations of a program with auxiliary passes")
+    b_ins = [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+    nmax = max(n for _, n in gens)
+    outs = _alloc(c, nmax)
+    for g, (ops, n) in enumerate(gens):
+        ins = [device_tensor(x, a.dtype) for x, a in zip(ops, prog.p_avals())]
+        if g:
+            outs[L.r_ctl - base].view(torch.int32)[0:2].zero_()     # (the item claim counter, per launch)
+        _queue(c, ins + b_ins, outs, n, L.n_zero if g == 0 else 0, 0)
+    _queue(c, [device_tensor(x, a.dtype) for x, a in zip(gens[0][0], prog.p_avals())] + b_ins, outs, 0, 0, L.flags)
+    tallies = [outs[L.r_out[k] - base] for k in prog.out_tallies]
+    ys = [outs[r - base][:gens[0][1]] for r in L.r_ys]
+    ntr = outs[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
+    return Outputs(tallies, outs[L.r_stats - base], ys, ntr, {}, [])
 
 
 _LANES = {}

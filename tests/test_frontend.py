@@ -180,8 +180,8 @@ def test_records_tracing_and_errors():
 def test_spawn_tracing_and_errors():
     """t.spawn: a hidden token tally threaded like an emit, one `tallymap_spawn` per spawn with the child's leaves
     (converted to the mapped inputs' dtypes); the generated kernel stages children per wave, claims their tickets
-    per flush and bounds them by the capacity.  Spawn without a Queue, a child of another structure, a float child leaf for an integer input and Records
-    with spawn raise (reference edge.py:183-188); the jvp program's spawn stores the child's tangents with it; the
+    per flush and bounds them by the capacity.  Spawn without a Queue, a child of another structure and a float child leaf for an integer input raise
+    (reference edge.py:183-188); the jvp program's spawn stores the child's tangents with it; the
     tree adjoint's recording and adjoint programs have the extra columns and operands they need."""
     from tallymap_amd._tally import QKEY
     from tallymap_amd.backend import kernel as K
@@ -208,9 +208,15 @@ def test_spawn_tracing_and_errors():
         tm.vmap(lambda t, g, x: t.spawn(x), outputs={"h": tm.Sum((1,))}, spawn=tm.Queue(8))._prepare((g0, xs))
     with pytest.raises(TypeError, match="float spawned child"):
         tm.vmap(lambda t, g, x: t.spawn((x, x)), outputs={"h": tm.Sum((1,))}, spawn=tm.Queue(8))._prepare((g0, xs))
-    with pytest.raises(tm.UnsupportedError, match="Records"):
-        tm.vmap(lambda t, x: t.append("r", {"v": x}).spawn(x), outputs={"r": tm.Records({"v": np.float32}, 8)},
-                spawn=tm.Queue(8))._prepare((xs,))
+    # Records with spawn: the count pass (no record tallies, a hidden count per Records output) and the fill pass
+    # (fields emitted at canonical offsets, an operand per Records output; the Sums discarded; spawn inert)
+    fr = tm.vmap(lambda t, x: t.append("r", {"v": x}).spawn(x, when=x > 9.0).add("h", 0, x),
+                 outputs={"r": tm.Records({"v": np.float32}, 8), "h": tm.Sum((2,))}, spawn=tm.Queue(8))
+    c = fr._prepare((xs,), "record")[0]
+    assert c.records == () and len(c.counts) == 1 and [s.name for s in c.tallies] == ["h", QKEY]
+    fl = fr._prepare((xs,), "fill")[0]
+    assert fl.nP == 2 and fl.spawn is None and [s.kind for s in fl.tallies] == ["discard", "sum", "discard"]
+    assert not any(e.prim == "tallymap_spawn" for e in C.walk_eqns(fl.jaxpr))
     # the tree adjoint's programs: the recording forward stores (parent, ordinal) with each child and returns the
     # item's spawn count; the adjoint program takes its first child slot and emits the child's float operands
     r = f._prepare((g0, xs), "record")[0]

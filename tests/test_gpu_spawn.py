@@ -386,3 +386,149 @@ def test_spawn_tree_adjoint_dropped_child_is_nan():
     f = tm.vmap(_chain, outputs={"Q": tm.Sum((NB,))}, spawn=tm.Queue(16))
     gx = _np(tm.grad(f, argnums=1)(g0, xs))
     assert np.isnan(gx).all()
+
+
+# ------------------------------------------------------------------------------------ Records of a spawning call
+THR = f32(0.3)
+
+
+def _rcascade(t, gen, x):
+    """the cascade (children x / 2 and x / 4 below generation 2) appending (gen, x) when x > 0.3."""
+    t = t.add("Q", gen, x)
+    t = t.append("r", {"g": gen, "x": x}, when=x > 0.3)
+    t = t.spawn((gen + 1, x * 0.5), when=gen < 2)
+    return t.spawn((gen + 1, x * 0.25), when=gen < 2)
+
+
+def _tree_nodes(xs):
+    """the cascade's nodes in the canonical order (roots, then each generation with a parent's children
+    consecutive, by ordinal): (gen, x, root index, factor) arrays."""
+    gens = [(np.zeros(len(xs), np.int32), xs.astype(f32), np.arange(len(xs)), np.ones(len(xs)))]
+    for g in range(2):
+        _, x, root, fac = gens[-1]
+        cx = np.stack([x * f32(0.5), x * f32(0.25)], 1).reshape(-1).astype(f32)
+        gens.append((np.full(len(cx), g + 1, np.int32), cx, np.repeat(root, 2),
+                     np.stack([fac * 0.5, fac * 0.25], 1).reshape(-1)))
+    return [np.concatenate(c) for c in zip(*gens)]
+
+
+def test_spawn_records_canonical_tree_order():
+    """Records of a spawning call hold node m's records at offset[m] + k, the nodes numbered roots first and then
+    generation by generation, a parent's children consecutive by ordinal (reference _api.py:783-805): bitwise
+    against the numpy enumeration of the tree; the Sum as the plain call's; appended exact."""
+    print("case: spawn + records cascade", flush=True)
+    n = 3000
+    g0, xs = _cascade_inputs(n)
+    f = tm.vmap(_rcascade, outputs={"Q": tm.Sum((NB,), fixed_point=True),
+                                    "r": tm.Records({"g": np.int32, "x": np.float32}, capacity=1 << 15)},
+                spawn=tm.Queue(1 << 14))
+    res = f(g0, xs)
+    _sync()
+    gen, x, _, _ = _tree_nodes(xs)
+    keep = x > THR
+    m = int(keep.sum())
+    assert int(_np(res.stats["appended"]["r"])) == m and int(_np(res.stats["spawned"])) == 6 * n
+    assert np.array_equal(_np(res.outputs["r"]["g"])[:m], gen[keep])
+    assert np.array_equal(_np(res.outputs["r"]["x"])[:m].view(np.uint32), x[keep].view(np.uint32))
+    assert not _np(res.outputs["r"]["x"])[m:].any() and not _np(res.outputs["r"]["g"])[m:].any()
+    want = np.array([sum(Fraction(float(v)) for v in x[gen == g]) if (gen == g).any() else 0 for g in range(NB)])
+    assert np.array_equal(_np(res.outputs["Q"]).view(np.uint32),
+                          np.array([float(w) for w in want], f32).view(np.uint32))
+
+
+def test_spawn_records_overflow_poisons():
+    print("case: spawn + records overflow", flush=True)
+    g0, xs = _cascade_inputs(3000)
+    f = tm.vmap(_rcascade, outputs={"Q": tm.Sum((NB,)), "r": tm.Records({"g": np.int32, "x": np.float32},
+                                                                        capacity=100)}, spawn=tm.Queue(1 << 14))
+    res = f(g0, xs)
+    _sync()
+    assert int(_np(res.stats["appended"]["r"])) > 100
+    assert int(_np(res.stats["records_dropped"]["r"])) == int(_np(res.stats["appended"]["r"])) - 100
+    assert (_np(res.outputs["r"]["g"]) == -1).all() and np.isnan(_np(res.outputs["r"]["x"])).all()
+    assert np.isnan(_np(res.outputs["Q"])).all()
+
+
+def test_spawn_records_tree_adjoint_closed_form():
+    """d (<ct, r.x> + <w, Q>) / d xs through the tree and the records: a node's x is its root's times its factor
+    (1, 1/2, 1/4, ...), so root i's cotangent is the sum over its nodes of factor (w[gen] + [x > 0.3] ct[slot]),
+    against float64 within 1e-5."""
+    print("case: spawn + records tree adjoint", flush=True)
+    n = 3000
+    g0, xs = _cascade_inputs(n)
+    f = tm.vmap(_rcascade, outputs={"Q": tm.Sum((NB,)), "r": tm.Records({"g": np.int32, "x": np.float32},
+                                                                      capacity=1 << 15)}, spawn=tm.Queue(1 << 14))
+    ct = np.random.default_rng(6).uniform(0.5, 1.5, 1 << 15).astype(f32)
+    w = np.arange(1.0, NB + 1, dtype=f32)
+    _, pull = tm.vjp(f, g0, xs, argnums=1)
+    gx = _np(pull({"Q": w, "r": {"x": ct}})).astype(np.float64)
+    gen, x, root, fac = _tree_nodes(xs)
+    keep = x > THR
+    slot = np.cumsum(keep) - 1
+    per = fac * (w[gen].astype(np.float64) + np.where(keep, ct[np.clip(slot, 0, None)].astype(np.float64), 0.0))
+    want = np.bincount(root, per, n)
+    assert np.max(np.abs(gx - want) / np.abs(want)) <= 1e-5
+
+
+def _shower_parented(roots, theta):
+    """the shower's particles in canonical node order (roots, then each generation with a parent's children
+    consecutive in spawn order): (g, final E) per particle, from the float32 emulation."""
+    gen = {k: np.asarray(v).copy() for k, v in roots.items()}
+    out_g, out_e = [], []
+    while len(gen["E"]):
+        m = len(gen["E"])
+        E, z, key, g = gen["E"].astype(f32), gen["z"].astype(f32), gen["key"], gen["g"]
+        n = np.zeros(m, np.int32)
+        nsp = np.zeros(m, np.int64)
+        kids = {k: [] for k in gen}
+        par, ordn = [], []
+        alive = (E > f32(1e-3)) & (n < 40)
+        while alive.any():
+            i = np.nonzero(alive)[0]
+            k = R._host_fold_in(key[i], n[i].astype(np.uint32))
+            u = R._host_uniform(k, 0.0, 1.0, (3,))
+            zi = (z[i] + u[:, 0] * f32(0.5)).astype(f32)
+            dep = (E[i] * theta[0]).astype(f32)
+            split = (u[:, 1] < f32(0.35)) & (g[i] < DEPTH)
+            ec = ((E[i] - dep) * theta[1] * (f32(0.5) + f32(0.5) * u[:, 2])).astype(f32)
+            kids["E"].append(ec[split])
+            kids["z"].append(zi[split])
+            kids["key"].append(R._host_fold_in(k[split], np.ones(int(split.sum()), np.uint32)))
+            kids["g"].append(g[i][split] + 1)
+            par.append(i[split])
+            ordn.append(nsp[i[split]].copy())
+            nsp[i[split]] += 1
+            E[i] = (E[i] - dep - np.where(split, ec, f32(0.0))).astype(f32)
+            z[i] = zi
+            n[i] += 1
+            alive = (E > f32(1e-3)) & (n < 40)
+        out_g.append(g.copy())
+        out_e.append(E.copy())
+        if not par:
+            break
+        o = np.lexsort((np.concatenate(ordn), np.concatenate(par)))
+        gen = {k: np.concatenate(v)[o] for k, v in kids.items()}
+    return np.concatenate(out_g), np.concatenate(out_e)
+
+
+def _rparticle(t, p, theta):
+    t, (n, e) = _particle(t, p, theta)
+    return t.append("end", {"g": p["g"], "E": e}), n
+
+
+def test_spawn_records_shower_node_order():
+    """one record (generation, final energy) per particle of the shower, in canonical node order, bitwise against
+    the emulation with its children sorted by (parent, spawn ordinal)."""
+    print("case: spawn + records shower", flush=True)
+    roots = _roots(2048)
+    theta = np.array(TH, f32)
+    g_w, e_w = _shower_parented(roots, theta)
+    f = tm.vmap(_rparticle, outputs={"dep": tm.Sum((NZ,)), "count": tm.Sum((NZ,), np.int32),
+                                     "end": tm.Records({"g": np.int32, "E": np.float32}, capacity=1 << 18)},
+                in_axes=(0, None), spawn=tm.Queue(1 << 16))
+    res = f(roots, theta)
+    _sync()
+    m = len(g_w)
+    assert int(_np(res.stats["appended"]["end"])) == m
+    assert np.array_equal(_np(res.outputs["end"]["g"])[:m], g_w)
+    assert np.array_equal(_np(res.outputs["end"]["E"])[:m].view(np.uint32), e_w.view(np.uint32))
