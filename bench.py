@@ -34,6 +34,11 @@ GRAD_BYTES_PER_ITEM = 13
 # HBM bytes per launch at N = 4,194,304 from rocprofv3 counter passes (profiles/c2_random_walk_traffic.md):
 # 2 x FETCH_SIZE + 1 x WRITE_SIZE (KiB), the factors those counters read on a plain 1 GiB device copy
 MEASURED_TRAFFIC = {"forward": 77_128_984, "gradient": 56_958_568}
+# wave64 VALU instructions per launch at N = 4,194,304 (rocprofv3 --pmc SQ_INSTS_VALU, profiles/
+# c2_random_walk_sq_counters.md) and MI355X's VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per 4
+# cycles on a 16-lane SIMD, at the 2.4 GHz peak engine clock
+MEASURED_VALU_INSTS = {"forward": 7.029e9, "gradient": 6.721e9}
+VALU_PEAK = 1024 * 2.4e9 / 4
 
 
 def cpu_baseline(x0, keys, drift, max_steps, target_s=10.0):
@@ -410,6 +415,12 @@ def main():
                      "traffic": a.traffic_bytes if a.traffic_bytes is not None
                      else (MEASURED_TRAFFIC[dom] if N == 4_194_304 else None),
                      "algorithmic_bytes_per_launch": bpi * N},
+        # the resource that binds: VALU issue (the HBM roofline above is the contract's; this kernel reads 17 B and
+        # runs ~406 steps of ~230 VALU instructions per item)
+        "valu_roofline": ({"bound": "valu", "achieved": MEASURED_VALU_INSTS[dom] / (dom_ms * 1e-3),
+                           "peak": VALU_PEAK, "unit": "wave64 VALU instructions/s",
+                           "frac": MEASURED_VALU_INSTS[dom] / (dom_ms * 1e-3) / VALU_PEAK,
+                           "insts_per_launch": MEASURED_VALU_INSTS[dom]} if N == 4_194_304 else None),
     }
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(x0, keys, drift, cfg["max_steps"])
