@@ -532,3 +532,69 @@ def test_spawn_records_shower_node_order():
     assert int(_np(res.stats["appended"]["end"])) == m
     assert np.array_equal(_np(res.outputs["end"]["g"])[:m], g_w)
     assert np.array_equal(_np(res.outputs["end"]["E"])[:m].view(np.uint32), e_w.view(np.uint32))
+
+
+def _mixed(t, p):
+    """children of every operand kind the staging rows convert (f64 and i64 as two words, bool as one, a u32 and
+    an f32 array), spawned from inside the branches of a cond inside a loop (divergent lanes at the ballot)."""
+    g = p["g"]
+
+    def body(i, t):
+        def even(t):
+            return t.spawn(dict(g=g + 1, x=p["x"] * 0.5, m=p["m"] * 3 + i, b=~p["b"], u=p["u"] + 1, v=p["v"] * 2.0),
+                           when=g < 2)
+
+        def odd(t):
+            return t.spawn(dict(g=g + 1, x=p["x"] * 0.25, m=p["m"] - i, b=p["b"], u=p["u"] * 2, v=p["v"] * 0.5),
+                           when=g < 2)
+        return lax.cond((p["u"][0] + i) % 2 == 0, even, odd, t)
+    t = lax.fori_loop(0, 2, body, t)
+    t = t.add("x", g, p["x"])
+    t = t.add("m", g, p["m"])
+    t = t.add("b", g, p["b"].astype(jnp.int32))
+    t = t.add("u", g, p["u"][0] + p["u"][1])
+    return t.add("v", g, p["v"][0] + p["v"][1] + p["v"][2])
+
+
+def test_spawn_operand_kinds_and_divergent_spawns():
+    """per-generation sums of every operand against the numpy enumeration of the tree, exactly (dyadic f64 and f32
+    values, integers)."""
+    print("case: spawn operand kinds", flush=True)
+    n = 5000
+    rng = np.random.default_rng(8)
+    p = dict(g=np.zeros(n, np.int32), x=rng.integers(0, 1 << 20, n).astype(np.float64) / 1024.0,
+             m=rng.integers(-1 << 40, 1 << 40, n).astype(np.int64), b=rng.integers(0, 2, n).astype(bool),
+             u=rng.integers(0, 1 << 20, (n, 2)).astype(np.uint32), v=(rng.integers(0, 1 << 10, (n, 3)) / 64.0).astype(f32))
+    outs = {"x": tm.Sum((4,), np.float64), "m": tm.Sum((4,), np.int64), "b": tm.Sum((4,), np.int32),
+            "u": tm.Sum((4,), np.uint32), "v": tm.Sum((4,), fixed_point=True)}
+    res = tm.vmap(_mixed, outputs=outs, spawn=tm.Queue(1 << 16))(p)
+    _sync()
+    want = {k: np.zeros(4, np.float64 if k in ("x", "v") else np.int64) for k in outs}
+    cur, spawned = p, 0
+    for g in range(3):
+        want["x"][g] = cur["x"].sum()
+        want["m"][g] = cur["m"].sum()
+        want["b"][g] = cur["b"].sum()
+        want["u"][g] = int((cur["u"][:, 0].astype(np.uint64) + cur["u"][:, 1]).astype(np.uint32).astype(np.uint64).sum()) % (1 << 32)
+        want["v"][g] = cur["v"].astype(np.float64).sum()
+        if g == 2:
+            break
+        kids = {k: [] for k in cur}
+        for i in range(2):
+            ev = (cur["u"][:, 0] + np.uint32(i)) % 2 == 0
+            for msk, even in ((ev, True), (~ev, False)):
+                c = {k: v[msk] for k, v in cur.items()}
+                kids["g"].append(c["g"] + 1)
+                kids["x"].append(c["x"] * (0.5 if even else 0.25))
+                kids["m"].append(c["m"] * 3 + i if even else c["m"] - i)
+                kids["b"].append(~c["b"] if even else c["b"])
+                kids["u"].append(c["u"] + np.uint32(1) if even else c["u"] * np.uint32(2))
+                kids["v"].append((c["v"] * f32(2.0) if even else c["v"] * f32(0.5)).astype(f32))
+        cur = {k: np.concatenate(v) for k, v in kids.items()}
+        spawned += len(cur["g"])
+    assert int(_np(res.stats["spawned"])) == spawned
+    assert np.array_equal(_np(res.outputs["x"]), want["x"])
+    assert np.array_equal(_np(res.outputs["m"]), want["m"])
+    assert np.array_equal(_np(res.outputs["b"]).astype(np.int64), want["b"])
+    assert np.array_equal(_np(res.outputs["u"]).astype(np.int64), want["u"])
+    assert np.array_equal(_np(res.outputs["v"]), want["v"].astype(f32))     # (the exact sum, rounded once)
