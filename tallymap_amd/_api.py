@@ -474,8 +474,10 @@ def _records_spawn(prepare, opts, names, args):
     ys, trunc = _split_ys(prog, list(o.ys))
     trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
     recs = list(prepare(args)[0].records)      # (name, capacity, fields) of each Records output
-    allc = [torch.cat([gc[j].long() for gc in o.gen_counts]) for j in range(len(recs))]
-    appended = [c.sum() for c in allc]
+    allc = [torch.cat([gc[j] for gc in o.gen_counts]) for j in range(len(recs))]
+    scans = [B.util.exclusive_scan(c) for c in allc]
+    appended = [x[-1] + c[-1] if len(c) else torch.zeros((), dtype=torch.int64, device="cuda")
+                for x, c in zip(scans, allc)]
     over = any(bool((a > cap).item()) for a, (_, cap, _) in zip(appended, recs))
     bad = over or bool((o.stats[ST["children_dropped"]] != 0).item()) or (
         prog.trunc is not None and bool(((o.stats[ST["children_truncated"]] != 0)
@@ -487,8 +489,7 @@ def _records_spawn(prepare, opts, names, args):
     rt = {}
     if o.generations is not None and not over:
         sizes = [n for _, _, n in o.generations]
-        offs = [(torch.cumsum(c, 0) - c).clamp(max=cap).to(torch.int32).split(sizes)
-                for c, (_, cap, _) in zip(allc, recs)]
+        offs = [x.clamp(max=cap).to(torch.int32).split(sizes) for x, (_, cap, _) in zip(scans, recs)]
         gens = [(list(ops) + [offs[j][g] for j in range(len(recs))], n)
                 for g, (ops, _, n) in enumerate(o.generations)]
         fo = B.run_generations(fprog, gens, bc, opts)
@@ -688,8 +689,7 @@ def _pullback(mapped, args, argnums):
         vprog = mapped._prepare(args, "adjoint")[0]
         o = B.run(prog, pi, bc, N, mapped._opts)
         for j, (r, cap, _) in enumerate(prog.records):
-            c = o.ys[prog.counts[j]].long()
-            extra.append((torch.cumsum(c, 0) - c).clamp(max=cap).to(torch.int32))
+            extra.append(B.util.exclusive_scan(o.ys[prog.counts[j]]).clamp(max=cap).to(torch.int32))
             bad = bad or bool((o.rcount[j] > cap).item())     # (an output past its capacity: NaN, as the forward)
     wrt = _float_args(vprog, axes, an)
 
@@ -761,10 +761,11 @@ def _tree_pullback(mapped, args, argnums):
     if recs and gens is not None:
         sizes = [n for _, _, n in gens]
         for j, (_, cap, _) in enumerate(recs):
-            c = torch.cat([gc[j].long() for gc in o.gen_counts])
-            over = over or bool((c.sum() > cap).item())
-            for g, x in enumerate((torch.cumsum(c, 0) - c).clamp(max=cap).to(torch.int32).split(sizes)):
-                roffs[g].append(x)
+            c = torch.cat([gc[j] for gc in o.gen_counts])
+            x = B.util.exclusive_scan(c)
+            over = over or (len(c) > 0 and bool((x[-1] + c[-1] > cap).item()))
+            for g, xg in enumerate(x.clamp(max=cap).to(torch.int32).split(sizes)):
+                roffs[g].append(xg)
     nf = sum(max(1, pav[j].size) for j in fpi)
     an_slots = {s.name: k for k, s in enumerate(aprog.tallies)}
     qf = an_slots.get(QF)

@@ -14,6 +14,7 @@ import numpy as np
 
 from . import compile as Cm
 from . import kernel as K
+from . import util as U
 
 _KERNELS = collections.OrderedDict()
 _LOCK = threading.Lock()
@@ -201,8 +202,8 @@ def _run_spawn(c, prog, ins, N):
             src = (lambda r: outs[r - base]) if not gcounts else (lambda r: ys_scr[r])
             gcounts.append([src(L.r_ys[j])[:n_cur].clone() for j in prog.counts])
         if rec and gens is not None:
-            counts = (outs[L.r_ys[prog.qcount] - base] if not gens else ys_scr[L.r_ys[prog.qcount]])[:n_cur].long()
-            off = torch.cumsum(counts, 0) - counts
+            counts = (outs[L.r_ys[prog.qcount] - base] if not gens else ys_scr[L.r_ys[prog.qcount]])[:n_cur]
+            off = U.exclusive_scan(counts)             # (each item's first child, in canonical order)
             gens.append((ops, off.to(torch.int32), n_cur))
         if cnt == 0:
             break
@@ -216,12 +217,10 @@ def _run_spawn(c, prog, ins, N):
             ys_scr = {r: torch.empty((Q,) + tuple(outs[r - base].shape[1:]), dtype=outs[r - base].dtype,
                                      device="cuda") for r in L.r_ys}
         if rec and gens is not None:                   # the children in canonical (parent, ordinal) order
-            dest = off[cur[nP][:n].long()] + cur[nP + 1][:n].long()
             ops = []
             for t in cur[:nP]:
                 z = torch.empty((n,) + tuple(t.shape[1:]), dtype=t.dtype, device="cuda")
-                sv = {torch.uint32: torch.int32, torch.uint64: torch.int64}.get(t.dtype)   # (no index_put for
-                (z.view(sv) if sv else z)[dest] = (t.view(sv) if sv else t)[:n]          # unsigned words)
+                U.tree_scatter(off, cur[nP], cur[nP + 1], t, z, n)
                 ops.append(z)
         else:
             ops = cur[:nP]

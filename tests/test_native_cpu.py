@@ -190,3 +190,13 @@ def test_exact_kernels_compile_without_shift_hazards():
                 assert not re.search(r"v_(lshlrev_b64|lshrrev_b64|ashrrev_i64)\S*\s+v\[\d+:\d+\],\s*v\d+,", d), o
     finally:
         K.LDS_BYTES = saved
+
+
+def test_util_module_compiles_for_gfx950():
+    """the spawn paths' scan and scatter module builds with hipRTC and holds its entries."""
+    from tallymap_amd.backend import compile as Cm
+    from tallymap_amd.backend import util
+    src = util._source()
+    for e in ("tm_xscan_local", "tm_xscan_top", "tm_xscan_add", "tm_tree_scatter", "tm_tree_scatter_b"):
+        assert f"void __launch_bounds__" in src and e in src
+    assert len(Cm.code_object(src, name="tm_util.hip")) > 0
