@@ -474,6 +474,25 @@ def _records_spawn(prepare, opts, names, args):
     ys, trunc = _split_ys(prog, list(o.ys))
     trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
     recs = list(prepare(args)[0].records)      # (name, capacity, fields) of each Records output
+    bad, over, offs = _tree_records(o, recs, prog, stats)
+    rt = {}
+    if offs is not None:
+        gens = [(list(ops) + [offs[j][g] for j in range(len(recs))], n)
+                for g, (ops, _, n) in enumerate(o.generations)]
+        fo = B.run_generations(fprog, gens, bc, opts)
+        rt = {fprog.tallies[k].name: t for k, t in zip(fprog.out_tallies, fo.tallies)}
+    _tree_records_out(res_out, rt, recs, bad, over, [""])
+    return Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
+
+
+def _tree_records(o, recs, prog, stats):
+    """the Records bookkeeping of a spawning call from its recording forward `o`: each output's exact count
+    (stats appended / records_dropped / records_mismatch), whether any output is past its capacity (`over`) or the
+    call is poisoned (`bad`: that, a dropped child, a truncated item or child), and per output and generation the
+    nodes' canonical offsets (None when the tree is incomplete or an output overflowed)."""
+    import torch
+
+    from . import backend as B
     allc = [torch.cat([gc[j] for gc in o.gen_counts]) for j in range(len(recs))]
     scans = [B.util.exclusive_scan(c) for c in allc]
     appended = [x[-1] + c[-1] if len(c) else torch.zeros((), dtype=torch.int64, device="cuda")
@@ -486,30 +505,38 @@ def _records_spawn(prepare, opts, names, args):
     for (r, cap, _), a in zip(recs, appended):
         stats["appended"][r], stats["records_dropped"][r] = a, (a - cap).clamp(min=0)
         stats["records_mismatch"][r] = 0
-    rt = {}
-    if o.generations is not None and not over:
-        sizes = [n for _, _, n in o.generations]
-        offs = [x.clamp(max=cap).to(torch.int32).split(sizes) for x, (_, cap, _) in zip(scans, recs)]
-        gens = [(list(ops) + [offs[j][g] for j in range(len(recs))], n)
-                for g, (ops, _, n) in enumerate(o.generations)]
-        fo = B.run_generations(fprog, gens, bc, opts)
-        rt = {fprog.tallies[k].name: t for k, t in zip(fprog.out_tallies, fo.tallies)}
+    if o.generations is None or over:
+        return bad, over, None
+    sizes = [n for _, _, n in o.generations]
+    return bad, over, [x.clamp(max=cap).to(torch.int32).split(sizes) for x, (_, cap, _) in zip(scans, recs)]
+
+
+def _tree_records_out(res_out, rt, recs, bad, over, sfx):
+    """res_out[r] = {field: the fill tally rkey(r, field) + suffix}, for each suffix in sfx ('' the primal, "'" or
+    "'l" a tangent lane: float fields only), zeros where the fill did not run; poisoned when `bad` (floats NaN,
+    integers -1); an output past its capacity poisons every float Sum too."""
+    import torch
+
+    from . import backend as B
     from ._tally import rkey
-    for r, cap, fields in recs:
-        res_out[r] = {}
-        for f, dt in fields:
-            t = rt.get(rkey(r, f))
-            if t is None:
-                t = torch.zeros((cap,), dtype=B.torch_dtype(dt), device="cuda")
-            if bad:
-                t = t.fill_(float("nan")) if dt in (C.F32, C.F64) else t.fill_(-1)
-            res_out[r][f] = t
-    if over:                                   # (a Records output past its capacity poisons every float Sum too)
-        for n in list(res_out):
-            v = res_out[n]
-            if not isinstance(v, dict) and v.dtype in (torch.float32, torch.float64):
-                v.fill_(float("nan"))
-    return Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
+    outs = [res_out] if len(sfx) == 1 and sfx[0] == "" else res_out
+    for d, x in zip(outs, sfx):
+        for r, cap, fields in recs:
+            d[r] = {}
+            for f, dt in fields:
+                if x and dt not in (C.F32, C.F64):
+                    continue
+                t = rt.get(rkey(r, f) + x)
+                if t is None:
+                    t = torch.zeros((cap,), dtype=B.torch_dtype(dt), device="cuda")
+                if bad:
+                    t = t.fill_(float("nan")) if dt in (C.F32, C.F64) else t.fill_(-1)
+                d[r][f] = t
+        if over:                               # (a Records output past its capacity poisons every float Sum too)
+            for n in list(d):
+                v = d[n]
+                if not isinstance(v, dict) and v.dtype in (torch.float32, torch.float64):
+                    v.fill_(float("nan"))
 
 
 def _split_ys(prog, ys):
@@ -852,9 +879,10 @@ def _run_tangents(mapped, args, tans, lanes):
     of the float per-item results (None for the others)])."""
     from . import backend as B
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
-    if prog.records and prog.spawn is not None:
-        raise UnsupportedError("tallymap: forward mode through Records outputs of a spawning call is not supported "
-                               "by this backend")
+    recs = list(prog.records)
+    rs = bool(recs) and prog.spawn is not None
+    if rs:      # Records of a spawning call: the recording forward's jvp, then the fill program's over the tree
+        prog = mapped._prepare(args, "record")[0]
     pt, bt, pp, pb = [], [], [], []
     for pos, x in enumerate(axes):
         leaves, _ = flatten(args[pos])
@@ -884,9 +912,21 @@ def _run_tangents(mapped, args, tans, lanes):
     if prog.spawn is not None:
         stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
     trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
-    _record_outputs(prog, o, res_out, stats)
-    primal = Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
     t_tal = [dict() for _ in range(lanes)]
+    if rs:
+        bad, over, offs = _tree_records(o, recs, prog, stats)
+        rt = {}
+        if offs is not None:
+            fprog = mapped._prepare(args, "fill")[0]
+            qf = _jvp_prog(fprog, tuple(pp) + (False,) * len(recs), tuple(pb), lanes)
+            gens = [(list(ops[:prog.nP]) + [offs[j][g] for j in range(len(recs))] + list(ops[prog.nP:]), n)
+                    for g, (ops, _, n) in enumerate(o.generations)]
+            fo = B.run_generations(qf, gens, list(bc) + bt, mapped._opts)
+            rt = {qf.tallies[k].name: t for k, t in zip(qf.out_tallies, fo.tallies)}
+        _tree_records_out(res_out, rt, recs, bad, over, [""])
+    else:
+        _record_outputs(prog, o, res_out, stats)
+    primal = Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
     at = {slot: i for i, slot in enumerate(q.out_tallies)}     # (the launch returns the "sum" tallies only)
     k = nT
     for slot in q.tangent_tallies:
@@ -894,10 +934,12 @@ def _run_tangents(mapped, args, tans, lanes):
             if prog.tallies[slot].kind == "sum" and prog.tallies[slot].name in names:
                 t_tal[l][prog.tallies[slot].name] = o.tallies[at[k]].reshape(prog.tallies[slot].shape)
             k += 1
-    for r, cap, fields in prog.records:        # tangents of the float record fields (canonical, like the primal)
+    for r, cap, fields in (prog.records if not rs else ()):     # tangents of the float record fields (canonical)
         for l in range(lanes):
             t_tal[l][r] = {f: o.records[r][f + ("'" if lanes == 1 else f"'{l}")] for f, dt in fields
                            if dt in (C.F32, C.F64)}
+    if rs:
+        _tree_records_out(t_tal, rt, recs, bad, over, ["'"] if lanes == 1 else [f"'{l}" for l in range(lanes)])
     t_ys = [[None] * ny for _ in range(lanes)]
     m = ny
     for j in q.tangent_ys:

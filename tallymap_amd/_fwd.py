@@ -102,14 +102,17 @@ def _jvp_eqn(e, ins, tins, lanes):
         return _jvp_cond(e, ins, tins, lanes)
     if e.prim == "tallymap_spawn":
         # the child's operands, then `lanes` tangents of each float one (invar-major, as the program's per-item
-        # tangent operands are ordered)
-        extra = []
-        for v, t in zip(e.invars[2:], tins[2:]):
+        # tangent operands are ordered), then the recording forward's own columns (parent, ordinal: `extra`)
+        nx = int(e.params.get("extra", 0))
+        child = e.invars[2:len(e.invars) - nx]
+        tan = []
+        for v, t in zip(child, tins[2:2 + len(child)]):
             if _isf(v.aval):
-                extra += [_fit(t[l], v.aval) if t is not None else _zero(v.aval) for l in range(lanes)]
+                tan += [_fit(t[l], v.aval) if t is not None else _zero(v.aval) for l in range(lanes)]
+        ops = list(ins[:2 + len(child)]) + tan + list(ins[2 + len(child):])
         vs = [x.var if C.is_traced(x) else C.Lit(np.asarray(x), C.AVal(np.shape(x), np.asarray(x).dtype))
-              for x in list(ins) + extra]
-        return C.bind("tallymap_spawn", vs, [e.outvars[0].aval]), [None]
+              for x in ops]
+        return C.bind("tallymap_spawn", vs, [e.outvars[0].aval], **e.params), [None]
     outs = A._replay(e, ins)
     if e.prim in ("tallymap_emit", "tallymap_put"):
         tt, tv = tins[0], tins[2]
@@ -324,7 +327,7 @@ def jvp_program(prog, pert_pi, pert_bc, lanes=1):
             tl.append(dataclasses.replace(s, name=s.name + ("'" if lanes == 1 else f"'{l}")))
     check_tallies(out_jx, len(tl), prog.where)
     q = ItemProgram(out_jx, tuple(tl), nP + npt, nB + len(t_b), prog.trunc, f"{prog.tag}+jvp{lanes}", prog.where,
-                    prog.records, prog.counts, prog.spawn)
+                    prog.records, prog.counts, prog.spawn, prog.spawn_mode, prog.qcount)
     q.tangent_tallies = tf
     q.tangent_ys = yt
     q.lanes = lanes

@@ -238,7 +238,7 @@ class Tally:
         if mode == "record":
             # the recording forward: the child also stores its parent (the item index) and its ordinal k
             kv = k.var if C.is_traced(k) else C.literal(int(k), C.I32, weak=False)
-            new = C.bind("tallymap_spawn", [tok.var, wv] + vs + [ref.var, kv], [tok.aval])[0]
+            new = C.bind("tallymap_spawn", [tok.var, wv] + vs + [ref.var, kv], [tok.aval], extra=2)[0]
             a = dict(self._a)
             a[QKEY] = new
             return Tally(a, self._shapes, {**self._r, QKEY: (k + wi, ref)}, self._ri)

@@ -598,3 +598,27 @@ def test_spawn_operand_kinds_and_divergent_spawns():
     assert np.array_equal(_np(res.outputs["b"]).astype(np.int64), want["b"])
     assert np.array_equal(_np(res.outputs["u"]).astype(np.int64), want["u"])
     assert np.array_equal(_np(res.outputs["v"]), want["v"].astype(f32))     # (the exact sum, rounded once)
+
+
+def test_spawn_records_jvp_closed_form():
+    """forward mode through the Records of a spawning call: along v, the tangent of node m's record x is its root's
+    v times its factor (1, 1/2, 1/4, ...: exact), so the tangent records are the primal's enumeration with v in
+    place of x, bitwise; the tangent of the exact Sum likewise."""
+    print("case: spawn + records jvp", flush=True)
+    n = 3000
+    g0, xs = _cascade_inputs(n)
+    v = np.random.default_rng(7).uniform(-1.0, 1.0, n).astype(f32)
+    f = tm.vmap(_rcascade, outputs={"Q": tm.Sum((NB,), fixed_point=True),
+                                    "r": tm.Records({"g": np.int32, "x": np.float32}, capacity=1 << 15)},
+                spawn=tm.Queue(1 << 14))
+    res, tan = tm.jvp(f, (g0, xs), (None, v))
+    _sync()
+    gen, x, root, fac = _tree_nodes(xs)
+    keep = x > THR
+    m = int(keep.sum())
+    tv = (v[root].astype(np.float64) * fac).astype(f32)
+    assert np.array_equal(_np(res.outputs["r"]["x"])[:m].view(np.uint32), x[keep].view(np.uint32))
+    assert np.array_equal(_np(tan.outputs["r"]["x"])[:m].view(np.uint32), tv[keep].view(np.uint32))
+    assert not _np(tan.outputs["r"]["x"])[m:].any() and "g" not in tan.outputs["r"]
+    want = [float(sum(Fraction(float(t)) for t in tv[gen == g])) for g in range(NB)]
+    assert np.array_equal(_np(tan.outputs["Q"]).view(np.uint32), np.array(want, f32).view(np.uint32))
