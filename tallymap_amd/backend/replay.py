@@ -18,8 +18,10 @@ transposes after it) whose primal outputs a counting lane keeps and whose cotang
 a wave whose live lanes all count runs the plain step instead.  An item with K > TAPE steps takes the two-level
 checkpointed sweep inside its lane (checkpoints every ceil(K / H) steps in the tape's first half H, each segment's
 states in the second half, re-run from the checkpoint in pieces when longer than it).  The tape is the lane's
-region of one buffer of launched lanes x TAPE x state words (u32 columns: word w of slot k of lane l at
-(k * W + w) * lanes + l, so a wave's stores and loads are coalesced); nothing in it outlives the launch.
+region of one buffer of launched lanes x TAPE x Wp u32 words, lane-major (word w of slot k of lane l at
+(l * TAPE + k) * Wp + w; Wp = the state's words padded to a multiple of 4): under step refill a wave's lanes are at
+different steps, so each lane's state is kept contiguous and its consecutive steps in consecutive 16-byte units;
+nothing in it outlives the launch.
 """
 import numpy as np
 
@@ -130,6 +132,7 @@ def build(adj, block=K.BLOCK, tape=TAPE, chunk=K.CHUNK, refill=REFILL):
                 for j, nm in enumerate(names)]
     st = [(n, car_avals[j].dtype) for j, nm in enumerate(car_names) if nm is not None for n in nm]
     W = sum(_nwords(dt) for _, dt in st)
+    Wp = W if W <= 2 else -(-W // 4) * 4      # (a lane's tape slot: whole 16-byte units)
     lam = {j: [declare(np.float32, f"tm_l{j}_{e}") for e in range(len(car_names[j]))]
            for j in range(len(car_names)) if car_names[j] is not None and car_act[j]}
     gq = [q for q in range(nbc) if f_ctin[q]]
@@ -146,9 +149,12 @@ def build(adj, block=K.BLOCK, tape=TAPE, chunk=K.CHUNK, refill=REFILL):
     cc_vals = [const_val(r) for r in sp.cconst]
     bc_vals = [const_val(r) for r in sp.bconst]
 
-    # ---- tape access: word w of slot k at (k * W + w) * tm_nl + tm_lg
+    # ---- tape access: lane-major, word w of slot k of lane l at (l * tape + k) * Wp + w.  Step refill puts a
+    # wave's lanes at different steps, so a slot-major layout (word w of slot k of every lane side by side) made
+    # each 4-byte access its own line; here a lane's state is Wp contiguous words (W padded to a multiple of 4:
+    # whole 16-byte units) and its consecutive steps fill consecutive ones, which L2 combines into whole lines.
     def tape_addr(slot, w):
-        return f"tm_tape[((u64)({slot}) * {W}u + {w}u) * tm_nl + tm_lg]"
+        return f"tm_tape[(tm_lg * {tape}ull + (u64)({slot})) * {Wp}u + {w}u]"
 
     def tape_store(slot, names_dts, ind):
         w = 0
@@ -237,7 +243,7 @@ def build(adj, block=K.BLOCK, tape=TAPE, chunk=K.CHUNK, refill=REFILL):
     from . import compile as Cm
     R = n_in + len(res) + 1
     r_tape = n_in + len(res)
-    res.append(((tape * W,), np.dtype(np.uint32), "tape"))
+    res.append(((tape * Wp,), np.dtype(np.uint32), "tape"))
     src = [Cm.prelude(), f"struct TmParams {{ void* p[{R}]; }};",
            f"#define TM_STATS ((i32*)P.p[{r_stats}])", f"#define TM_CTL ((u32*)P.p[{r_ctl}])"]
     zero_words = []
