@@ -69,7 +69,8 @@ def _cfg_runs(name, n, dev_inputs):
     import tallymap_amd as tm
     from tallymap_amd import configs
     cfg = configs.SIZED[name](n) if name in configs.SIZED else configs.CONFIGS[name]
-    f = tm.vmap(cfg["item"], outputs=cfg["outputs"], in_axes=cfg["in_axes"], max_steps=cfg["max_steps"])
+    f = tm.vmap(cfg["item"], outputs=cfg["outputs"], in_axes=cfg["in_axes"], max_steps=cfg["max_steps"],
+                **cfg.get("opts", {}))
     argn = {"c1": 2, "c3": 1, "c4": 3}
     if name in argn:
         g = tm.grad(f, argnums=argn[name])

@@ -318,7 +318,8 @@ def prebuild(entries, n=64):
             pl = R.plan(adj)
             if any(pl.car_act):
                 from . import replay as RP
-                src, _ = RP.build(adj, block=K.BLOCK, tape=RP.TAPE)
+                src, _ = RP.build(adj, block=K.BLOCK, tape=RP.TAPE,
+                                  refill=int(cfg.get("opts", {}).get("rev_refill", RP.REFILL)))
             else:
                 src, _ = K.build(R.forward_only_program(adj, pl), block=K.BLOCK, schedule="step", refill=1)
             Cm.code_object(src, name=f"tm_{adj.tag}.hip", store_pkg=True)

@@ -127,7 +127,10 @@ def c3_item(t, key, mu_a):
     return t, k
 
 
-C3 = dict(item=c3_item, outputs={"absorbed": Sum((C3_NB, C3_NB))}, in_axes=(0, None), max_steps=1024)
+# (opts: the replay gradient's refill -- photon histories of very different lengths, so a wave takes new items as
+# soon as 8 of its lanes are free)
+C3 = dict(item=c3_item, outputs={"absorbed": Sum((C3_NB, C3_NB))}, in_axes=(0, None), max_steps=1024,
+          opts={"rev_refill": 8})
 
 
 def c3_inputs(n=4_194_304, seed=0):
@@ -237,7 +240,10 @@ def c5_item(t, th0, om0, item_id, A):
 
 
 def c5_config(n):
-    return dict(item=c5_item, outputs={"state": Sum((n, 2))}, in_axes=(0, 0, 0, None), max_steps=20_000)
+    # (opts: every pendulum integrates the same interval, so its step count falls in a narrow band: the replay
+    # gradient refills a wave only when all 64 lanes are free, keeping counting and reversing lanes apart)
+    return dict(item=c5_item, outputs={"state": Sum((n, 2))}, in_axes=(0, 0, 0, None), max_steps=20_000,
+                opts={"rev_refill": 64})
 
 
 C5 = c5_config(1_048_576)
