@@ -505,8 +505,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                        a.shape, a.dtype)
         return Val([f"(({'const ' + ct}*)P.p[{i}])[tm_item * {n} + {e}]" for e in range(n)], a.shape, a.dtype)
 
-    decls, pre_lines, step_lines, post_lines = [], [], [], []
-    ys_write = []
+    decls, pre_lines, step_lines = [], [], []
 
     def write_ys(vals, trunc_idx):
         lines = []
