@@ -669,20 +669,39 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
 
 
 # ----------------------------------------------------------------------------------------- reverse mode
-def _float_args(prog, axes, argnums):
-    """map positional argnums to (per-item operand indices, broadcast operand indices) (leaves of float32)."""
-    pi_idx, bc_idx = [], []
+def _arg_leaves(prog, args, axes, argnums):
+    """the operand leaves of the positional arguments in argnums -> ({pos: (in_axis, operand indices of its leaves,
+    treedef, leaf shapes)}, wrt = (float32 per-item operand indices, float32 broadcast operand indices))."""
+    pav, bav = prog.p_avals(), prog.b_avals()
+    spec, wp, wb = {}, [], []
     p = b = 0
     for pos, x in enumerate(axes):
+        leaves, td = flatten(args[pos])
+        base = p if x == 0 else b
+        idx = list(range(base, base + len(leaves)))
+        if pos in argnums:
+            spec[pos] = (x, idx, td, [_shape(v) for v in leaves])
+            for i in idx:
+                if (pav if x == 0 else bav)[i].dtype == C.F32:
+                    (wp if x == 0 else wb).append(i)
         if x == 0:
-            if pos in argnums:
-                pi_idx.append(p)
-            p += 1
+            p += len(leaves)
         else:
-            if pos in argnums:
-                bc_idx.append(b)
-            b += 1
-    return tuple(pi_idx), tuple(bc_idx)
+            b += len(leaves)
+    return spec, (tuple(wp), tuple(wb))
+
+
+def _arg_cotangents(spec, wrt, g_pi, g_bc):
+    """the cotangents of the arguments in spec, each with its argument's structure (None for a leaf that is not
+    float32), in positional order; one argument alone is returned bare."""
+    gp, gb = dict(zip(wrt[0], g_pi)), dict(zip(wrt[1], g_bc))
+    out = []
+    for pos in sorted(spec):
+        x, idx, td, shapes = spec[pos]
+        src = gp if x == 0 else gb
+        leaves = [src.get(i) if x == 0 else (src[i].reshape(sh) if i in src else None) for i, sh in zip(idx, shapes)]
+        out.append(unflatten(td, leaves) if td is not None else leaves[0])
+    return tuple(out) if len(out) != 1 else out[0]
 
 
 def _argnums(argnums, nargs):
@@ -718,7 +737,7 @@ def _pullback(mapped, args, argnums):
         for j, (r, cap, _) in enumerate(prog.records):
             extra.append(B.util.exclusive_scan(o.ys[prog.counts[j]]).clamp(max=cap).to(torch.int32))
             bad = bad or bool((o.rcount[j] > cap).item())     # (an output past its capacity: NaN, as the forward)
-    wrt = _float_args(vprog, axes, an)
+    spec, wrt = _arg_leaves(vprog, args, axes, an)
 
     def pullback(ct_outputs=None, ct_per_item=None):
         cts = {}
@@ -741,19 +760,7 @@ def _pullback(mapped, args, argnums):
         if bad:
             g_pi = [x.float().fill_(float("nan")) for x in g_pi]
             g_bc = [x.float().fill_(float("nan")) for x in g_bc]
-        out = []
-        gp, gb = iter(g_pi), iter(g_bc)
-        p = b = 0
-        for pos, x in enumerate(axes):
-            if pos in an:
-                if x == 0:
-                    out.append(next(gp) if p in wrt[0] else None)
-                else:
-                    g = next(gb) if b in wrt[1] else None
-                    out.append(g.reshape(np.shape(args[pos])) if g is not None else None)
-            p += x == 0
-            b += x is None
-        return tuple(out) if len(out) != 1 else out[0]
+        return _arg_cotangents(spec, wrt, g_pi, g_bc)
     return pullback
 
 
@@ -773,12 +780,12 @@ def _tree_pullback(mapped, args, argnums):
     rprog, meta, pi, bc, N, axes = mapped._prepare(args, "record")
     aprog = mapped._prepare(args, "adjoint")[0]
     an = _argnums(argnums, len(args))
-    want = _float_args(rprog, axes, an)
+    spec, want = _arg_leaves(rprog, args, axes, an)
     pav = rprog.p_avals()
     fpi = tuple(j for j, a in enumerate(pav) if a.dtype in (C.F32, C.F64))
     if any(pav[j].dtype == C.F64 for j in fpi):
         raise UnsupportedError("tallymap: reverse mode through spawn with float64 per-item operands")
-    wrt = (fpi, want[1])
+    wrt = (fpi, want[1])        # (every float per-item operand: the children's cotangents flow through them)
     o = B.run(rprog, pi, bc, N, mapped._opts)
     gens = o.generations
     Q = int(rprog.spawn)
@@ -831,19 +838,8 @@ def _tree_pullback(mapped, args, argnums):
         if nan:
             g_root = [torch.full_like(x, float("nan")) for x in g_root]
             g_bc = [torch.full_like(x, float("nan")) for x in g_bc]
-        out = []
-        gp, gb = dict(zip(fpi, g_root)), iter(g_bc)
-        p = b = 0
-        for pos, x in enumerate(axes):
-            if pos in an:
-                if x == 0:
-                    out.append(gp.get(p) if p in want[0] else None)
-                else:
-                    g = next(gb) if b in want[1] else None
-                    out.append(g.reshape(np.shape(args[pos])) if g is not None else None)
-            p += x == 0
-            b += x is None
-        return tuple(out) if len(out) != 1 else out[0]
+        gr = dict(zip(fpi, g_root))
+        return _arg_cotangents(spec, want, [gr[i] for i in want[0]], g_bc)
     return pullback
 
 
