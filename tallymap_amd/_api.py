@@ -869,6 +869,18 @@ def _jvp_prog(prog, pp, pb, lanes):
     return q
 
 
+def _match_leaves(prim, tan):
+    """the leaves of the tangent pytree `tan` aligned with the leaves of `prim` (a None subtree of tan stands for
+    zeros: one None per leaf of prim's subtree)."""
+    if tan is None:
+        return [None] * len(flatten(prim)[0])
+    if isinstance(prim, dict):
+        return [v for k in sorted(prim) for v in _match_leaves(prim[k], tan.get(k))]
+    if isinstance(prim, (list, tuple)):
+        return [v for p, t in zip(prim, tan) for v in _match_leaves(p, t)]
+    return [tan]
+
+
 def _run_tangents(mapped, args, tans, lanes):
     """one launch of the jvp program with `lanes` directions.  tans[pos]: None or a list of `lanes` tangent arrays
     for positional argument pos (its shape) -> (primal Result, per lane {name: tangent tally}, per lane [tangents
@@ -895,8 +907,11 @@ def _run_tangents(mapped, args, tans, lanes):
                 pt += [z] * lanes
             elif on:
                 for t in tl:
-                    tleaves, _ = flatten(t)
-                    (pt if x == 0 else bt).append(tleaves[j])
+                    tv = _match_leaves(args[pos], t)[j]
+                    if tv is None:                 # (a None subtree of the tangent: zero)
+                        import torch
+                        tv = torch.zeros(_shape(leaf), dtype=B.torch_dtype(dt), device="cuda")
+                    (pt if x == 0 else bt).append(tv)
     q = _jvp_prog(prog, tuple(pp), tuple(pb), lanes)
     o = B.run(q, list(pi) + pt, list(bc) + bt, N, mapped._opts)
     names = mapped._names

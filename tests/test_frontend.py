@@ -235,3 +235,12 @@ def test_spawn_tracing_and_errors():
         tm.vmap(item, outputs={"h": tm.Sum((2,))}, spawn=100)
     with pytest.raises(ValueError, match="capacity"):
         tm.Queue(0)
+
+
+def test_tangent_leaves_align_with_primal_leaves():
+    """a tangent pytree with None subtrees lines up with the primal's leaves (None per leaf of the subtree)."""
+    from tallymap_amd._api import _match_leaves
+    prim = dict(a=np.ones(3), b=(np.ones(2), np.ones(4)), c=np.ones(1))
+    t = dict(a=None, b=(None, "B1"), c="C")
+    assert _match_leaves(prim, t) == [None, None, "B1", "C"]
+    assert _match_leaves(prim, None) == [None] * 4
