@@ -74,13 +74,23 @@ class Records:
             fields, capacity = capacity, fields
         if not isinstance(fields, dict) or not fields:
             raise TypeError("tallymap: Records(fields, capacity): fields is a non-empty {name: dtype} dict")
+        fl = {str(k): np.dtype(v) for k, v in fields.items()}
+        for k, dt in fl.items():
+            if dt == np.bool_:
+                raise TypeError(f"tallymap: Records field {k!r} of dtype bool: use an integer dtype (0 / 1)")
         if capacity is None:
             raise ValueError("tallymap: Records needs a capacity on this backend")
         capacity = int(capacity)
         if not 0 < capacity <= MAX_ITEMS:
             raise ValueError(f"tallymap: Records capacity must be in [1, 2^31 - 1], got {capacity}")
-        self.fields = {str(k): np.dtype(v) for k, v in fields.items()}
+        self.fields = fl
         self.capacity = capacity
+
+    def __eq__(self, o):
+        return isinstance(o, Records) and o.fields == self.fields and o.capacity == self.capacity
+
+    def __hash__(self):
+        return hash((tuple(self.fields.items()), self.capacity))
 
     def __repr__(self):
         return f"Records({ {k: v.name for k, v in self.fields.items()} }, capacity={self.capacity})"

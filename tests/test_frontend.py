@@ -174,7 +174,9 @@ def test_records_tracing_and_errors():
         _prog(lambda t, x: t.add("r", 0, 1), out, [((), np.float32)], [], (0,))
     with pytest.raises(ValueError, match="capacity"):
         tm.Records({"i": np.int32})
-    assert tm.Records(16, {"i": np.int32}).capacity == 16
+    assert tm.Records(16, {"i": np.int32}) == tm.Records({"i": np.int32}, capacity=16)     # (records.py:461)
+    with pytest.raises(TypeError, match="integer"):
+        tm.Records({"b": bool}, capacity=4)
 
 
 def test_spawn_tracing_and_errors():
