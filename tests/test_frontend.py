@@ -246,3 +246,20 @@ def test_tangent_leaves_align_with_primal_leaves():
     t = dict(a=None, b=(None, "B1"), c="C")
     assert _match_leaves(prim, t) == [None, None, "B1", "C"]
     assert _match_leaves(prim, None) == [None] * 4
+
+
+def test_argument_leaves_and_cotangent_structure():
+    """reverse mode maps each positional argument to its operand leaves (float32 ones differentiated) and returns
+    a cotangent with the argument's structure, None for the other leaves."""
+    from tallymap_amd._api import _arg_cotangents, _arg_leaves
+
+    def item(t, p, w):
+        return t.add("h", 0, p["x"] * w[0] + p["y"][0])
+    p = dict(x=np.ones(8, np.float32), k=np.zeros(8, np.int32), y=np.ones((8, 2), np.float32))
+    w = np.ones(3, np.float32)
+    f = tm.vmap(item, outputs={"h": tm.Sum((1,))}, in_axes=(0, None))
+    prog = f._prepare((p, w))[0]
+    spec, wrt = _arg_leaves(prog, (p, w), (0, None), (0, 1))
+    assert wrt == ((1, 2), (0,))                  # leaves sorted by key: k (int32), x, y; then w
+    g = _arg_cotangents(spec, wrt, ["gx", "gy"], [np.arange(3.0)])
+    assert g[0] == {"k": None, "x": "gx", "y": "gy"} and g[1].shape == (3,)
