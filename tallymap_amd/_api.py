@@ -65,7 +65,9 @@ class Records:
     sum of the per-item counts); slots past the last record are zero.  Result.stats['appended'][name] is the number
     of records (exact also beyond the capacity) and stats['records_dropped'][name] the number that did not fit.  A
     call in which any Records output receives more than its capacity (or any item is truncated) makes every float
-    output of the call NaN (records and sums) and every integer record field -1.  Fields are scalars of float32, float64, int32, uint32, int64 or
+    output of the call NaN (records and sums) and every integer record field -1.  Without a capacity, each call
+    first runs a count pass and sizes the output to the next power of two at or above its record count (reference
+    _api.py:838-852).  Fields are scalars of float32, float64, int32, uint32, int64 or
     uint64; float fields carry tangents (jvp, jacfwd).  One pass: each append claims a raw slot with one atomic and
     the same launch moves the records to the canonical slots (reference _records.py)."""
 
@@ -78,11 +80,10 @@ class Records:
         for k, dt in fl.items():
             if dt == np.bool_:
                 raise TypeError(f"tallymap: Records field {k!r} of dtype bool: use an integer dtype (0 / 1)")
-        if capacity is None:
-            raise ValueError("tallymap: Records needs a capacity on this backend")
-        capacity = int(capacity)
-        if not 0 < capacity <= MAX_ITEMS:
-            raise ValueError(f"tallymap: Records capacity must be in [1, 2^31 - 1], got {capacity}")
+        if capacity is not None:
+            capacity = int(capacity)
+            if not 0 < capacity <= MAX_ITEMS:
+                raise ValueError(f"tallymap: Records capacity must be in [1, 2^31 - 1], got {capacity}")
         self.fields = fl
         self.capacity = capacity
 
@@ -327,8 +328,8 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
     tspecs = []
     recs = []
     # how appends run: one pass (claimed raw slots), only counted, or emitted at canonical offsets (operands)
-    rmode = ({None: None, "record": "count" if spawn is not None else None, "adjoint": "adjoint", "fill": "fill"}
-             [spawn_mode])
+    rmode = ({None: None, "record": "count" if spawn is not None else None, "adjoint": "adjoint", "fill": "fill",
+              "count": "count"}[spawn_mode])
     for n in sorted(outs_spec):
         s = outs_spec[n]
         if RSEP in n:
@@ -365,7 +366,7 @@ def build_program(fn, outs_spec, axes, pav, bav, max_steps, ptree=None, btree=No
         if int(np.prod(shape, dtype=np.int64)) > MAX_ITEMS:
             raise ValueError(f"tallymap: output {n!r} has more than 2^31 - 1 cells")
         tspecs.append(TSpec(n, shape, dt, exact, fixed=fixed, scale=scale,
-                            kind="discard" if spawn_mode == "fill" else "sum"))
+                            kind="discard" if spawn_mode in ("fill", "count") else "sum"))
     if spawn is not None:
         tspecs.append(TSpec(QKEY, (1,), C.I32, kind="discard"))    # the spawn token (orders t.spawn like an emit)
         nf = sum(a.size for a in pav if a.dtype in (C.F32, C.F64))
@@ -671,11 +672,48 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
         per_item = unflatten(meta["ytree"], ys)
         return Result(res_out, per_item, trunc, stats)
 
-    mapped.__wrapped__ = fn
-    mapped._prepare = prepare
-    mapped._opts = opts
-    mapped._names = names
-    return mapped
+    # Records outputs without a capacity: each call runs a count pass first and then the call sized by it
+    dyn = [n for n in names if isinstance(outs_spec[n], Records) and outs_spec[n].capacity is None]
+    sized_cache = {}
+
+    def sized(args):
+        """the mapped function with every Records capacity fixed for this call's arguments (itself when all are
+        given): the capacity-less ones sized by a count pass to the next power of two >= their record count."""
+        if not dyn:
+            return mapped
+        if spawn is not None:
+            raise ValueError("tallymap: Records outputs of a spawning call need a capacity")
+        from . import backend as B
+        prog, _, pi, bc, N, _ = prepare(args, "count")
+        o = B.run(prog, pi, bc, N, opts)
+        rnames = [n for n in names if isinstance(outs_spec[n], Records)]
+        caps = {}
+        for j, r in enumerate(rnames):
+            if r in dyn:
+                tot = int(o.ys[prog.counts[j]].long().sum().item())
+                c = 1 << max(0, (tot - 1).bit_length())
+                if c > MAX_ITEMS:
+                    raise ValueError(f"tallymap: Records output {r!r} has no capacity and its call appended {tot} "
+                                     "records: more than the largest capacity (2^30 as a power of two): split the call")
+                caps[r] = c
+        key = tuple(sorted(caps.items()))
+        f = sized_cache.get(key)
+        if f is None:
+            spec = {n: (Records(outs_spec[n].fields, caps[n]) if n in caps else outs_spec[n]) for n in names}
+            f = sized_cache[key] = vmap(fn, outputs=spec, in_axes=in_axes, max_steps=max_steps, spawn=spawn,
+                                        backend=backend, **opts)
+        return f
+
+    def entry(*args):
+        return sized(args)(*args) if dyn else mapped(*args)
+
+    for g in (mapped, entry):
+        g.__wrapped__ = fn
+        g._prepare = prepare
+        g._opts = opts
+        g._names = names
+        g._sized = sized if dyn else (lambda args: mapped)
+    return entry
 
 
 # ----------------------------------------------------------------------------------------- reverse mode
@@ -732,6 +770,7 @@ def vjp(mapped, *args, argnums=None):
 def _pullback(mapped, args, argnums):
     from . import backend as B
     from ._tally import RSEP
+    mapped = mapped._sized(args)
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     if prog.spawn is not None:
         return _tree_pullback(mapped, args, argnums)
@@ -896,6 +935,7 @@ def _run_tangents(mapped, args, tans, lanes):
     for positional argument pos (its shape) -> (primal Result, per lane {name: tangent tally}, per lane [tangents
     of the float per-item results (None for the others)])."""
     from . import backend as B
+    mapped = mapped._sized(args)
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     recs = list(prog.records)
     rs = bool(recs) and prog.spawn is not None
@@ -990,7 +1030,8 @@ def jacfwd(mapped, argnums=0):
     an = (argnums,) if isinstance(argnums, int) else tuple(argnums)
 
     def jac(*args):
-        prog, meta, pi, bc, N, axes = mapped._prepare(args)
+        m = mapped._sized(args)
+        prog, meta, pi, bc, N, axes = m._prepare(args)
         dirs = []
         for a in an:
             if axes[a] == 0:
@@ -1003,16 +1044,16 @@ def jacfwd(mapped, argnums=0):
                 e = np.zeros(x.size, x.dtype)
                 e[i] = 1
                 dirs.append((a, e.reshape(x.shape)))
-        cols = {n: [] for n in mapped._names}
+        cols = {n: [] for n in m._names}
         for s in range(0, len(dirs), MAX_LANES):
             chunk = dirs[s:s + MAX_LANES]
             tans = [None] * len(args)
             for a in an:
                 lanes = [d if aa == a else np.zeros_like(np.asarray(args[a])) for aa, d in chunk]
                 tans[a] = lanes
-            _, t_tal, _, _ = _run_tangents(mapped, args, tans, len(chunk))
+            _, t_tal, _, _ = _run_tangents(m, args, tans, len(chunk))
             for l in range(len(chunk)):
-                for n in mapped._names:
+                for n in m._names:
                     if n in t_tal[l]:
                         cols[n].append(t_tal[l][n])
         out = {}

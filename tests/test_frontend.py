@@ -173,7 +173,11 @@ def test_records_tracing_and_errors():
     with pytest.raises(KeyError, match="Records output"):
         _prog(lambda t, x: t.add("r", 0, 1), out, [((), np.float32)], [], (0,))
     with pytest.raises(ValueError, match="capacity"):
-        tm.Records({"i": np.int32})
+        tm.Records({"i": np.int32}, capacity=0)
+    # without a capacity: the count program (appends only counted, Sums discarded, a count per Records output)
+    fc = tm.vmap(item, outputs={"r": tm.Records({"i": np.int32, "v": np.float32}), "h": tm.Sum((2,))}, in_axes=(0,))
+    c = fc._prepare((np.ones(4, np.float32),), "count")[0]
+    assert c.records == () and len(c.counts) == 1 and [s.kind for s in c.tallies] == ["discard"]
     assert tm.Records(16, {"i": np.int32}) == tm.Records({"i": np.int32}, capacity=16)     # (records.py:461)
     with pytest.raises(TypeError, match="integer"):
         tm.Records({"b": bool}, capacity=4)

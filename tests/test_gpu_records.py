@@ -193,3 +193,26 @@ def test_records_reverse_mode_overflow_is_nan():
     f = tm.vmap(_walker, outputs=_outputs(1000, 1 << 13), in_axes=(0, 0, None), max_steps=100)
     _, pull = tm.vjp(f, xs, keys, theta, argnums=2)
     assert np.isnan(_np(pull({"steps": {"w": 1.0}}))).all()
+
+
+def test_records_without_capacity_sized_by_count_pass():
+    """Records without a capacity: a count pass sizes each output to the next power of two at or above its record
+    count (reference _api.py:838-852); the records equal the explicit-capacity call's bitwise, and reverse mode
+    sizes the same way."""
+    print("case: records without capacity", flush=True)
+    xs, keys, theta = configs.c1_inputs(1 << 14)
+    outs = {"steps": tm.Records({"bin": np.int32, "w": np.float32}),
+            "ends": tm.Records({"k": np.int32, "x": np.float32}), "hist": tm.Sum((2,))}
+    f = tm.vmap(_walker, outputs=outs, in_axes=(0, 0, None), max_steps=100)
+    res = f(xs, keys, theta)
+    ref = tm.vmap(_walker, outputs=_outputs(1 << 18, 1 << 15), in_axes=(0, 0, None), max_steps=100)(xs, keys, theta)
+    _sync()
+    n = int(_np(ref.stats["appended"]["steps"]))
+    cap = 1 << (n - 1).bit_length()
+    assert _np(res.outputs["steps"]["w"]).shape == (cap,) and _np(res.outputs["ends"]["x"]).shape == (1 << 14,)
+    assert np.array_equal(_np(res.outputs["steps"]["w"])[:n].view(np.uint32),
+                          _np(ref.outputs["steps"]["w"])[:n].view(np.uint32))
+    assert int(_np(res.stats["records_dropped"]["steps"])) == 0
+    g = float(_np(tm.grad(f, weights={"steps": {"w": 1.0}}, argnums=2)(xs, keys, theta)))
+    w = _np(ref.outputs["steps"]["w"]).astype(np.float64)[:n]
+    assert abs(g - w.sum() / 2.0) <= 1e-5 * w.sum() / 2.0
