@@ -597,6 +597,8 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
     max_steps: cap on every top-level while loop; an item that hits it is flagged in Result.truncated and makes
                every float tally of the call NaN
     spawn:     tallymap_amd.Queue(capacity) to allow t.spawn(child) (forward calls; run generation by generation)
+    The returned function also takes n_active=n: only items i < n run (a fixed capacity N with a varying active
+    count, reference _api.py:469-472); the others emit nothing, are never truncated and get zero per-item results.
     backend:   'auto' / 'hip' (the HIP kernel backend; it never falls back)
     opts:      schedule 'step' (default: a lane refills at loop-step granularity) | 'item'; block (threads per
                block, default 256); refill (idle lanes a wave waits for before it claims, default 1); compact
@@ -656,12 +658,14 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
                 _PROGS.popitem(last=False)
         return prog, meta, pi, bc, N, axes
 
-    def mapped(*args):
+    def mapped(*args, n_active=None):
         from . import backend as B
         prog, meta, pi, bc, N, _ = prepare(args)
         if prog.records and prog.spawn is not None:
+            if n_active is not None:
+                raise ValueError("tallymap: n_active with spawn is not supported")
             return _records_spawn(prepare, opts, names, args)
-        o = B.run(prog, pi, bc, N, opts)
+        o = B.run(prog, pi, bc, N, opts, n_active=None if n_active is None else int(n_active))
         res_out = _sum_outputs(prog, o, names)
         stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
         if prog.spawn is not None:
@@ -704,8 +708,8 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
                                         backend=backend, **opts)
         return f
 
-    def entry(*args):
-        return sized(args)(*args) if dyn else mapped(*args)
+    def entry(*args, n_active=None):
+        return (sized(args) if dyn else mapped)(*args, n_active=n_active)
 
     for g in (mapped, entry):
         g.__wrapped__ = fn

@@ -117,9 +117,10 @@ def _alloc(c, N):
     return outs
 
 
-def _queue(c, ins, outs, N, n_zero, flags, stream=None):
+def _queue(c, ins, outs, N, n_zero, flags, stream=None, n_main=None):
     """queue c's kernels over N items on `stream` (default: torch's current one): tm_zero when n_zero, tm_main
-    when N > 0, tm_post when flags & 2, then the auxiliary passes of the layout."""
+    when N > 0 (over the first n_main items when given: n_active), tm_post when flags & 2, then the auxiliary
+    passes of the layout (over all N)."""
     import ctypes
 
     import torch
@@ -127,7 +128,8 @@ def _queue(c, ins, outs, N, n_zero, flags, stream=None):
     bufs = [t.data_ptr() for t in ins] + [t.data_ptr() for t in outs]
     arr = (ctypes.c_void_p * len(bufs))(*bufs)
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
-    Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), n_zero, flags, N, c.block))
+    Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), n_zero, flags,
+                                N if n_main is None else n_main, c.block))
     for name, kind, block, cap in (getattr(L, "aux", None) or []):
         if N == 0 and kind != "cap":         # (no item ran: only the canonical outputs are written, as zeros)
             continue
@@ -136,8 +138,9 @@ def _queue(c, ins, outs, N, n_zero, flags, stream=None):
         Cm.check(Cm.lib().tm_launch_aux(c.id, name.encode(), ctypes.c_void_p(s), arr, len(bufs), N, grid, block))
 
 
-def run(prog, pi, bc, N, opts):
-    """the kernel backend's run(): outputs of prog over N items."""
+def run(prog, pi, bc, N, opts, n_active=None):
+    """the kernel backend's run(): outputs of prog over N items (only the first n_active of them run when given:
+    the others emit nothing, count as nothing and get zero per-item results)."""
     c = compiled(prog, opts)
     ins = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
     ins += [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
@@ -148,8 +151,19 @@ def run(prog, pi, bc, N, opts):
         if tuple(x.shape) != tuple(a.shape):
             raise ValueError(f"tallymap_amd: broadcast operand of shape {tuple(x.shape)}, expected {a.shape}")
     if getattr(prog, "spawn", None) is not None:
+        if n_active is not None:
+            raise ValueError("tallymap: n_active with spawn is not supported")
         return _run_spawn(c, prog, ins, N)
-    res = launch(c, ins, N)
+    if n_active is None:
+        res = launch(c, ins, N)
+    else:
+        n = int(n_active)
+        if not 0 <= n <= N:
+            raise ValueError(f"tallymap: n_active={n} outside [0, N={N}]")
+        res = _alloc(c, N)
+        for r in c.layout.r_ys:                    # (the skipped items' per-item results: zero)
+            res[r - c.layout.n_in][n:].zero_()
+        _queue(c, ins, res, N, c.layout.n_zero, c.layout.flags, n_main=n)
     L = c.layout
     base = L.n_in
     tallies = [res[L.r_out[k] - base] for k in prog.out_tallies]

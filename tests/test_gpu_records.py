@@ -216,3 +216,26 @@ def test_records_without_capacity_sized_by_count_pass():
     g = float(_np(tm.grad(f, weights={"steps": {"w": 1.0}}, argnums=2)(xs, keys, theta)))
     w = _np(ref.outputs["steps"]["w"]).astype(np.float64)[:n]
     assert abs(g - w.sum() / 2.0) <= 1e-5 * w.sum() / 2.0
+
+
+@pytest.mark.parametrize("n", [0, 5, 9_999, 1 << 14])
+def test_n_active_runs_only_the_first_items(n):
+    """n_active = n: the call over 2^14 items equals the call over the first n items (exact Sum bitwise, Records
+    bitwise, per-item results), and the skipped items' per-item results are zero (reference edge.py:617-627)."""
+    print(f"case: n_active={n}", flush=True)
+    xs, keys, theta = configs.c1_inputs(1 << 14)
+    outs = dict(_outputs(1 << 18, 1 << 15), hist=tm.Sum((2,), fixed_point=True))
+    f = tm.vmap(_walker, outputs=outs, in_axes=(0, 0, None), max_steps=100)
+    a = f(xs, keys, theta, n_active=n)
+    _sync()
+    k = _np(a.per_item)
+    assert not k[n:].any() and not _np(a.truncated)[n:].any()
+    if n == 0:
+        assert int(_np(a.stats["appended"]["steps"])) == 0 and not _np(a.outputs["hist"]).any()
+        return
+    b = f(xs[:n], keys[:n], theta)
+    _sync()
+    m = int(_np(b.stats["appended"]["steps"]))
+    assert int(_np(a.stats["appended"]["steps"])) == m and np.array_equal(k[:n], _np(b.per_item))
+    assert np.array_equal(_np(a.outputs["hist"]).view(np.uint32), _np(b.outputs["hist"]).view(np.uint32))
+    assert np.array_equal(_np(a.outputs["steps"]["w"]).view(np.uint32), _np(b.outputs["steps"]["w"]).view(np.uint32))
