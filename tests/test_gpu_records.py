@@ -239,3 +239,22 @@ def test_n_active_runs_only_the_first_items(n):
     assert int(_np(a.stats["appended"]["steps"])) == m and np.array_equal(k[:n], _np(b.per_item))
     assert np.array_equal(_np(a.outputs["hist"]).view(np.uint32), _np(b.outputs["hist"]).view(np.uint32))
     assert np.array_equal(_np(a.outputs["steps"]["w"]).view(np.uint32), _np(b.outputs["steps"]["w"]).view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [0, 1, 257])
+def test_small_and_empty_calls(n):
+    """N = 0, 1 and one not a multiple of the block (reference edge.py:296-307): Sums, Records and per-item results
+    of the right shapes; nothing emitted at N = 0; the same values as a larger call's first n items."""
+    print(f"case: N={n}", flush=True)
+    xs, keys, theta = configs.c1_inputs(512)
+    f = tm.vmap(_walker, outputs=dict(_outputs(1 << 12, 1 << 10), hist=tm.Sum((2,), fixed_point=True)),
+                in_axes=(0, 0, None), max_steps=100)
+    a = f(xs[:n], keys[:n], theta)
+    b = f(xs, keys, theta, n_active=n)
+    _sync()
+    assert _np(a.per_item).shape == (n,) and _np(a.outputs["hist"]).shape == (2,)
+    assert np.array_equal(_np(a.outputs["hist"]).view(np.uint32), _np(b.outputs["hist"]).view(np.uint32))
+    assert np.array_equal(_np(a.outputs["steps"]["w"]).view(np.uint32), _np(b.outputs["steps"]["w"]).view(np.uint32))
+    assert np.array_equal(_np(a.per_item), _np(b.per_item)[:n])
+    if n == 0:
+        assert not _np(a.outputs["hist"]).any() and int(_np(a.stats["appended"]["steps"])) == 0
