@@ -250,6 +250,62 @@ def cond(pred, true_fun, false_fun, *operands):
     return unflatten(otd, outs)
 
 
+SCAN_UNROLL = 256            # lax.scan with stacked inputs or outputs is unrolled up to this many steps
+
+
+def scan(f, init, xs=None, length=None, reverse=False, unroll=1):
+    """lax.scan(f, init, xs, length): (carry, ys).  The item's arrays are small and static, so a scan of up to
+    SCAN_UNROLL steps is unrolled and its ys stacked along a new leading axis, as JAX's scan returns them; a
+    longer one must read no xs and return no ys, and runs as a fori_loop."""
+    xl, xtd = flatten(xs)
+    n = length if length is not None else (_shape0(xl[0]) if xl else None)
+    if n is None:
+        raise C.TraceError("lax.scan: give xs or length")
+    n = int(n)
+    if n > SCAN_UNROLL:
+        if xl:
+            raise C.TraceError(f"lax.scan: {n} steps over xs (unrolled up to {SCAN_UNROLL} steps)")
+
+        def body(i, c):
+            c2, y = f(c, None)
+            if flatten(y)[0]:
+                raise C.TraceError(f"lax.scan: {n} steps returning ys (unrolled up to {SCAN_UNROLL} steps)")
+            return c2
+        return fori_loop(0, n, body, init), None
+    carry, ys = init, []
+    for i in (range(n - 1, -1, -1) if reverse else range(n)):
+        carry, y = f(carry, unflatten(xtd, [v[i] for v in xl]) if xl else None)
+        ys.append(y)
+    if reverse:
+        ys = ys[::-1]
+    yl = [flatten(y)[0] for y in ys]
+    if not ys or not yl[0]:
+        return carry, ys[0] if ys else None
+    from . import numpy as jnp
+    return carry, unflatten(flatten(ys[0])[1], [jnp.stack([y[j] for y in yl]) for j in range(len(yl[0]))])
+
+
+def switch(index, branches, *operands):
+    """lax.switch(index, branches, *operands): branches[clamp(index, 0, len - 1)](*operands), as a chain of conds."""
+    branches = list(branches)
+    if not C.is_traced(index):
+        return branches[min(max(int(index), 0), len(branches) - 1)](*operands)
+    if len(branches) == 1:
+        return branches[0](*operands)
+    from . import numpy as jnp
+    i = jnp.clip(index, 0, len(branches) - 1)
+
+    def pick(k):
+        if k == len(branches) - 1:
+            return branches[k]
+        return lambda *ops: cond(i == k, branches[k], pick(k + 1), *ops)
+    return pick(0)(*operands)
+
+
+def _shape0(x):
+    return x.shape[0] if C.is_traced(x) else np.shape(x)[0]
+
+
 def select(pred, on_true, on_false):
     return C.select(pred, on_true, on_false)
 

@@ -267,3 +267,19 @@ def test_argument_leaves_and_cotangent_structure():
     assert wrt == ((1, 2), (0,))                  # leaves sorted by key: k (int32), x, y; then w
     g = _arg_cotangents(spec, wrt, ["gx", "gy"], [np.arange(3.0)])
     assert g[0] == {"k": None, "x": "gx", "y": "gy"} and g[1].shape == (3,)
+
+
+def test_scan_and_switch_trace():
+    """lax.scan (unrolled, ys stacked; a long scan without ys as a loop) and lax.switch (a chain of conds, the
+    index clamped) trace; a long scan with ys raises."""
+    def item(t, x):
+        c, ys = lax.scan(lambda c, v: (c + v * x, c * 2.0), 0.0, jnp.stack([x, x + 1.0, x + 2.0]))
+        n, _ = lax.scan(lambda c, _: (c + 1, None), 0, length=1000)
+        s = lax.switch((x * 3.0).astype(jnp.int32), [lambda v: v, lambda v: v * 2.0, lambda v: v * 3.0], x)
+        return t.add("h", 0, c + ys[2] + s), n
+    p = _prog(item, {"h": tm.Sum((1,))}, [((), np.float32)], [], (0,))
+    prims = [e.prim for e in C.walk_eqns(p.jaxpr)]
+    assert prims.count("while") == 1 and prims.count("cond") >= 2
+    with pytest.raises(C.TraceError, match="unrolled"):
+        _prog(lambda t, x: (t, lax.scan(lambda c, _: (c, c), x, length=1000)[1]), {"h": tm.Sum((1,))},
+              [((), np.float32)], [], (0,))

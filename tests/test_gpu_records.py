@@ -258,3 +258,30 @@ def test_small_and_empty_calls(n):
     assert np.array_equal(_np(a.per_item), _np(b.per_item)[:n])
     if n == 0:
         assert not _np(a.outputs["hist"]).any() and int(_np(a.stats["appended"]["steps"])) == 0
+
+
+def _scan_switch_item(t, x):
+    c, ys = lax.scan(lambda c, v: (c + v, c * 2.0), 0.0, jnp.stack([x, x + 1.0, x + 2.0]))
+    n, _ = lax.scan(lambda c, _: (c + 1, None), 0, length=1000)
+    s = lax.switch((x * 3.0).astype(jnp.int32), [lambda v: v, lambda v: v * 2.0, lambda v: v * 3.0], x)
+    return t.add("h", 0, c + ys[2] + s), (n, s)
+
+
+def test_scan_and_switch_items():
+    """an item with an unrolled scan (ys stacked), a 1000-step scan run as a loop and a switch: per-item results
+    and the exact tally against a float32 numpy restatement of the same arithmetic, bitwise."""
+    print("case: scan and switch", flush=True)
+    x = np.random.default_rng(2).uniform(0, 1, 10_000).astype(f32)
+    res = tm.vmap(_scan_switch_item, outputs={"h": tm.Sum((1,), fixed_point=True)}, in_axes=(0,))(x)
+    _sync()
+    c0 = (f32(0.0) + x).astype(f32)
+    c1 = (c0 + (x + f32(1.0))).astype(f32)
+    c = (c1 + (x + f32(2.0))).astype(f32)
+    ys2 = (c1 * f32(2.0)).astype(f32)
+    k = np.clip((x * f32(3.0)).astype(np.int32), 0, 2)
+    s = np.choose(k, [x, (x * f32(2.0)).astype(f32), (x * f32(3.0)).astype(f32)]).astype(f32)
+    n, sg = res.per_item
+    assert (_np(n) == 1000).all() and np.array_equal(_np(sg).view(np.uint32), s.view(np.uint32))
+    from oracle import exact as X
+    v = ((c + ys2).astype(f32) + s).astype(f32)
+    assert _np(res.outputs["h"])[0].view(np.uint32) == X.exact_sum(v)[0].view(np.uint32)
