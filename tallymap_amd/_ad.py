@@ -428,9 +428,19 @@ def r_concatenate(g, ins, outs, e):
     return res
 
 
+def r_dynamic_index(g, ins, outs, e):
+    """the transpose of x[i] (i clamped): g in row i of a zero array (one select per row); no cotangent for i."""
+    x, i = ins
+    from . import numpy as jnp
+    rest = tuple(x.shape[1:])
+    z = np.zeros(rest, g[0].dtype)
+    return [C.stack([jnp.where(i == r, g[0], z) for r in range(x.shape[0])]), None]
+
+
 RULES = {"add": r_add, "sub": r_sub, "mul": r_mul, "div": r_div, "neg": r_neg, "max": r_max, "min": r_min,
          "abs": r_abs, "sqrt": r_sqrt, "rsqrt": r_rsqrt, "exp": r_exp, "log": r_log, "log1p": r_log1p,
          "expm1": r_expm1, "sin": r_sin, "cos": r_cos, "tanh": r_tanh, "logistic": r_logistic, "atan2": r_atan2,
          "pow": r_pow, "integer_pow": r_integer_pow, "erf_inv": r_erf_inv, "select_n": r_select,
          "convert_element_type": r_convert, "copy": r_copy, "slice": r_slice, "squeeze": r_reshape,
-         "reshape": r_reshape, "broadcast_in_dim": r_broadcast, "concatenate": r_concatenate}
+         "reshape": r_reshape, "broadcast_in_dim": r_broadcast, "concatenate": r_concatenate,
+         "dynamic_index": r_dynamic_index}

@@ -434,9 +434,12 @@ def select(pred, on_true, on_false):
 
 
 def getitem(x, i):
-    """static indexing of a small array: x[i] (int) -> slice + squeeze, as jnp does for a constant index."""
+    """x[i] along the leading axis: a constant index -> slice + squeeze, as jnp does; a traced integer index ->
+    dynamic_index (normalised if negative, then clamped into range, as jnp's gather)."""
+    if is_traced(i):
+        return dynamic_index(x, i)
     if not isinstance(i, (int, np.integer)):
-        raise TraceError("only static integer indices are supported in item code")
+        raise TraceError("only integer indices are supported in item code")
     n = x.shape[0]
     i = int(i)
     if i < 0:
@@ -447,6 +450,22 @@ def getitem(x, i):
     s = bind("slice", [x.var], [AVal((1,) + rest, x.dtype, x.aval.weak)],
              start_indices=(i,) + (0,) * len(rest), limit_indices=(i + 1,) + rest, strides=None)[0]
     return bind("squeeze", [s.var], [AVal(rest, x.dtype, x.aval.weak)], dimensions=(0,))[0]
+
+
+def dynamic_index(x, i):
+    """row i of x (i traced, integer): i < 0 counts from the end, then i is clamped to [0, n - 1] (jnp indexing
+    with a traced index; lax.dynamic_index_in_dim clamps the same way)."""
+    if not is_traced(x):
+        x = Tracer(bind("copy", [literal(np.asarray(x))], [literal(np.asarray(x)).aval.strong()])[0].var)
+    if not x.shape:
+        raise TraceError("indexing a 0-d value")
+    if not np.issubdtype(i.dtype, np.integer) or i.shape != ():
+        raise TraceError("a traced index must be an integer scalar")
+    n = x.shape[0]
+    i = convert(i, I32)
+    i = select(i < 0, i + n, i)
+    i = select(i < 0, literal(0, I32, weak=False), select(i > n - 1, literal(n - 1, I32, weak=False), i))
+    return bind("dynamic_index", [x.var, i.var], [AVal(x.shape[1:], x.dtype, x.aval.weak)])[0]
 
 
 def stack(xs):

@@ -114,6 +114,10 @@ def _jvp_eqn(e, ins, tins, lanes):
               for x in ops]
         return C.bind("tallymap_spawn", vs, [e.outvars[0].aval], **e.params), [None]
     outs = A._replay(e, ins)
+    if e.prim == "dynamic_index":          # linear in the array: the same row of its tangent
+        if tins[0] is None:
+            return outs, [None]
+        return outs, [[A._replay(e, [tins[0][l], ins[1]])[0] for l in range(lanes)]]
     if e.prim in ("tallymap_emit", "tallymap_put"):
         tt, tv = tins[0], tins[2]
         if tt is None:

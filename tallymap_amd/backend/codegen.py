@@ -511,6 +511,28 @@ def _slice(em, e, ins):
     return Val(res, out.shape, out.dtype)
 
 
+@rule("dynamic_index")
+def _dynamic_index(em, e, ins):
+    """row i of x (i clamped by the front end; clamped again here before any pointer load): a broadcast array
+    read in place loads ptr[i * row + e]; an array in registers selects its row with a compare chain."""
+    x, i = ins
+    out = e.outvars[0].aval
+    n = x.shape[0]
+    r = max(1, out.size)
+    ct = ctype(out.dtype)
+    ic = em.bind(f"min(max((i32){i.el[0]}, 0), {n - 1})", np.int32, "di")
+    res = []
+    for k in range(r):
+        if x.ptr is not None:
+            res.append(em.bind(f"{x.ptr}[(i64){ic} * {r} + {k}]", out.dtype, "dv"))
+            continue
+        expr = x.el[(n - 1) * r + k]
+        for j in range(n - 2, -1, -1):
+            expr = f"({ic} == {j} ? ({ct})({x.el[j * r + k]}) : ({ct})({expr}))"
+        res.append(em.bind(expr, out.dtype, "dv"))
+    return Val(res, out.shape, out.dtype)
+
+
 @rule("squeeze", "reshape")
 def _reshape(em, e, ins):
     x = ins[0]

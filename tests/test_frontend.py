@@ -283,3 +283,15 @@ def test_scan_and_switch_trace():
     with pytest.raises(C.TraceError, match="unrolled"):
         _prog(lambda t, x: (t, lax.scan(lambda c, _: (c, c), x, length=1000)[1]), {"h": tm.Sum((1,))},
               [((), np.float32)], [], (0,))
+
+
+def test_dynamic_index_traces():
+    """x[i] with a traced integer index: one dynamic_index equation after the normalisation and clamp; a float
+    index raises."""
+    def item(t, x, tab):
+        return t.add("h", 0, tab[(x * 10.0).astype(jnp.int32)])
+    p = _prog(item, {"h": tm.Sum((1,))}, [((), np.float32)], [((64,), np.float32)], (0, None))
+    assert sum(e.prim == "dynamic_index" for e in C.walk_eqns(p.jaxpr)) == 1
+    with pytest.raises(C.TraceError, match="integer"):
+        _prog(lambda t, x, tab: t.add("h", 0, tab[x]), {"h": tm.Sum((1,))}, [((), np.float32)],
+              [((64,), np.float32)], (0, None))

@@ -285,3 +285,51 @@ def test_scan_and_switch_items():
     from oracle import exact as X
     v = ((c + ys2).astype(f32) + s).astype(f32)
     assert _np(res.outputs["h"])[0].view(np.uint32) == X.exact_sum(v)[0].view(np.uint32)
+
+
+def _table_item(t, x, k, tab, small):
+    """the reference's basic edge item shape (edge.py:110-118): a bin picked by a traced index, a broadcast table
+    read at it (64 entries: read in place) and a small one (4 entries: in registers), negative and large indices
+    clamped as jnp does."""
+    i = (x * 80.0).astype(jnp.int32) - 8          # in [-8, 72): negatives count from the end, then clamped
+    w = tab[i] * small[k % 4] + small[k - 6]
+    return t.add("Q", jnp.clip(i, 0, 63), w * x), w
+
+
+def test_dynamic_index_forward_jvp_grad():
+    """tab[i] with a traced i: values against numpy's take with jnp's normalisation and clamping, bitwise
+    (exact tally); jvp w.r.t. the table against the closed form d w / d tab[j]; grad w.r.t. the small table against
+    forward mode."""
+    print("case: dynamic index", flush=True)
+    rng = np.random.default_rng(21)
+    n = 20_000
+    x = rng.uniform(0, 1, n).astype(f32)
+    k = rng.integers(0, 12, n).astype(np.int32)
+    tab = rng.uniform(0.5, 1.5, 64).astype(f32)
+    small = np.array([1.0, 2.0, 0.5, -1.0], f32)
+    f = tm.vmap(_table_item, outputs={"Q": tm.Sum((64,), fixed_point=True)}, in_axes=(0, 0, None, None))
+    res = f(x, k, tab, small)
+    _sync()
+
+    def take(a, j):
+        j = np.where(j < 0, j + len(a), j)
+        return a[np.clip(j, 0, len(a) - 1)]
+    i = (x * f32(80.0)).astype(np.int32) - 8
+    w = (take(tab, i) * take(small, k % 4) + take(small, k - 6)).astype(f32)
+    assert np.array_equal(_np(res.per_item).view(np.uint32), w.view(np.uint32))
+    from oracle import exact as X
+    v = (w * x).astype(f32)
+    b = np.clip(i, 0, 63)
+    want = np.array([X.exact_sum(v[b == j])[0] if (b == j).any() else f32(0) for j in range(64)], f32)
+    assert np.array_equal(_np(res.outputs["Q"]).view(np.uint32), want.view(np.uint32))
+    dt = rng.standard_normal(64).astype(f32)
+    _, tan = tm.jvp(f, (x, k, tab, small), (None, None, dt, None))
+    _sync()
+    tw = take(dt, i).astype(np.float64) * take(small, k % 4)
+    assert np.allclose(_np(tan.per_item).astype(np.float64), tw, rtol=1e-6, atol=1e-7)
+    ct = rng.uniform(0.5, 1.5, 64).astype(f32)
+    g = _np(tm.grad(f, weights={"Q": ct}, argnums=3)(x, k, tab, small)).astype(np.float64)
+    ds = np.eye(4, dtype=f32)
+    J = [float(np.dot(_np(tm.jvp(f, (x, k, tab, small), (None, None, None, ds[j]))[1].outputs["Q"]).astype(
+        np.float64), ct)) for j in range(4)]
+    assert np.allclose(g, J, rtol=1e-4), (g, J)
