@@ -130,6 +130,8 @@ def _queue(c, ins, outs, N, n_zero, flags, stream=None, n_main=None):
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
     Cm.check(Cm.lib().tm_launch(c.id, ctypes.c_void_p(s), arr, len(bufs), n_zero, flags,
                                 N if n_main is None else n_main, c.block))
+    if n_main == 0:
+        N = 0          # (tm_main did not run: its per-wave hole lists are unwritten, so the passes see no items)
     for name, kind, block, cap in (getattr(L, "aux", None) or []):
         if N == 0 and kind != "cap":         # (no item ran: only the canonical outputs are written, as zeros)
             continue
