@@ -226,6 +226,11 @@ def test_n_active_runs_only_the_first_items(n):
     xs, keys, theta = configs.c1_inputs(1 << 14)
     outs = dict(_outputs(1 << 18, 1 << 15), hist=tm.Sum((2,), fixed_point=True))
     f = tm.vmap(_walker, outputs=outs, in_axes=(0, 0, None), max_steps=100)
+    # the allocator's cached small blocks hold all-ones bytes, so a pass that read scratch the launch never wrote
+    # (the hole list when no item runs) would see garbage rather than the zeros of fresh memory
+    import torch
+    junk = [torch.full((1 << 18,), -1, dtype=torch.int32, device="cuda") for _ in range(64)]
+    del junk
     a = f(xs, keys, theta, n_active=n)
     _sync()
     k = _np(a.per_item)
