@@ -1,11 +1,13 @@
 /* tallymap_rocm.h -- the C ABI of libtallymap_rocm.so, the MI355X (gfx950) launch library of the tallymap_amd
- * kernel backend.  Plain pointers and sizes only.  Every entry returns 0 on success and a nonzero code on failure;
- * tm_last_error() then holds the message (per thread).
+ * kernel backend.  Plain pointers and sizes only.  Every tm_ entry returns 0 on success and a nonzero code on
+ * failure; tm_last_error() then holds the message (per thread).  The two tallymap_ entries keep the reference's
+ * return conventions.
  *
  * It replaces the reference's CUDA launch shim, tallymap/backends/kernel/shim.cc (and the NVRTC calls of
  * compile.py), entry for entry:
- *   tm_register      <- tallymap_register      (shim.cc:134-142)
- *   tm_kernel_info   <- tallymap_kernel_info   (shim.cc:147-155)
+ *   tallymap_register, tallymap_kernel_info: the reference's own names and signatures (shim.cc:134-155), below
+ *   tm_register      <- tallymap_register      (shim.cc:134-142), returning an error for an empty image
+ *   tm_kernel_info   <- tallymap_kernel_info   (shim.cc:147-155), for any block size and before a launch
  *   tm_launch        <- SjLaunchImpl, the body of the XLA FFI handler TallymapLaunch (shim.cc:157-250), as a
  *                       plain C call: an XLA FFI handler bound for platform "ROCM" forwards its buffers, stream and
  *                       attrs (kernel_id, block, n_zero, flags, n_items) to it
@@ -19,6 +21,7 @@
 #define TALLYMAP_ROCM_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -59,6 +62,17 @@ int tm_kernel_info(long long id, int block, long long out[8]);
 
 const char* tm_last_error(void);
 void tm_free(void* p);
+
+/* The reference launch shim's own registry exports, with its signatures and return conventions, so that its
+ * compile.py binds this library unchanged (compile.py:215-237):
+ *   tallymap_register    <- shim.cc:134-142: copies `n` bytes of the code object `data` under `id`; the first
+ *                           registration of an id wins; returns 0 (an empty image registers nothing).
+ *   tallymap_kernel_info <- shim.cc:144-155: once the program's item loop has been launched on some device, fills
+ *                           out[7] = {registers per lane, private (scratch) bytes per lane, static LDS bytes per
+ *                           block, blocks per CU at the launch block size, CUs, max resident threads per CU, block
+ *                           size of the first launch} and returns 1; returns 0 before any launch (nothing loaded). */
+int tallymap_register(int64_t id, const char* data, size_t n, const char* note);
+int tallymap_kernel_info(int64_t id, long long* out);
 
 #ifdef __cplusplus
 }

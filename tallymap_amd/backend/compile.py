@@ -83,6 +83,15 @@ def runtime_paths():
     return _paths
 
 
+def load_shim():
+    """ctypes handle of libtallymap_rocm.so, loaded after torch (whose HIP runtime the process uses), not yet bound
+    with tm_init."""
+    if not os.path.exists(SHIM):
+        raise BackendError(f"tallymap_amd: {SHIM} is not built (run __graft_entry__.build())")
+    runtime_paths()
+    return ctypes.CDLL(SHIM)
+
+
 def lib():
     """libtallymap_rocm.so, bound to this process's HIP runtime.  Raises BackendError when it is not built: the
     backend has no fallback."""
@@ -92,6 +101,7 @@ def lib():
             if not os.path.exists(SHIM):
                 raise BackendError(f"tallymap_amd: {SHIM} is not built (run __graft_entry__.build() or "
                                    "python -m tallymap_amd.build)")
+            hip, rtc = runtime_paths()        # (torch first: its HIP runtime is the one this process uses)
             L = ctypes.CDLL(SHIM)
             vp, i, ll, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
             L.tm_init.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
@@ -101,9 +111,10 @@ def lib():
             L.tm_launch.argtypes = [ll, vp, ctypes.POINTER(vp), i, i, i, ll, i]
             L.tm_launch_aux.argtypes = [ll, ctypes.c_char_p, vp, ctypes.POINTER(vp), i, ll, ctypes.c_uint, i]
             L.tm_kernel_info.argtypes = [ll, i, ctypes.POINTER(ll)]
+            L.tallymap_register.argtypes = [ctypes.c_int64, ctypes.c_char_p, sz, ctypes.c_char_p]
+            L.tallymap_kernel_info.argtypes = [ctypes.c_int64, ctypes.POINTER(ll)]
             L.tm_last_error.restype = ctypes.c_char_p
             L.tm_free.argtypes = [vp]
-            hip, rtc = runtime_paths()
             if L.tm_init(hip.encode(), rtc.encode()):
                 raise BackendError(L.tm_last_error().decode())
             _lib = L

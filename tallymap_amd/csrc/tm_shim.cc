@@ -11,6 +11,7 @@
 #include <hip/hiprtc.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -79,7 +80,9 @@ struct Loaded {
   hipFunction_t zero = nullptr, main = nullptr, post = nullptr;
   std::map<std::string, hipFunction_t> aux;     // other entries (the Records passes), looked up on first use
   int cus = 0;
+  int per_cu = 0;               // max resident threads per CU (device attribute)
   std::map<int, int> occ;       // block size -> blocks per CU of tm_main
+  int block0 = 0, occ0 = 0;     // block size and blocks per CU of the first tm_main launch (0: not launched yet)
 };
 
 std::map<long long, std::shared_ptr<Program>>& registry() {
@@ -157,7 +160,8 @@ int loaded(long long id, std::shared_ptr<Loaded>* out) {
     return fail("tallymap_rocm: %s has neither tm_main nor tm_adjoint", pr->second->note.c_str());
   probe(&L->zero, "tm_zero");
   probe(&L->post, "tm_post");
-  if ((e = g_rt.hipDeviceGetAttribute(&L->cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess)
+  if ((e = g_rt.hipDeviceGetAttribute(&L->cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess ||
+      (e = g_rt.hipDeviceGetAttribute(&L->per_cu, hipDeviceAttributeMaxThreadsPerMultiProcessor, dev)) != hipSuccess)
     return fail("tallymap_rocm: device attribute: %s", herr(e));
   modules()[{id, dev}] = L;
   *out = L;
@@ -271,6 +275,11 @@ int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, 
     const long long cap = (long long)L->cus * occ;
     const unsigned grid = (unsigned)(want < cap ? want : cap);
     if (launch1(L->main, grid, block, s, args, "tm_main")) return 1;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!L->block0) {
+      L->block0 = block;
+      L->occ0 = occ;
+    }
   }
   if ((flags & 2) && L->post && launch1(L->post, 64, 256, s, args, "tm_post")) return 1;
   return 0;
@@ -326,6 +335,35 @@ int tm_kernel_info(long long id, int block, long long out[8]) {
   out[5] = L->cus;
   out[6] = maxt;
   out[7] = (long long)L->cus * occ;
+  return 0;
+}
+
+// The reference's own two registry exports (shim.cc:134-155), with its argument lists and return conventions, so
+// its compile.py binds this library unchanged (compile.py:215-237).
+
+int tallymap_register(int64_t id, const char* data, size_t n, const char* note) {
+  // first registration wins; an empty image registers nothing (a later registration of the id still counts)
+  if (data && n) (void)tm_register((long long)id, data, n, note);
+  return 0;
+}
+
+int tallymap_kernel_info(int64_t id, long long* out) {
+  if (!g_hip_ok || !out) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto& kv : modules()) {
+    if (kv.first.first != (long long)id || !kv.second->block0) continue;
+    const Loaded& L = *kv.second;
+    int regs = 0, priv = 0, lds = 0;
+    if (g_rt.hipFuncGetAttribute(&regs, HIP_FUNC_ATTRIBUTE_NUM_REGS, L.main) != hipSuccess ||
+        g_rt.hipFuncGetAttribute(&priv, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES, L.main) != hipSuccess ||
+        g_rt.hipFuncGetAttribute(&lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, L.main) != hipSuccess) {
+      (void)g_rt.hipGetLastError();
+      return 0;
+    }
+    const long long v[7] = {regs, priv, lds, L.occ0, L.cus, L.per_cu, L.block0};
+    for (int i = 0; i < 7; ++i) out[i] = v[i];
+    return 1;
+  }
   return 0;
 }
 

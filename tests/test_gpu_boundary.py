@@ -1,0 +1,41 @@
+"""The reference-named registry exports on the GPU: tallymap_kernel_info answers once the program has run, with the
+reference's field order (shim.cc:144-155), and its figures agree with tm_kernel_info's."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import configs
+from tallymap_amd.backend import compile as Cm
+from tallymap_amd import backend as B
+
+pytestmark = pytest.mark.gpu
+
+
+def test_tallymap_kernel_info_after_launch():
+    import torch
+    from tallymap_amd import _core as CO
+    from tallymap_amd._api import build_program
+    print("case: C1 N=4096, tallymap_kernel_info before and after the first launch", flush=True)
+    C = configs.C1
+    xs, keys, theta = configs.c1_inputs(4096)
+    pav = [CO.AVal(np.shape(xs)[1:], np.float32), CO.AVal(np.shape(keys)[1:], np.uint32)]
+    bav = [CO.AVal((), np.float32)]
+    prog, _ = build_program(C["item"], C["outputs"], C["in_axes"], pav, bav, C["max_steps"])
+    c = B.compiled(prog, {"block": 192})        # (a block size no other test uses: a fresh module entry)
+    lib = Cm.lib()
+    out = (ctypes.c_longlong * 7)()
+    had = lib.tallymap_kernel_info(c.id, out)
+    res = B.run(prog, [xs, keys], [theta], 4096, {"block": 192})
+    torch.cuda.synchronize()
+    assert int(res.stats.cpu().numpy()[4]) >= 0
+    assert lib.tallymap_kernel_info(c.id, out) == 1
+    regs, local, shared, occ, cus, per_cu, block = list(out)
+    info = B.kernel_info(c)
+    assert block == 192 and c.block == 192
+    assert (regs, local, shared, occ, cus) == (info["regs"], info["private_bytes"], info["lds_bytes"],
+                                                info["blocks_per_cu"], info["cus"])
+    assert occ * block * cus == info["resident_threads"]
+    assert per_cu >= occ * block and cus >= 1
+    assert had in (0, 1)       # (1 when an earlier test launched the same module at this block size)

@@ -23,23 +23,39 @@ def _build(src, out):
 def test_cabi_exports_every_declared_symbol():
     hdr = open(os.path.join(ROOT, "include", "tallymap_rocm.h")).read()
     hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)          # declarations only, not the comments
-    names = sorted(set(re.findall(r"^[a-z][\w \*]*?\b(tm_[a-z_]+)\(", hdr, flags=re.M)))
+    names = sorted(set(re.findall(r"^[a-z][\w \*]*?\b((?:tm|tallymap)_[a-z_]+)\(", hdr, flags=re.M)))
     assert {"tm_init", "tm_compile", "tm_register", "tm_launch", "tm_kernel_info", "tm_last_error",
-            "tm_free"} <= set(names)
+            "tm_free", "tallymap_register", "tallymap_kernel_info"} <= set(names)
     from tallymap_amd.backend import compile as Cm
-    lib = ctypes.CDLL(Cm.SHIM)
+    lib = Cm.load_shim()
     for n in names:
         assert hasattr(lib, n), n
 
 
 def test_cabi_errors_without_init():
     from tallymap_amd.backend import compile as Cm
-    lib = ctypes.CDLL(Cm.SHIM)
+    lib = Cm.load_shim()
     lib.tm_last_error.restype = ctypes.c_char_p
     # tm_register copies; an empty image is refused with a message
     lib.tm_register.argtypes = [ctypes.c_longlong, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]
     assert lib.tm_register(1, b"", 0, b"x") != 0
     assert b"empty image" in lib.tm_last_error()
+
+
+def test_reference_registry_exports_keep_reference_conventions():
+    """tallymap_register / tallymap_kernel_info as the reference's compile.py binds them (compile.py:215-237):
+    register returns 0 (an empty image registers nothing); kernel_info returns 0 until the program has been launched
+    -- here no runtime is bound and nothing is loaded, so 0, and out[] is left alone."""
+    from tallymap_amd.backend import compile as Cm
+    lib = Cm.load_shim()
+    lib.tallymap_register.argtypes = [ctypes.c_int64, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]
+    lib.tallymap_kernel_info.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_longlong)]
+    assert lib.tallymap_register(7, b"", 0, b"x") == 0
+    assert lib.tallymap_register(8, b"not a code object", 17, None) == 0
+    out = (ctypes.c_longlong * 7)(*([-5] * 7))
+    assert lib.tallymap_kernel_info(8, out) == 0
+    assert lib.tallymap_kernel_info(12345, out) == 0
+    assert list(out) == [-5] * 7
 
 
 @pytest.fixture(scope="module")
