@@ -13,7 +13,8 @@
  *                       attrs (kernel_id, block, n_zero, flags, n_items) to it
  *   tm_compile       <- compile.compile_cubin's NVRTC sequence (compile.py:160-173), with hipRTC for gfx950
  *   tm_init          <- compile.py's Drv / dlopen of the driver (shim.cc:44-82): binds the HIP runtime the process
- *                       already uses (no second runtime, no device code in this library)
+ *                       already uses (no second runtime; the library's only device code is the scratch array
+ *                       of tm_launch_noalloc, every kernel lives in the program's own code object)
  *   tm_launch_aux    <- _records.canon (_records.py:45-74): the Records canonicalisation, here device passes of the
  *                       program's own module instead of XLA ops
  */
@@ -73,6 +74,23 @@ void tm_free(void* p);
  *                           size of the first launch} and returns 1; returns 0 before any launch (nothing loaded). */
 int tallymap_register(int64_t id, const char* data, size_t n, const char* note);
 int tallymap_kernel_info(int64_t id, long long* out);
+
+/* Bytes of the device array tm_launch_noalloc places scratch buffers in: one per GPU the library runs on, held
+ * until the process ends. */
+#define TM_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* tm_launch for callers that cannot allocate device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference.  The caller passes the inputs and outputs in
+ * bufs as for tm_launch; the n_slots buffers named by slots[] (their bufs entries are ignored and may be NULL) are
+ * placed instead, 256-byte aligned and `bytes[j]` long, in the library's own per-device array of
+ * TM_NOALLOC_SCRATCH_BYTES: the program's scratch (exact and fixed-point words, the claim / truncation counters,
+ * a replay tape).  A layout that does not fit is refused with an error before anything is queued.  tm_zero
+ * (n_zero > 0) clears what must start at zero, as for tm_launch; the array otherwise keeps the last call's
+ * contents.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race.  The first call on a device resolves the array there (and loads the program's module, as
+ * tm_launch does); later calls allocate nothing. */
+int tm_launch_noalloc(long long id, void* stream, void* const* bufs, int n, const int* slots,
+                      const long long* bytes, int n_slots, int n_zero, int flags, long long n_items, int block);
 
 #ifdef __cplusplus
 }

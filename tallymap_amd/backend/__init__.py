@@ -140,6 +140,38 @@ def _queue(c, ins, outs, N, n_zero, flags, stream=None, n_main=None):
         Cm.check(Cm.lib().tm_launch_aux(c.id, name.encode(), ctypes.c_void_p(s), arr, len(bufs), N, grid, block))
 
 
+def launch_noalloc(c, ins, N, stream=None):
+    """c over N items through tm_launch_noalloc: the outputs are allocated here (torch), the scratch buffers of the
+    layout (exact / fixed-point words, ctl) live in the library's per-device array -> the result tensors in layout
+    order, with None at the scratch slots.  A program with Records or spawn (their passes and generations run
+    through tm_launch_aux and the host) is refused."""
+    import ctypes
+
+    import torch
+    L = c.layout
+    if getattr(L, "aux", None) or getattr(L, "r_q", None) or not getattr(L, "scratch", None):
+        raise ValueError("tallymap_amd: launch_noalloc runs plain forward programs (no Records, no spawn)")
+    scr = set(L.scratch)
+    outs, slots, nbytes = [], [], []
+    for j, (shape, dt, per_item) in enumerate(L.res):
+        r = L.n_in + j
+        sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
+        if r in scr:
+            outs.append(None)
+            slots.append(r)
+            nbytes.append(int(np.prod(sh, dtype=np.int64)) * np.dtype(dt).itemsize)
+        else:
+            outs.append(torch.empty(sh, dtype=torch_dtype(dt), device="cuda"))
+    bufs = [t.data_ptr() for t in ins] + [0 if t is None else t.data_ptr() for t in outs]
+    arr = (ctypes.c_void_p * len(bufs))(*bufs)
+    sl = (ctypes.c_int * max(1, len(slots)))(*slots)
+    nb = (ctypes.c_longlong * max(1, len(nbytes)))(*nbytes)
+    s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    Cm.check(Cm.lib().tm_launch_noalloc(c.id, ctypes.c_void_p(s), arr, len(bufs), sl, nb, len(slots), L.n_zero,
+                                        L.flags, N, c.block))
+    return outs
+
+
 def run(prog, pi, bc, N, opts, n_active=None):
     """the kernel backend's run(): outputs of prog over N items (only the first n_active of them run when given:
     the others emit nothing, count as nothing and get zero per-item results)."""

@@ -113,6 +113,8 @@ def lib():
             L.tm_kernel_info.argtypes = [ll, i, ctypes.POINTER(ll)]
             L.tallymap_register.argtypes = [ctypes.c_int64, ctypes.c_char_p, sz, ctypes.c_char_p]
             L.tallymap_kernel_info.argtypes = [ctypes.c_int64, ctypes.POINTER(ll)]
+            L.tm_launch_noalloc.argtypes = [ll, vp, ctypes.POINTER(vp), i, ctypes.POINTER(i), ctypes.POINTER(ll), i,
+                                            i, i, ll, i]
             L.tm_last_error.restype = ctypes.c_char_p
             L.tm_free.argtypes = [vp]
             if L.tm_init(hip.encode(), rtc.encode()):

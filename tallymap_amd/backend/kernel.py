@@ -57,6 +57,8 @@ class Layout:
     aux: list = dataclasses.field(default_factory=list)
     # spawn: the next generation's per-item operand buffers (result indices, one per per-item operand, Q rows)
     r_q: list = dataclasses.field(default_factory=list)
+    # the buffers only the kernels read (exact / fixed-point words, ctl): what tm_launch_noalloc may place itself
+    scratch: list = dataclasses.field(default_factory=list)
 
 
 def _split(jx):
@@ -966,5 +968,6 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     L = Layout(n_in=n_in, res=res, n_zero=n_zero, r_out=r_out, r_ctl=r_ctl, r_stats=r_stats, r_ys=r_ys,
                flags=flags, mode=mode, priv=priv, zero_words=zero_words, r_q=r_q,
                records=[dict(name=ri["name"], capacity=ri["capacity"], r_ctr=(r_rctr, 2 * ri["ctr"] + 1),
-                             fields={f: rr for f, (_, rr) in ri["fields"].items()}) for ri in rec_info], aux=aux)
+                             fields={f: rr for f, (_, rr) in ri["fields"].items()}) for ri in rec_info], aux=aux,
+               scratch=sorted(r_scr.values()) + [r_ctl])
     return "\n".join(src) + "\n", L

@@ -1,0 +1,93 @@
+// tm_launch_noalloc (include/tallymap_rocm.h): tm_launch with the program's scratch buffers -- exact and fixed-point
+// words, the claim and truncation counters, a replay tape -- placed in a device array of this library instead of
+// buffers the caller allocates.  For callers that cannot allocate device memory: code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the reference.
+//
+// The array is a file-scope __device__ variable, so every GPU the library runs on holds its own copy (loaded with
+// this library's code object, kept until the process ends).  Host code never passes the variable's name to a
+// kernel -- on the host that name is only a registration handle -- but the device address hipGetSymbolAddress
+// returns for it, resolved once per device with that device current and kept in g_scratch.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+
+#include "../../include/tallymap_rocm.h"
+
+int tm_fail_msg(const char* msg);     // tm_shim.cc: sets tm_last_error(), returns 1
+
+static __device__ __align__(256) unsigned char scratch[TM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kMaxBufs = 4096;
+constexpr int kMaxSlots = 256;
+constexpr unsigned long long kAlign = 256;
+
+std::mutex g_na_mu;
+void* g_scratch[kMaxDevices];         // per device: the device address of its copy of `scratch` (null: not yet)
+
+int err(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  return tm_fail_msg(buf);
+}
+
+// the device address of `scratch` on the current device, resolved on the first call there
+int scratch_base(unsigned char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return err("tallymap_rocm: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return err("tallymap_rocm: device %d is beyond the no-alloc table", dev);
+  std::lock_guard<std::mutex> lk(g_na_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return err("tallymap_rocm: resolving the no-alloc scratch array on device %d: %s", dev,
+                 e != hipSuccess ? hipGetErrorString(e) : "null address");
+    g_scratch[dev] = p;
+  }
+  *out = static_cast<unsigned char*>(g_scratch[dev]);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int tm_launch_noalloc(long long id, void* stream, void* const* bufs, int n, const int* slots,
+                                 const long long* bytes, int n_slots, int n_zero, int flags, long long n_items,
+                                 int block) {
+  if (!bufs || n < 1 || n > kMaxBufs) return err("tallymap_rocm: tm_launch_noalloc: %d buffers (1..%d)", n, kMaxBufs);
+  if (n_slots < 0 || n_slots > n || n_slots > kMaxSlots || (n_slots > 0 && (!slots || !bytes)))
+    return err("tallymap_rocm: tm_launch_noalloc: bad scratch slot list (%d slots of %d buffers)", n_slots, n);
+  // the layout in the array: each slot 256-byte aligned, in the order given; checked in full before any HIP call
+  unsigned long long off[kMaxSlots];
+  bool seen[kMaxBufs] = {};
+  unsigned long long end = 0;
+  for (int j = 0; j < n_slots; ++j) {
+    const int s = slots[j];
+    if (s < 0 || s >= n || seen[s])
+      return err("tallymap_rocm: tm_launch_noalloc: scratch slot %d is out of range or repeated", s);
+    if (bytes[j] < 0) return err("tallymap_rocm: tm_launch_noalloc: negative size for scratch slot %d", s);
+    seen[s] = true;
+    const unsigned long long at = (end + kAlign - 1) / kAlign * kAlign;
+    const unsigned long long b = static_cast<unsigned long long>(bytes[j]);
+    if (at > TM_NOALLOC_SCRATCH_BYTES || b > TM_NOALLOC_SCRATCH_BYTES - at)
+      return err("tallymap_rocm: tm_launch_noalloc: the program's scratch needs more than the %u bytes of the "
+                 "no-alloc array (slot %d: %lld bytes at offset %llu); use tm_launch with caller buffers",
+                 TM_NOALLOC_SCRATCH_BYTES, s, bytes[j], at);
+    off[j] = at;
+    end = at + b;
+  }
+  unsigned char* base = nullptr;
+  if (n_slots > 0 && scratch_base(&base)) return 1;
+  void* p[kMaxBufs];
+  for (int i = 0; i < n; ++i) p[i] = bufs[i];
+  for (int j = 0; j < n_slots; ++j) p[slots[j]] = base + off[j];
+  return tm_launch(id, stream, p, n, n_zero, flags, n_items, block);
+}

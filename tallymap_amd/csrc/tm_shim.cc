@@ -1,8 +1,10 @@
 // libtallymap_rocm.so -- the C-ABI launch library of the tallymap_amd kernel backend (include/tallymap_rocm.h).
 //
-// Host code only.  The HIP runtime and hipRTC are resolved with dlopen / dlsym at tm_init, so the library binds to
+// Host code.  The HIP runtime and hipRTC are resolved with dlopen / dlsym at tm_init, so the library binds to
 // the runtime the process already loaded (a framework's bundled libamdhip64) instead of starting a second one; the
-// hip headers are used for types and enum values only.  Every kernel (zeroing, the item loop, the readout) lives in
+// hip headers are used for types and enum values only.  (The library's one piece of device code, the scratch array
+// of tm_launch_noalloc, is in tm_noalloc.hip; loaded after the framework, the library's own HIP dependency resolves
+// to that same runtime.)  Every kernel (zeroing, the item loop, the readout) lives in
 // the program's own code object, registered with tm_register and loaded per device on its first launch.
 //
 // Reference: tallymap/backends/kernel/shim.cc (CUDA driver version of the same registry and launch sequence).
@@ -372,3 +374,6 @@ const char* tm_last_error(void) { return g_err.c_str(); }
 void tm_free(void* p) { free(p); }
 
 }  // extern "C"
+
+// (internal to the library) the error path of tm_noalloc.hip
+__attribute__((visibility("hidden"))) int tm_fail_msg(const char* msg) { return fail("%s", msg); }

@@ -1,0 +1,83 @@
+"""tm_launch_noalloc against tm_launch through the C ABI: the same program, the same inputs, the scratch buffers
+(exact words, counters) in the library's per-device array instead of caller allocations.  Outputs must be bitwise
+equal -- exact tallies are order independent, trip counts and flags are integers -- on two calls in a row, the
+second with fewer items (the array keeps the first call's contents: tm_zero must clear what has to start at zero).
+Runs alone in a fresh process and after the other tests."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import _core as CO
+from tallymap_amd import backend as B
+from tallymap_amd import configs
+from tallymap_amd._api import Sum, build_program
+from tallymap_amd.backend import compile as Cm
+
+pytestmark = pytest.mark.gpu
+
+
+def _prog(cfg, args, exact):
+    outs = {k: Sum(v.shape, fixed_point=True) if exact else v for k, v in cfg["outputs"].items()}
+    axes = cfg["in_axes"]
+    pav = [CO.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
+    bav = [CO.AVal(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
+    return build_program(cfg["item"], outs, axes, pav, bav, cfg["max_steps"])[0]
+
+
+def _ins(args, axes):
+    pi = [B.device_tensor(a, np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
+    bc = [B.device_tensor(a, np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
+    return pi + bc
+
+
+def _pair(c, args, axes, N):
+    import torch
+    ins = _ins(args, axes)
+    ref = B.launch(c, ins, N)
+    got = B.launch_noalloc(c, ins, N)
+    torch.cuda.synchronize()
+    scr = set(c.layout.scratch)
+    n = 0
+    for j, (r, g) in enumerate(zip(ref, got)):
+        if c.layout.n_in + j in scr:
+            assert g is None
+            continue
+        assert g is not None
+        a, b = r.cpu().numpy(), g.cpu().numpy()
+        assert a.shape == b.shape
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"result {j} differs"
+        n += 1
+    return n
+
+
+@pytest.mark.parametrize("name,n1,n2", [("c1", 10_000, 3_000), ("c3", 65_536, 8_192)])
+def test_noalloc_matches_tm_launch(name, n1, n2):
+    cfg = getattr(configs, name.upper())
+    args = getattr(configs, f"{name}_inputs")(n1)
+    prog = _prog(cfg, args, exact=True)
+    c = B.compiled(prog, {})
+    assert c.layout.scratch
+    for N in (n1, n2):
+        print(f"case: {name} exact tallies, N={N}: tm_launch vs tm_launch_noalloc", flush=True)
+        a = [np.asarray(x)[:N] if ax == 0 else x for x, ax in zip(args, cfg["in_axes"])]
+        assert _pair(c, a, cfg["in_axes"], N) >= 3
+
+
+def test_noalloc_refuses_oversized_scratch():
+    import torch
+    cfg = configs.C1
+    args = configs.c1_inputs(1024)
+    c = B.compiled(_prog(cfg, args, exact=True), {})
+    ins = _ins(args, cfg["in_axes"])
+    outs = B._alloc(c, 1024)
+    bufs = [t.data_ptr() for t in ins] + [t.data_ptr() for t in outs]
+    arr = (ctypes.c_void_p * len(bufs))(*bufs)
+    sl = (ctypes.c_int * 1)(c.layout.scratch[0])
+    nb = (ctypes.c_longlong * 1)((32 << 20) + 1)
+    lib = Cm.lib()
+    rc = lib.tm_launch_noalloc(c.id, None, arr, len(bufs), sl, nb, 1, c.layout.n_zero, c.layout.flags, 1024,
+                               c.block)
+    assert rc != 0 and b"no-alloc array" in lib.tm_last_error()
+    torch.cuda.synchronize()
