@@ -397,14 +397,48 @@ def true_divide(a, b):
 
 
 def floor_divide(a, b):
-    dt, _ = result_type(_aval(a), _aval(b))
-    if _kind(dt) == 2:
-        return unop("floor", binop("div", a, b))
-    raise TraceError("integer floor division is not supported by this backend's tracer")
+    """jnp.floor_divide (`//`) as JAX defines it, primitive for primitive: unsigned -> div; signed -> div, minus 1
+    where the signs differ and the remainder is nonzero; float -> CPython's float_divmod (rem, div of the
+    difference, a correction, then round half away from zero)."""
+    dt, weak = result_type(_aval(a), _aval(b))
+    k = _kind(dt)
+    if k == 1 and np.issubdtype(dt, np.unsignedinteger):
+        return binop("div", a, b)
+    if k == 1:
+        a, b = _coerce_t(a, dt, weak), _coerce_t(b, dt, weak)
+        q = binop("div", a, b)
+        fix = binop("and", binop("ne", unop("sign", a), unop("sign", b)), binop("ne", binop("rem", a, b), 0))
+        return select(fix, q - 1, q)
+    if k == 2:
+        a, b = _coerce_t(a, dt, weak), _coerce_t(b, dt, weak)
+        mod = binop("rem", a, b)
+        div = binop("div", binop("sub", a, mod), b)
+        ind = binop("and", binop("ne", mod, 0), binop("ne", unop("sign", b), unop("sign", mod)))
+        div = select(ind, div - 1, div)
+        return bind("round", [div.var], [div.aval], rounding_method=0)[0]
+    raise TraceError(f"floor division of {dt}")
 
 
 def remainder(a, b):
-    return binop("rem", a, b)
+    """jnp.remainder (`%`) as JAX defines it: an integer divisor of 0 is replaced by 1; the truncated remainder
+    (lax.rem) takes the divisor's sign by one add where the two signs differ and it is nonzero."""
+    dt, weak = result_type(_aval(a), _aval(b))
+    if _kind(dt) not in (1, 2):
+        raise TraceError(f"remainder of {dt}")
+    a, b = _coerce_t(a, dt, weak), _coerce_t(b, dt, weak)
+    if _kind(dt) == 1:
+        b = select(b == 0, literal(1, dt, weak=weak), b)
+    t = binop("rem", a, b)
+    plus = binop("and", binop("ne", binop("lt", t, 0), binop("lt", b, 0)), binop("ne", t, 0))
+    return select(plus, binop("add", t, b), t)
+
+
+def _coerce_t(x, dt, weak):
+    """x as a traced value of dtype dt (constants are materialised: the JAX definitions above apply primitives to
+    both operands)."""
+    if is_traced(x):
+        return x if x.dtype == dt else convert(x, dt, weak)
+    return Tracer(bind("copy", [literal(np.asarray(x, dt), dt)], [AVal((), dt, weak)])[0].var)
 
 
 def power(a, b):

@@ -219,9 +219,9 @@ def b_div(t, a):
 
 def b_rem(t, a):
     if t == "float":
-        return f"__builtin_fmodf({a[0]}, {a[1]})"
+        return f"tm_fmodf({a[0]}, {a[1]})"
     if t == "double":
-        return f"__builtin_fmod({a[0]}, {a[1]})"
+        return f"tm_fmod({a[0]}, {a[1]})"
     return f"tm_irem(({t})({a[0]}), ({t})({a[1]}))"
 
 
@@ -412,6 +412,17 @@ def conv(x, f, t):
             raise CodegenError(f"conversion {f} -> {t} is not supported")
         return f"{fn}({x})"
     return f"(({t})({x}))"
+
+
+@rule("round")
+def _round(em, e, ins):
+    """lax.round: rounding_method 0 rounds half away from zero (C round), 1 half to even (C rint)."""
+    x = ins[0]
+    out = e.outvars[0].aval
+    t = ctype(out.dtype)
+    f = ("__builtin_round" if int(e.params.get("rounding_method", 0)) == 0 else "__builtin_rint") + \
+        ("f" if t == "float" else "")
+    return Val([em.bind(f"{f}({a})", out.dtype) for a in x.el], out.shape, out.dtype)
 
 
 @rule("convert_element_type")

@@ -111,6 +111,50 @@ template <class T, class U> TM_FN T tm_shra(T a, T b) {
   else return (T)(a >> (U)b);
 }
 
+// lax.rem of floats: the exact remainder x - trunc(x / y) y with x's sign (C fmod; the reference's CPU target calls
+// glibc's fmodf / fmod, which are exact).  NaN for a NaN operand, an infinite x or a zero y; x itself when |x| < |y|
+// (an infinite y included); +-0 when |x| == |y|.  Otherwise |x| = mx 2^ex', |y| = my 2^ey' with integer
+// significands, and the remainder is (mx 2^(ex' - ey') mod my) 2^ey': the reduction runs on the significands in
+// integer arithmetic (8 bits per step for f32: r < my < 2^24 keeps r << 8 within 32 bits; one bit per step for
+// f64, with no variable 64-bit shift), and scaling r (< my, so exact in the format) by 2^ey' rounds nothing.
+TM_FN float tm_fmodf(float x, float y) {
+  const u32 ux = tm_f2u(x), ax = ux & 0x7fffffffu, ay = tm_f2u(y) & 0x7fffffffu;
+  if (ax >= 0x7f800000u || ay > 0x7f800000u || ay == 0u) return __builtin_nanf("");
+  if (ax <= ay) return ax == ay ? tm_u2f(ux & 0x80000000u) : x;
+  int ex = (int)(ax >> 23), ey = (int)(ay >> 23);
+  u32 mx = ax & 0x7fffffu, my = ay & 0x7fffffu;
+  if (ex) mx |= 0x800000u; else ex = 1;        // (a subnormal: exponent field 1, no hidden bit)
+  if (ey) my |= 0x800000u; else ey = 1;
+  u32 r = mx % my;
+  for (int d = ex - ey; d > 0;) {
+    const int sh = d < 8 ? d : 8;
+    r = (r << sh) % my;
+    d -= sh;
+  }
+  if (r == 0u) return tm_u2f(ux & 0x80000000u);
+  const float v = __builtin_ldexpf((float)r, ey - 150);
+  return (ux >> 31) ? -v : v;
+}
+TM_FN double tm_fmod(double x, double y) {
+  const u64 ux = tm_d2u(x), ax = ux & 0x7fffffffffffffffull, ay = tm_d2u(y) & 0x7fffffffffffffffull;
+  if (ax >= 0x7ff0000000000000ull || ay > 0x7ff0000000000000ull || ay == 0ull) return __builtin_nan("");
+  if (ax <= ay) return ax == ay ? tm_u2d(ux & 0x8000000000000000ull) : x;
+  int ex = (int)(ax >> 52), ey = (int)(ay >> 52);
+  u64 mx = ax & 0xfffffffffffffull, my = ay & 0xfffffffffffffull;
+  if (ex) mx |= 1ull << 52; else ex = 1;
+  if (ey) my |= 1ull << 52; else ey = 1;
+  while (!(mx >> 52)) { mx <<= 1; --ex; }     // normalise: both significands in [2^52, 2^53), so ex >= ey
+  while (!(my >> 52)) { my <<= 1; --ey; }
+  u64 r = mx >= my ? mx - my : mx;
+  for (int d = ex - ey; d > 0; --d) {
+    r <<= 1;
+    if (r >= my) r -= my;
+  }
+  if (r == 0ull) return tm_u2d(ux & 0x8000000000000000ull);
+  const double v = __builtin_ldexp((double)r, ey - 1075);
+  return (ux >> 63) ? -v : v;
+}
+
 // float -> integer toward zero, saturating, NaN -> 0
 TM_FN i32 tm_f2i32(float x) {
   return x != x ? 0 : (x <= -2147483648.0f ? (i32)0x80000000u : (x >= 2147483648.0f ? 0x7fffffff : (i32)x));

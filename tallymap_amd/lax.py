@@ -378,3 +378,44 @@ def shift_right_logical(x, n):
 
 def shift_left(x, n):
     return C.binop("shift_left", x, n)
+
+
+def shift_right_arithmetic(x, n):
+    return C.binop("shift_right_arithmetic", x, n)
+
+
+def div(a, b):
+    """lax.div: rounds toward zero for integers (x / 0 = -1 for signed, all ones for unsigned; INT_MIN / -1 =
+    INT_MIN); IEEE division for floats."""
+    return C.binop("div", a, b)
+
+
+def rem(a, b):
+    """lax.rem: the remainder with the dividend's sign (C fmod / %); integer x rem 0 = x, INT_MIN rem -1 = 0."""
+    return C.binop("rem", a, b)
+
+
+def round(x, rounding_method=0):      # noqa: A001 (lax.round)
+    """lax.round: 0 = half away from zero (lax.RoundingMethod.AWAY_FROM_ZERO), 1 = half to even."""
+    if int(rounding_method) not in (0, 1):
+        raise C.TraceError("lax.round: rounding_method must be 0 (away from zero) or 1 (to nearest even)")
+    if not C.is_traced(x) or C._kind(x.dtype) != 2:
+        raise C.TraceError("lax.round needs a traced float operand")
+    return C.bind("round", [x.var], [x.aval], rounding_method=int(rounding_method))[0]
+
+
+def neg(x):
+    return C.unop("neg", x)
+
+
+def abs(x):          # noqa: A001 (lax.abs)
+    return C.unop("abs", x)
+
+
+def sign(x):
+    return C.unop("sign", x)
+
+
+def clamp(lo, x, hi):
+    """lax.clamp(min, x, max) = min(max(x, lo), hi)."""
+    return C.binop("min", C.binop("max", x, lo), hi)

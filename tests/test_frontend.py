@@ -295,3 +295,23 @@ def test_dynamic_index_traces():
     with pytest.raises(C.TraceError, match="integer"):
         _prog(lambda t, x, tab: t.add("h", 0, tab[x]), {"h": tm.Sum((1,))}, [((), np.float32)],
               [((64,), np.float32)], (0, None))
+
+
+def test_floor_divide_and_remainder_follow_jnp():
+    """`//` and `%` trace to JAX's own definitions (jnp.floor_divide / jnp.remainder): signed integers divide with
+    lax.div and step down by one where the signs differ and the remainder is nonzero; an integer `%` replaces a zero
+    divisor by 1; floats go through rem, the sign correction and round (half away from zero)."""
+    def prims(fn, dt):
+        p = _prog(lambda t, a, b: (t, fn(a, b)), {}, [((), dt), ((), dt)], [], (0, 0))
+        return [e.prim for e in C.walk_eqns(p.jaxpr)], p
+    ps, _ = prims(lambda a, b: a // b, np.int32)
+    assert ps.count("div") == 1 and ps.count("rem") == 1 and ps.count("sign") == 2 and "select_n" in ps
+    ps, _ = prims(lambda a, b: a // b, np.uint32)
+    assert ps == ["div"]
+    ps, _ = prims(lambda a, b: a % b, np.int32)
+    assert ps.count("rem") == 1 and ps.count("select_n") == 2 and "add" in ps
+    ps, p = prims(lambda a, b: a // b, np.float32)
+    rnd = [e for e in C.walk_eqns(p.jaxpr) if e.prim == "round"]
+    assert len(rnd) == 1 and rnd[0].params["rounding_method"] == 0 and ps.count("rem") == 1
+    ps, _ = prims(lambda a, b: a % b, np.float32)
+    assert ps.count("rem") == 1 and "eq" not in ps           # (no zero-divisor guard for floats)

@@ -216,3 +216,14 @@ def test_util_module_compiles_for_gfx950():
     for e in ("tm_xscan_local", "tm_xscan_top", "tm_xscan_add", "tm_tree_scatter", "tm_tree_scatter_b"):
         assert f"void __launch_bounds__" in src and e in src
     assert len(Cm.code_object(src, name="tm_util.hip")) > 0
+
+
+def test_fmod_matches_glibc(tmp_path):
+    """lax.rem of floats (tm_fmodf / tm_fmod): bitwise glibc's exact fmodf / fmod on special values and 8M
+    pseudo-random pairs across the exponent range, subnormals included."""
+    exe = _build("tests/native/fmod_check.cc", str(tmp_path / "fmod_check"))
+    r = subprocess.run([exe, "4000000"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+    bad, tot = map(int, r.stdout.split()[-2:])
+    assert bad == 0 and tot > 8_000_000
+
