@@ -179,7 +179,8 @@ class ItemProgram:
 
 
 # ----------------------------------------------------------------------------------------- tally checks
-TALLY_OPS = ("tallymap_emit", "tallymap_claim", "tallymap_put", "tallymap_spawn")     # operand 0: the tally threaded
+TALLY_OPS = ("tallymap_emit", "tallymap_claim", "tallymap_put", "tallymap_spawn",     # operand 0: the tally threaded
+             "tallymap_tape_put")
 
 
 def check_tallies(jx, nT, where=""):

@@ -89,19 +89,25 @@ def compiled(prog, opts, adjoint=None):
     return c
 
 
-def launch(c, ins, N, stream=None):
-    """allocate c's results and queue its kernels -> the result tensors (in layout order)."""
-    outs = _alloc(c, N)
+def launch(c, ins, N, stream=None, tape=None):
+    """allocate c's results and queue its kernels -> the result tensors (in layout order).  tape: the tape
+    adjoint's item-major tape buffer (a program with a tape result uses it instead of allocating)."""
+    outs = _alloc(c, N, tape)
     _queue(c, ins, outs, N, c.layout.n_zero, c.layout.flags, stream)
     return outs
 
 
-def _alloc(c, N):
+def _alloc(c, N, tape=None):
     """c's result tensors for a launch over N items (uninitialised: tm_zero clears what must start at zero)."""
     import torch
     L = c.layout
     outs = []
     for shape, dt, per_item in L.res:
+        if per_item == ("itape",):
+            if tape is None:
+                raise ValueError("tallymap_amd: a tape program launched without its tape buffer")
+            outs.append(tape)
+            continue
         if per_item == "tape":          # per launched lane (the launcher's persistent grid at this N)
             sh = (_lanes(c, N),) + tuple(shape)
         elif per_item == ("rraw",):     # a Records raw buffer: the capacity + 255 spare slots per launched wave
@@ -385,7 +391,7 @@ def compiled_adjoint(adj, opts):
     tape = int(opts.get("rev_tape", RP.TAPE) or RP.TAPE)
     rrefill = int(opts.get("rev_refill", RP.REFILL))
     if sched not in ("step", "item"):
-        raise ValueError(f"tallymap_amd: rev_schedule must be 'step' or 'item', got {sched!r}")
+        raise ValueError(f"tallymap_amd: rev_schedule must be 'tape', 'step' or 'item', got {sched!r}")
     key = (adj.digest(), block, "adjoint", sched, ck if sched == "item" else (tape, rrefill))
     with _LOCK:
         hit = _KERNELS.get(key)
@@ -461,6 +467,26 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
                 for k, j in zip(q.out_tallies, adj.wrt_bc)]
         ys = [res[r - base] for r in L.r_ys]
         g_pi = ys[:len(adj.wrt_pi)]
+    elif opts.get("rev_schedule", "tape") == "tape":
+        from . import tape as T
+        tp = _TAPE.get(adj.digest())
+        if tp is None:
+            tp = _TAPE[adj.digest()] = T.programs(adj, pl)
+        cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"))
+        capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
+        tape = torch.empty((max(1, N * cap * tp.Wp),), dtype=torch.uint32, device="cuda")
+        # count: the loop with its states taped, POST's VJP -> K, lambda, P cotangents, truncation
+        c1 = compiled(tp.count, opts)
+        r1 = launch(c1, ins_p + ins_b + [capt], N, tape=tape)
+        hand = [r1[r - c1.layout.n_in] for r in c1.layout.r_ys]
+        # reverse: the steps' VJPs newest first from the tape, PRE's VJP -> the cotangents
+        c = compiled(tp.reverse, opts)
+        res = launch(c, ins_p + hand + ins_b + [capt], N, tape=tape)
+        L = c.layout
+        base = L.n_in
+        g_bc = [res[L.r_out[k] - base].reshape(prog.b_avals()[j].shape)
+                for k, j in zip(tp.reverse.out_tallies, adj.wrt_bc)]
+        g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
     else:
         c = compiled_adjoint(adj, opts)
         res = launch(c, ins_p + ins_b, N)
@@ -473,4 +499,5 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
 
 
 _FWD_ONLY = {}
+_TAPE = {}                  # adjoint digest -> tape.TapePrograms
 _ADJ = {}                   # (program digest, wrt) -> (reverse.Adjoint, reverse.Plan)

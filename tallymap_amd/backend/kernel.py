@@ -302,6 +302,10 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     r_rbs = result((), np.int64, per_item=True) if recs else None
     for ri in rec_info:        # per launched wave: the unused slot range [s0, s1) of its last batch (+ a count)
         ri["fin"] = result((), np.uint64, per_item=("rwave",))
+    # the tape adjoint's programs (backend/tape.py): a u32 buffer of N x cap x Wp words (cap: an operand), written
+    # by the count program's tape puts and read by the reverse program's gets; the caller allocates it
+    tape_w = int(getattr(prog, "tape_words", 0) or 0)
+    r_tape = result((tape_w,), np.uint32, per_item=("itape",)) if tape_w else None
     R = n_in + len(res)
 
     # ------------------------------------------------------------------------------- privatisation plan
@@ -398,6 +402,79 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         return t
     em.hooks["tallymap_put"] = put_rule
     em.hooks["tallymap_item_index"] = lambda em_, e, ins: Val(["((i32)tm_item)"], (), C.I32)
+
+    def _words_of(em_, v):
+        """the u32 words of a value's elements (a 64-bit element: low word first)."""
+        ws = []
+        for el in v.el:
+            ct = ctype(v.dtype)
+            if v.dtype.itemsize == 8:
+                b = em_.bind(f"__builtin_bit_cast(u64, ({ct})({el}))", C.U64, "tw")
+                ws += [f"(u32){b}", f"(u32)({b} >> 32)"]
+            elif ct in ("float", "i32", "u32"):
+                ws.append(f"__builtin_bit_cast(u32, ({ct})({el}))")
+            else:
+                ws.append(f"(u32)({el})")
+        return ws
+
+    def tape_row(em_, k, cap, const):
+        p = em_.fresh("tp")
+        em_.line(f"{const}u32* const {p} = ({const}u32*)P.p[{r_tape}] + ((u64)tm_item * (u64)(u32)({cap}) + "
+                 f"(u64)(u32)({k})) * {tape_w}ull;")
+        return p
+
+    def tape_put_rule(em_, e, ins):
+        """the state before step k into slot k of the item's tape row, when k < cap (whole 16-byte units)."""
+        t, k, cap = ins[0], ins[1], ins[2]
+        ws = [w_ for v in ins[3:] for w_ in _words_of(em_, v)]
+        ws += ["0u"] * (tape_w - len(ws))
+        em_.open(f"if ((u32)({k.el[0]}) < (u32)({cap.el[0]}))")
+        p = tape_row(em_, k.el[0], cap.el[0], "")
+        u = 4 if tape_w % 4 == 0 else (2 if tape_w % 2 == 0 else 1)
+        for q in range(0, tape_w, u):
+            if u == 1:
+                em_.line(f"{p}[{q}] = {ws[q]};")
+            else:
+                em_.line(f"*(tm_u32x{u}*)&{p}[{q}] = (tm_u32x{u}){{{', '.join(ws[q:q + u])}}};")
+        em_.close()
+        return t
+    em.hooks["tallymap_tape_put"] = tape_put_rule
+
+    def tape_get_rule(em_, e, ins):
+        """the state stored in slot j (< cap) of the item's tape row."""
+        j, cap = ins
+        p = tape_row(em_, j.el[0], cap.el[0], "const ")
+        words = []
+        u = 4 if tape_w % 4 == 0 else (2 if tape_w % 2 == 0 else 1)
+        for q in range(0, tape_w, u):
+            if u == 1:
+                words.append(em_.bind(f"{p}[{q}]", C.U32, "tq"))
+                continue
+            v = em_.fresh("tq")
+            em_.line(f"const tm_u32x{u} {v} = *(const tm_u32x{u}*)&{p}[{q}];")
+            words += [f"{v}.{c}" for c in "xyzw"[:u]]
+        outs, w_ = [], 0
+        for o in e.outvars:
+            a = o.aval
+            ct = ctype(a.dtype)
+            els = []
+            for _ in range(max(1, a.size)):
+                if a.dtype.itemsize == 8:
+                    els.append(em_.bind(f"__builtin_bit_cast({ct}, (u64)({words[w_]}) | ((u64)({words[w_ + 1]}) << 32))",
+                                        a.dtype, "tg"))
+                    w_ += 2
+                elif ct in ("float", "i32", "u32"):
+                    els.append(em_.bind(f"__builtin_bit_cast({ct}, (u32)({words[w_]}))", a.dtype, "tg"))
+                    w_ += 1
+                elif ct == "bool":
+                    els.append(em_.bind(f"(({words[w_]}) != 0u)", a.dtype, "tg"))
+                    w_ += 1
+                else:
+                    els.append(em_.bind(f"({ct})({words[w_]})", a.dtype, "tg"))
+                    w_ += 1
+            outs.append(Val(els, a.shape, a.dtype))
+        return outs
+    em.hooks["tallymap_tape_get"] = tape_get_rule
 
     def spawn_rule(em_, e, ins):
         """a spawned child.  Staged (QS > 0): the spawning lanes write the child's operands as words into their

@@ -1,0 +1,348 @@
+"""The replay adjoint as two phase-uniform launches of the forward template (reference tallymap/_reverse.py:324-444,
+1079-1180 is the adjoint computed; reverse.py holds the shared analysis: the PRE / LOOP / POST split, carry activity
+and relevance, the step, POST and PRE VJP programs).
+
+The single-kernel replay (replay.py) runs counting and reversing lanes in the same waves, so a wave holding both
+runs the step and its VJP for every lane, and a wave waits for its refill threshold before it takes new items.  Here
+the two phases are two ordinary item programs, each run by the forward template (kernel.build: step refill, LDS
+operand staging, tail-phase repacking, paced claims), so every wave runs one kind of step:
+
+  count    PRE; the loop, storing the state before step k in the item's tape row (slots 0 .. cap-1); POST and
+           POST's VJP.  Per-item results: the step count K, the cotangent lambda of the final carries (the active
+           ones), the cotangents of the loop's P values, the truncation flag.
+  reverse  PRE (the P values again: the loop constants); the loop j = K-1 .. 0: the state before step j from the
+           tape, BODY's VJP (no primal outputs, so the compiler drops the primal work the transposes do not read:
+           the step-size control of C5, say), lambda -> lambda, the loop constants' cotangents summed; then PRE's
+           VJP: per-item operand cotangents (stored), one exact emit per differentiated broadcast element.  The
+           truncation flag passes through as the program's own, so tm_post poisons every cotangent (reference
+           _primitive.py:586-594).
+
+The tape is one u32 buffer of N x cap x Wp words, item-major (word w of slot k of item i at (i cap + k) Wp + w; Wp
+= the state's words, padded to an even count and moved in 16- or 8-byte units), written by the count launch and
+read by the reverse launch.  Carries that count steps (start at a constant, gain 1 per step) are not stored: before
+step k they are that constant + k.
+cap is a runtime operand: the largest multiple of 16 (at most 1024) that keeps the tape within BUDGET bytes, so the
+kernels do not depend on N.  An item longer than cap steps is reversed exactly all the same: the state before a
+step j >= cap is recomputed from the last stored one (slot cap-1) inside the reverse step, which costs
+(K - cap)^2 / 2 extra steps for that item; the BASELINE configs never take that branch (C3: K <= 71 over 2^18 items,
+cap 80 at N = 4,194,304; C5: K <= 296, cap 512).
+"""
+import dataclasses
+
+import numpy as np
+
+from .. import _ad as AD
+from .. import _core as C
+from .. import lax as L
+from .._api import ItemProgram, TSpec, check_tallies
+from .reverse import ReverseError, _ct_reader
+
+BUDGET = 16 << 30           # bytes of tape per gradient call
+CAP_MAX = 1024
+CAP_MIN = 16
+
+
+def _nwords(dt):
+    return 2 if np.dtype(dt).itemsize == 8 else 1
+
+
+def state_carries(sp):
+    """the loop carries that form a step's state (every carry but the tallies riding through the loop)."""
+    return [j for j, s in enumerate(sp.car_slot) if s is None]
+
+
+def step_counters(sp):
+    """{carry index: c} of the int32 scalar carries that start at the literal c and gain 1 per step (the cap's
+    counter, an item's own step index): before step k such a carry is c + k, so the tape does not store it."""
+    out = {}
+    defs = {e.outvars[0].id: e for e in sp.body.eqns if len(e.outvars) == 1}
+    for j in state_carries(sp):
+        v0, vb, vin = sp.pre.outvars[j], sp.body.outvars[j], sp.body.invars[len(sp.bconst) + j]
+        if not (isinstance(v0, C.Lit) and v0.aval.shape == () and v0.aval.dtype == C.I32 and isinstance(vb, C.Var)):
+            continue
+        e = defs.get(vb.id)
+        if e is None or e.prim != "add":
+            continue
+        a, b = e.invars
+        one = [x for x in (a, b) if isinstance(x, C.Lit) and x.aval.shape == () and int(x.val) == 1]
+        var = [x for x in (a, b) if isinstance(x, C.Var)]
+        if one and var and var[0].id == vin.id:
+            out[j] = int(v0.val)
+    return out
+
+
+def stored_carries(sp):
+    """the state carries the tape stores (step counters are reconstructed from the slot index)."""
+    aff = step_counters(sp)
+    return [j for j in state_carries(sp) if j not in aff]
+
+
+def state_words(sp):
+    """u32 words of one tape slot: the stored state's words, an odd count above 2 padded by one; the slot is then
+    stored and loaded in 16-byte units when its words are a multiple of 4, else in 8-byte units (C5's six words:
+    24 bytes, not 32)."""
+    W = sum(max(1, sp.body.outvars[j].aval.size) * _nwords(sp.body.outvars[j].aval.dtype) for j in stored_carries(sp))
+    return max(1, W) if W <= 2 else W + (W & 1)
+
+
+def tape_cap(N, Wp, want=None):
+    """the tape slots per item at N items (`want`: a caller's choice, clamped to >= 1)."""
+    if want:
+        return max(1, int(want))
+    per = BUDGET // max(1, int(N) * Wp * 4)
+    return int(max(CAP_MIN, min(CAP_MAX, per // 16 * 16)))
+
+
+def _put(tok, k, cap, leaves, Wp):
+    ins = [C.as_var(tok), C.as_var(k), C.as_var(cap)] + [C.as_var(x) for x in leaves]
+    return C.bind("tallymap_tape_put", ins, [tok.aval], words=Wp)[0]
+
+
+def _get(j, cap, avals, Wp):
+    return C.bind("tallymap_tape_get", [C.as_var(j), C.as_var(cap)], list(avals), words=Wp)
+
+
+def _consts(sp, Pv):
+    def cval(ref):
+        kind, x = ref
+        return Pv[x] if kind == "P" else AD._t(x, {})
+    return [cval(r) for r in sp.cconst], [cval(r) for r in sp.bconst]
+
+
+def _never(sp):
+    """the loop split() adds to a loop-free item (it never runs)."""
+    return not sp.cond.eqns and isinstance(sp.cond.outvars[0], C.Lit) and not bool(sp.cond.outvars[0].val)
+
+
+@dataclasses.dataclass
+class TapePrograms:
+    count: ItemProgram
+    reverse: ItemProgram
+    Wp: int
+    n_lam: list             # per active carry j (in order): its cotangent per-item result of `count`
+    n_gp: list              # per P var q with a cotangent from POST: (q, aval)
+
+
+def programs(adj, pl):
+    """-> TapePrograms of adj (reverse.Adjoint) under pl (reverse.Plan); raises ReverseError when no loop carry
+    needs the reverse sweep (the forward-only adjoint applies then)."""
+    if not any(pl.car_act):
+        raise ReverseError("internal: the tape adjoint is for programs with an active loop carry")
+    prog, sp = adj.prog, pl.sp
+    nT, nP, nB = prog.nT, prog.nP, prog.nB
+    pav, bav, yav = prog.p_avals(), prog.b_avals(), prog.y_avals()
+    ft, fy = pl.ft, pl.fy
+    S_of = {k: prog.tallies[k].S for k in ft}
+    nbc = len(sp.bconst)
+    sc = state_carries(sp)
+    stc = stored_carries(sp)
+    aff = step_counters(sp)
+    car_av = [v.aval for v in sp.body.outvars]
+    Wp = state_words(sp)
+    post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, pl.P_act + list(pl.car_act), _ct_reader(ft, S_of),
+                                             {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None})
+    lam_j = [j for j in range(sp.ncar) if pl.car_act[j]]
+    gp_q = [q for q in range(sp.nP) if p_ctin[q]]
+    P_av = [v.aval for v in sp.pre.outvars[sp.ncar:]]
+    disc = [dataclasses.replace(s, kind="discard") for s in prog.tallies]
+    I32, F32 = C.I32, C.F32
+
+    # ------------------------------------------------------------------------------------------ count
+    tspecs = disc + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
+    b = C.Builder()
+    C._STACK.append(b)
+    try:
+        tin = [C.Tracer(b.new_invar(C.AVal((s.S,), s.dtype))) for s in tspecs]
+        pin = [C.Tracer(b.new_invar(a)) for a in pav]
+        cyin = [C.Tracer(b.new_invar(C.AVal(yav[j].shape, F32))) for j in fy]
+        bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
+        ctin = [C.Tracer(b.new_invar(C.AVal((prog.tallies[k].S,), F32))) for k in ft]
+        cap = C.Tracer(b.new_invar(C.AVal((), I32)))
+        ct_read = _ct_reader(ft, S_of, ctin)
+        pre_outs = AD.eval_jaxpr(sp.pre, tin[:nT] + pin + bin_)
+        cars0, Pv = list(pre_outs[:sp.ncar]), list(pre_outs[sp.ncar:])
+        ccv, bcv = _consts(sp, Pv)
+
+        def cond_f(c):
+            return AD.eval_jaxpr(sp.cond, ccv + list(c[0]))[0]
+
+        def body_f(c):
+            cars, k, tok = list(c[0]), c[1], c[2]
+            tok = _put(tok, k, cap, [cars[j] for j in stc], Wp)
+            return (AD.eval_jaxpr(sp.body, bcv + cars), k + 1, tok)
+        tok0 = tin[nT]
+        if sp.ncar and not _never(sp):
+            cars_f, K_, tok = L.while_loop(cond_f, body_f, (cars0, np.int32(0), tok0))
+        else:
+            cars_f, K_, tok = cars0, C.Tracer(C.bind("copy", [C.literal(0, I32, False)], [C.AVal((), I32)])[0].var), tok0
+        cars_f = list(cars_f)
+        post_outs = AD.eval_jaxpr(sp.post, Pv + cars_f)
+        post_cts = []
+        for j, m in enumerate(p_ctout):
+            if m:
+                q = j - nT
+                post_cts.append(cyin[fy.index(q)] if q >= 0 and q in fy else np.float32(0.0))
+        pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read)
+        got, k = {}, 0
+        for q, m in enumerate(p_ctin):
+            if m:
+                got[q] = pv[k]
+                k += 1
+
+        def tracer_of(x, aval):
+            if C.is_traced(x):
+                return x
+            return C.Tracer(C.bind("copy", [C.literal(np.broadcast_to(np.asarray(x, aval.dtype), aval.shape)
+                                                      .copy(), aval.dtype)], [C.AVal(aval.shape, aval.dtype)])[0].var)
+        ys = [tracer_of(K_, C.AVal((), I32))]
+        for j in lam_j:
+            ys.append(tracer_of(got.get(sp.nP + j, np.float32(0.0)), C.AVal(car_av[j].shape, F32)))
+        for q in gp_q:
+            ys.append(tracer_of(got[q], C.AVal(P_av[q].shape, F32)))
+        trunc = None
+        if prog.trunc is not None:
+            ys.append(post_outs[nT + prog.trunc])
+            trunc = len(ys) - 1
+        touts = [C.Tracer(b.local(t.var)) if C.is_traced(t) else t for t in post_outs[:nT]] + [tok]
+        outs = [b.local(t.var) for t in touts] + [b.local(y.var) for y in ys]
+    finally:
+        C._STACK.pop()
+    jx = C.Jaxpr(b.invars, outs, b.eqns)
+    check_tallies(jx, len(tspecs), adj.where)
+    count = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft) + 1, trunc, adj.tag + "-count", adj.where)
+    count.tape_words = Wp
+
+    # ----------------------------------------------------------------------------------------- reverse
+    body_vjp, f_ctout, f_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + list(pl.car_act), _ct_reader(ft, S_of),
+                                             {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
+                                             ct_given=list(pl.car_act))
+    for ci, ca in zip(f_ctin[nbc:], pl.car_act):
+        if ci and not ca:
+            raise ReverseError("internal: carry activity mismatch")
+    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)})
+    gq = [q for q in range(nbc) if f_ctin[q]]
+    tspecs = disc + [TSpec(f"ct{j}", tuple(bav[j].shape) or (1,), np.dtype(np.float32), exact=True)
+                     for j in adj.wrt_bc]
+    b = C.Builder()
+    C._STACK.append(b)
+    try:
+        tin = [C.Tracer(b.new_invar(C.AVal((s.S,), s.dtype))) for s in tspecs]
+        pin = [C.Tracer(b.new_invar(a)) for a in pav]
+        cyin = [C.Tracer(b.new_invar(C.AVal(yav[j].shape, F32))) for j in fy]
+        kin = C.Tracer(b.new_invar(C.AVal((), I32)))
+        lamin = [C.Tracer(b.new_invar(C.AVal(car_av[j].shape, F32))) for j in lam_j]
+        gpin = [C.Tracer(b.new_invar(C.AVal(P_av[q].shape, F32))) for q in gp_q]
+        trin = C.Tracer(b.new_invar(C.AVal((), C.BOOL))) if prog.trunc is not None else None
+        bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
+        ctin = [C.Tracer(b.new_invar(C.AVal((prog.tallies[k].S,), F32))) for k in ft]
+        cap = C.Tracer(b.new_invar(C.AVal((), I32)))
+        ct_read = _ct_reader(ft, S_of, ctin)
+        pre_outs = AD.eval_jaxpr(sp.pre, tin[:nT] + pin + bin_)
+        cars0, Pv = list(pre_outs[:sp.ncar]), list(pre_outs[sp.ncar:])
+        ccv, bcv = _consts(sp, Pv)
+        st_av = [car_av[j] for j in stc]
+        tcj = [j for j in range(sp.ncar) if sp.car_slot[j] is not None]     # the tallies riding through the loop
+
+        def assemble(st, tc):
+            cars = [None] * sp.ncar
+            for j, x in zip(sc, st):
+                cars[j] = x
+            for j, x in zip(tcj, tc):
+                cars[j] = x
+            return cars
+
+        def rcond(c):
+            return c[0] >= 0
+
+        def rbody(c):
+            j, lam, gk, tc = c[0], list(c[1]), list(c[2]), list(c[3])
+            jj = L.min(j, cap - 1)
+            got_ = dict(zip(stc, _get(jj, cap, st_av, Wp)))
+            st = [got_[q] if q in got_ else jj + aff[q] for q in sc]
+
+            def recompute(s, t):
+                def step(_, x):
+                    o = AD.eval_jaxpr(sp.body, bcv + assemble(list(x[0]), list(x[1])))
+                    return [o[q] for q in sc], [o[q] for q in tcj]
+                return L.fori_loop(0, j - jj, step, (list(s), list(t)))
+            st, tc = L.cond(j > jj, recompute, lambda s, t: (list(s), list(t)), list(st), tc)
+            st, tc = list(st), list(tc)
+            cts = []
+            it = iter(lam)
+            for jc, m in enumerate(f_ctout):
+                if m:
+                    cts.append(next(it) if pl.car_act[jc] else np.zeros(car_av[jc].shape, np.float32)[()])
+            vj = AD.eval_jaxpr(body_vjp, bcv + assemble(st, tc) + cts, ct_read)
+            k2, newlam, newgk = 0, {}, []
+            for q, m in enumerate(f_ctin):
+                if not m:
+                    continue
+                if q < nbc:
+                    newgk.append(vj[k2])
+                else:
+                    newlam[q - nbc] = vj[k2]
+                k2 += 1
+            lam2 = [newlam.get(jc, np.zeros(car_av[jc].shape, np.float32)[()]) for jc in lam_j]
+            gk2 = [g + d for g, d in zip(gk, newgk)]
+            return j - 1, lam2, gk2, tc
+        g0 = [np.zeros(sp.body.invars[q].aval.shape, np.float32)[()] for q in gq]
+        tc0 = [cars0[j] for j in tcj]
+        if sp.ncar and not _never(sp):
+            _, lam_f, gk_f, tc_f = L.while_loop(rcond, rbody, (kin - 1, list(lamin), g0, tc0))
+        else:
+            lam_f, gk_f, tc_f = list(lamin), g0, tc0
+        lam_f, gk_f, tc_f = list(lam_f), list(gk_f), list(tc_f)
+        gP = {q: g for q, g in zip(gp_q, gpin)}
+        for kk, q in enumerate(gq):                 # the body constants' step sums onto their P var
+            r = sp.bconst[q]
+            if r[0] == "P":
+                gP[r[1]] = gk_f[kk] if r[1] not in gP else gP[r[1]] + gk_f[kk]
+        lam_of = dict(zip(lam_j, lam_f))
+        pre_cts = []
+        for j, (o, m) in enumerate(zip(sp.pre.outvars, r_ctout)):
+            if m:
+                z = np.zeros(o.aval.shape, np.float32)[()]
+                pre_cts.append(lam_of.get(j, z) if j < sp.ncar else gP.get(j - sp.ncar, z))
+        gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read)
+        g_pi, g_bc, k = {}, {}, 0
+        for q, m in enumerate(r_ctin):
+            if m:
+                if nT <= q < nT + nP:
+                    g_pi[q - nT] = gr[k]
+                elif q >= nT + nP:
+                    g_bc[q - nT - nP] = gr[k]
+                k += 1
+        ct_t = []
+        for jj_, j in enumerate(adj.wrt_bc):
+            t = tin[nT + jj_]
+            v = g_bc.get(j)
+            for e in range(max(1, bav[j].size)):
+                if v is None:
+                    continue
+                ve = v if (not C.is_traced(v) or v.shape == ()) else v[e]
+                vv = ve.var if C.is_traced(ve) else C.literal(np.float32(ve), F32, False)
+                t = C.bind("tallymap_emit", [t.var, C.literal(e, I32, False), vv], [t.aval])[0]
+            ct_t.append(t)
+        ys = []
+        for i in adj.wrt_pi:
+            v = g_pi.get(i)
+            if v is None or not C.is_traced(v):
+                v = C.Tracer(C.bind("copy", [C.literal(np.zeros(pav[i].shape, np.float32), F32)],
+                                    [C.AVal(pav[i].shape, F32)])[0].var)
+            ys.append(v)
+        trunc = None
+        if trin is not None:
+            ys.append(trin)
+            trunc = len(ys) - 1
+        by_slot = {sp.car_slot[j]: x for j, x in zip(tcj, tc_f)}
+        touts = [by_slot[k] for k in range(nT)] + ct_t
+        outs = [b.local(t.var) for t in touts] + [b.local(y.var) for y in ys]
+    finally:
+        C._STACK.pop()
+    jx = C.Jaxpr(b.invars, outs, b.eqns)
+    check_tallies(jx, len(tspecs), adj.where)
+    nPr = nP + len(fy) + 1 + len(lam_j) + len(gp_q) + (1 if trin is not None else 0)
+    rev = ItemProgram(jx, tuple(tspecs), nPr, nB + len(ft) + 1, trunc, adj.tag + "-reverse", adj.where)
+    rev.poison_ys = True
+    rev.tape_words = Wp
+    return TapePrograms(count, rev, Wp, lam_j, [(q, P_av[q]) for q in gp_q])

@@ -26,6 +26,10 @@ typedef int i32;
 typedef unsigned int u32;
 typedef long long i64;
 typedef unsigned long long u64;
+#if defined(__clang__)
+typedef u32 tm_u32x4 __attribute__((ext_vector_type(4)));     // a 16-byte unit (one dwordx4 load / store)
+typedef u32 tm_u32x2 __attribute__((ext_vector_type(2)));     // an 8-byte unit
+#endif
 
 #ifdef __HIPCC_RTC__
 #define TM_DEVICE_ONLY 1

@@ -239,40 +239,39 @@ TM_FN float tm_expf(float x) {
 }
 
 // ------------------------------------------------------------------------------------------ sinf / cosf
-struct TmSinCos {
-  double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3;
-};
-TM_FN const TmSinCos& tm_sincos_table(int which) {
-  static const TmSinCos T[2] = {
-      {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, 0x1p0, -0x1.ffffffd0c621cp-2,
-       0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
-       0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
-      {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, -0x1p0, 0x1.ffffffd0c621cp-2,
-       -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
-       0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13}};
-  return T[which];
-}
-TM_FN float tm_sc_poly(double x, double x2, const TmSinCos& p, int n) {
+// ARM's __sincosf_table[0] as constants.  Its second table is the same with the cosine coefficients c0..c4 negated,
+// and a polynomial with every coefficient negated gives exactly the negated result (each fma and the final rounding
+// are symmetric under negation), so the device keeps one constant set and flips the sign of the cosine result
+// instead of selecting a table per lane: a per-lane table address turns every coefficient into a global load.
+constexpr double TM_SC_HPI_INV = 0x1.45F306DC9C883p+23, TM_SC_HPI = 0x1.921FB54442D18p0;
+constexpr double TM_SC_C0 = 0x1p0, TM_SC_C1 = -0x1.ffffffd0c621cp-2, TM_SC_C2 = 0x1.55553e1068f19p-5,
+                 TM_SC_C3 = -0x1.6c087e89a359dp-10, TM_SC_C4 = 0x1.99343027bf8c3p-16;
+constexpr double TM_SC_S1 = -0x1.555545995a603p-3, TM_SC_S2 = 0x1.1107605230bc4p-7, TM_SC_S3 = -0x1.994eb3774cf24p-13;
+// the table's sign[n & 3] = {1, -1, -1, 1}: -1 when bits 0 and 1 of n differ
+TM_FN double tm_sc_sign(int n) { return ((n ^ (n >> 1)) & 1) ? -1.0 : 1.0; }
+// n even: the sine polynomial; n odd: the cosine polynomial, negated when `flip` (the second table)
+TM_FN float tm_sc_poly(double x, double x2, int n, bool flip) {
   if ((n & 1) == 0) {
     const double x3 = x * x2;
-    const double s1 = __builtin_fma(x2, p.s3, p.s2);
+    const double s1 = __builtin_fma(x2, TM_SC_S3, TM_SC_S2);
     const double x7 = x3 * x2;
-    const double s = __builtin_fma(x3, p.s1, x);
+    const double s = __builtin_fma(x3, TM_SC_S1, x);
     return (float)__builtin_fma(x7, s1, s);
   }
   const double x4 = x2 * x2;
-  const double c2 = __builtin_fma(x2, p.c4, p.c3);
-  const double c1 = __builtin_fma(x2, p.c1, p.c0);
+  const double c2 = __builtin_fma(x2, TM_SC_C4, TM_SC_C3);
+  const double c1 = __builtin_fma(x2, TM_SC_C1, TM_SC_C0);
   const double x6 = x4 * x2;
-  const double c = __builtin_fma(x4, p.c2, c1);
-  return (float)__builtin_fma(x6, c2, c);
+  const double c = __builtin_fma(x4, TM_SC_C2, c1);
+  const float r = (float)__builtin_fma(x6, c2, c);
+  return flip ? -r : r;
 }
 // |x| < 120: n = round(x 2/pi) (through 2^24-scaled integer arithmetic), x - n pi/2 with one fma
-TM_FN double tm_sc_reduce_fast(double x, const TmSinCos& p, int* np) {
-  const double r = x * p.hpi_inv;
+TM_FN double tm_sc_reduce_fast(double x, int* np) {
+  const double r = x * TM_SC_HPI_INV;
   const int n = ((i32)r + 0x800000) >> 24;
   *np = n;
-  return __builtin_fma(-(double)n, p.hpi, x);
+  return __builtin_fma(-(double)n, TM_SC_HPI, x);
 }
 // |x| >= 120: x (4/pi) mod 4 in 64-bit fixed point from a 2/pi bit table
 TM_FN double tm_sc_reduce_large(u32 xi, int* np) {
@@ -300,19 +299,19 @@ TM_FN float tm_sinf(float y) {
   int n;
   if (tm_abstop12(y) < tm_abstop12(0x1.921FB6p-1f)) {
     if (tm_abstop12(y) < tm_abstop12(0x1p-12f)) return y;
-    return tm_sc_poly(x, x * x, tm_sincos_table(0), 0);
+    return tm_sc_poly(x, x * x, 0, false);
   }
   if (tm_abstop12(y) < tm_abstop12(120.0f)) {
-    x = tm_sc_reduce_fast(x, tm_sincos_table(0), &n);
-    const double s = tm_sincos_table(0).sign[n & 3];
-    return tm_sc_poly(x * s, x * x, tm_sincos_table((n & 2) ? 1 : 0), n);
+    x = tm_sc_reduce_fast(x, &n);
+    const double s = tm_sc_sign(n);
+    return tm_sc_poly(x * s, x * x, n, (n & 2) != 0);
   }
   if (tm_abstop12(y) < tm_abstop12(__builtin_inff())) {
     const u32 xi = tm_f2u(y);
     const int sign = (int)(xi >> 31);
     x = tm_sc_reduce_large(xi, &n);
-    const double s = tm_sincos_table(0).sign[(n + sign) & 3];
-    return tm_sc_poly(x * s, x * x, tm_sincos_table(((n + sign) & 2) ? 1 : 0), n);
+    const double s = tm_sc_sign(n + sign);
+    return tm_sc_poly(x * s, x * x, n, ((n + sign) & 2) != 0);
   }
   return y - y;
 }
@@ -321,19 +320,19 @@ TM_FN float tm_cosf(float y) {
   int n;
   if (tm_abstop12(y) < tm_abstop12(0x1.921FB6p-1f)) {
     if (tm_abstop12(y) < tm_abstop12(0x1p-12f)) return 1.0f;
-    return tm_sc_poly(x, x * x, tm_sincos_table(0), 1);
+    return tm_sc_poly(x, x * x, 1, false);
   }
   if (tm_abstop12(y) < tm_abstop12(120.0f)) {
-    x = tm_sc_reduce_fast(x, tm_sincos_table(0), &n);
-    const double s = tm_sincos_table(0).sign[n & 3];
-    return tm_sc_poly(x * s, x * x, tm_sincos_table((n & 2) ? 1 : 0), n ^ 1);
+    x = tm_sc_reduce_fast(x, &n);
+    const double s = tm_sc_sign(n);
+    return tm_sc_poly(x * s, x * x, n ^ 1, (n & 2) != 0);
   }
   if (tm_abstop12(y) < tm_abstop12(__builtin_inff())) {
     const u32 xi = tm_f2u(y);
     const int sign = (int)(xi >> 31);
     x = tm_sc_reduce_large(xi, &n);
-    const double s = tm_sincos_table(0).sign[(n + sign) & 3];
-    return tm_sc_poly(x * s, x * x, tm_sincos_table(((n + sign) & 2) ? 1 : 0), n ^ 1);
+    const double s = tm_sc_sign(n + sign);
+    return tm_sc_poly(x * s, x * x, n ^ 1, ((n + sign) & 2) != 0);
   }
   return y - y;
 }

@@ -39,18 +39,24 @@ def test_c1_grad_theta(oracle):
     assert abs(got - closed) <= GTOL * abs(closed)
 
 
-VARIANTS = [dict(), dict(rev_tape=4), dict(rev_tape=2), dict(rev_refill=1), dict(rev_refill=64),
+VARIANTS = [dict(), dict(rev_tape=4), dict(rev_tape=2), dict(rev_tape=1), dict(schedule="item"),
+            dict(rev_schedule="step"), dict(rev_schedule="step", rev_tape=4), dict(rev_schedule="step", rev_tape=2),
+            dict(rev_schedule="step", rev_refill=1), dict(rev_schedule="step", rev_refill=64),
             dict(rev_schedule="item"), dict(rev_schedule="item", rev_checkpoints=4),
             dict(rev_schedule="item", rev_checkpoints=1)]
 
 
-@pytest.mark.parametrize("opts", VARIANTS, ids=["step", "tape4", "tape2", "refill1", "refill64", "item16", "item4",
-                                                "item1"])
+@pytest.mark.parametrize("opts", VARIANTS, ids=["tape", "tape4", "tape2", "tape1", "tape-itemsched", "step",
+                                                "step-tape4", "step-tape2", "step-refill1", "step-refill64", "item16",
+                                                "item4", "item1"])
 def test_c1_grad_xs_and_replay_variants(oracle, opts):
     """cotangents of xs (per item, through the loop state: the replay) and of theta with weights ct, against the
-    oracle; the replay variants -- the step-scheduled tape (an ~8-step item overflows a 4- or 2-slot tape into the
-    checkpointed sweep; waves refilled by 1 or 64 free lanes) and the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its segment
-    re-runs) -- give bitwise the same per-item cotangents and broadcast cotangent (reference tests/reverse.py:216)."""
+    oracle; the replay variants give bitwise the same per-item cotangents and broadcast cotangent (reference
+    tests/reverse.py:216): the two-launch tape adjoint (the default; a 4-, 2- or 1-slot tape makes the ~8-step
+    items recompute the states past the tape inside the reverse step; the item schedule of the forward template),
+    the single-kernel step-scheduled replay (an item overflowing a 4- or 2-slot tape takes the checkpointed sweep;
+    waves refilled by 1 or 64 free lanes) and the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its
+    segment re-runs)."""
     print(f"case: C1 vjp (xs, theta) {opts}", flush=True)
     xs, keys, theta = configs.c1_inputs()
     ct = np.linspace(0.5, 2.0, 16).astype(np.float32)
