@@ -25,10 +25,13 @@
  * Every float tally also gets a float64 shadow sum of the same emits: the re-summation the tolerances are
  * measured against.
  *
- * Pinned by tests/test_oracle.py (known answers, closed forms, special cases, scipy) except where noted:
- *   PARITY UNPINNED: fold_in / split / uniform / normal layering on the threefry core (JAX's partitionable PRNG;
- *   JAX is absent here: pinned only by agreement with the independent numpy restatement in tallymap_amd.random);
- *   c3_item's forward-mode gradient with scattering (pinned through its mu_s = 0 special case only).
+ * Pinned by tests/test_oracle.py (known answers, closed forms, special cases, brute force, scipy) except where
+ * noted.  Config 2: a pure-Python walker with an independent normal() (trip counts and counts bitwise), the
+ * drifted-Brownian exit laws with Siegmund's overshoot correction, N(0, 1) moments and a KS test of normal().
+ * Config 3's gradient with scattering: photon by photon against the float64 closed form along the frozen path.
+ *   PARITY UNPINNED: fold_in / split / uniform / normal LAYERING on the threefry core (which counters and keys
+ *   JAX's partitionable PRNG feeds threefry): JAX is absent here, and its restatements (this file, the numpy one in
+ *   tallymap_amd.random, the Python one in tests/test_oracle.py) agree with each other only.
  */
 #include <fenv.h>
 #include <math.h>

@@ -186,10 +186,13 @@ def objdump():
 def shift_hazards(img):
     """[(kernel, instruction)]: the 64-bit VALU shifts (v_lshlrev_b64, v_lshrrev_b64, v_ashrrev_i64) of code object
     `img` whose shift amount is in a VGPR v(8k+7), the last register of an allocation block, which gfx950 executes
-    wrongly (the device runtime's 32-bit-half shifts avoid them).  None when llvm-objdump is not installed."""
+    wrongly (the device runtime's 32-bit-half shifts avoid them).  Raises when llvm-objdump is not installed: an
+    unchecked code object is refused, never accepted."""
     tool = objdump()
     if tool is None:
-        return None
+        raise BackendError("tallymap_amd: llvm-objdump (ROCm's, under $ROCM_PATH/llvm/bin or /opt/rocm/llvm/bin) is "
+                           "needed to check a new code object for the gfx950 64-bit shift hazard; refusing to use an "
+                           "unchecked one")
     import tempfile
     with tempfile.NamedTemporaryFile(suffix=".co") as fh:
         fh.write(img)

@@ -23,6 +23,29 @@
 //              fdlibm's float atanf / atan2f (Sun, freely redistributable) in float arithmetic, in glibc's form
 //              (atanf returns +-pi/2 from |x| >= 2^25).  Checked bitwise against glibc on all 2^32 atanf arguments
 //              and on random atan2f pairs over the full exponent range.
+//
+// Upstream notices of the restated code (the logf / expf / sinf / cosf reductions, tables and polynomial
+// coefficients, and the atanf / atan2f code and coefficients):
+//
+//   ARM optimized-routines (math/logf.c, math/expf.c, math/sinf.c, math/cosf.c and their data files):
+//     Copyright (c) 2017-2022, Arm Limited.
+//     SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception.  Used here under the MIT license:
+//     Permission is hereby granted, free of charge, to any person obtaining a copy of this software and
+//     associated documentation files (the "Software"), to deal in the Software without restriction, including
+//     without limitation the rights to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+//     copies of the Software, and to permit persons to whom the Software is furnished to do so, subject to the
+//     following conditions: The above copyright notice and this permission notice shall be included in all copies
+//     or substantial portions of the Software.  THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND,
+//     EXPRESS OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY, FITNESS FOR A PARTICULAR
+//     PURPOSE AND NONINFRINGEMENT.  IN NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM,
+//     DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM, OUT OF OR IN
+//     CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE SOFTWARE.
+//
+//   fdlibm (s_atanf.c, e_atan2f.c; float versions by Ian Lance Taylor, Cygnus Support):
+//     Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//     Developed at SunPro, a Sun Microsystems, Inc. business.
+//     Permission to use, copy, modify, and distribute this software is freely granted, provided that this notice
+//     is preserved.
 #pragma once
 
 // w = -log(t) for erf_inv, t = (1 - a)(1 + a) in [2^-24, 1]: t = 2^k z, z in [0x1.6ap-1, 0x1.6ap0) split into 64

@@ -8,6 +8,9 @@
 //   libm_check f32 <fn> <stride> <offset>
 //                              logf / expf / sinf / cosf / atanf on every stride-th f32 bit pattern from offset
 //                              (stride 1: all 2^32): bitwise mismatches and the largest ulp distance
+//   libm_check uniform         every f32 that jax.random.uniform(key) produces (2^23 values u in [0, 1)), through
+//                              the argument forms the configs use: logf(1 - u) (the slab's free path) and
+//                              sinf / cosf(f32(2 pi) u) (the azimuths of the slab and of walk on spheres): bitwise
 //   libm_check atan2 <n> <seed>
 //                              n random (y, x) pairs of finite f32 over the full exponent range: tm_atan2f vs glibc
 #include <cmath>
@@ -33,6 +36,20 @@ static float ref_erfinvf(float y) {
   return y == 0.0f ? y : (float)copysign(ref_giles(y), (double)y); }
 
 int main(int argc, char** argv) {
+  if (argc > 1 && !strcmp(argv[1], "uniform")) {
+    long n = 0, bad = 0;
+    const float twopi = (float)(2.0 * M_PI);
+    for (uint32_t m = 0; m < (1u << 23); ++m) {
+      const float u = tm_fmax(0.0f, (tm_u2f(m | 0x3f800000u) - 1.0f) * 1.0f + 0.0f);
+      const float a = 1.0f - u, phi = twopi * u;
+      n += 3;
+      if (tm_f2u(tm_logf(a)) != tm_f2u(logf(a))) { if (++bad < 10) printf("  logf(%a)\n", a); }
+      if (tm_f2u(tm_sinf(phi)) != tm_f2u(sinf(phi))) { if (++bad < 10) printf("  sinf(%a)\n", phi); }
+      if (tm_f2u(tm_cosf(phi)) != tm_f2u(cosf(phi))) { if (++bad < 10) printf("  cosf(%a)\n", phi); }
+    }
+    printf("uniform: %ld arguments, %ld mismatches\n", n, bad);
+    return bad != 0;
+  }
   if (argc > 1 && !strcmp(argv[1], "erfinv_normal")) {
     const float lo = tm_u2f(0xbf7fffffu), span = 1.0f - lo;
     long n = 0, bad = 0, logdiff = 0;

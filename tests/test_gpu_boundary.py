@@ -39,3 +39,31 @@ def test_tallymap_kernel_info_after_launch():
     assert occ * block * cus == info["resident_threads"]
     assert per_cu >= occ * block and cus >= 1
     assert had in (0, 1)       # (1 when an earlier test launched the same module at this block size)
+
+
+def test_launch_refuses_a_program_past_the_private_segment_limit():
+    """a module whose item loop needs more than 64 KiB of private (scratch) memory per lane is refused by tm_launch
+    before anything is queued, with a message naming the figure (reference shim.cc:97-121 explains such a
+    launch's out-of-memory failure; here it never gets that far).  The kernel itself is in bounds for any lane."""
+    import torch
+    print("case: tm_launch of a 96 KiB-per-lane private array (refused before launch)", flush=True)
+    src = ("struct TmParams { void* p[1]; };\n"
+           "extern \"C\" __global__ void tm_main(const TmParams P, const long long n) {\n"
+           "  volatile float a[24576];\n"
+           "  const unsigned i = threadIdx.x % 24576u;\n"
+           "  a[i] = 1.0f;\n"
+           "  ((float*)P.p[0])[0] = a[(i * 7u) % 24576u];\n"
+           "}\n")
+    img = Cm.code_object(src, name="tm_private.hip")
+    lib = Cm.lib()
+    kid = 0x7e57_0001
+    Cm.check(lib.tm_register(kid, img, len(img), b"private-segment probe"))
+    out = (ctypes.c_longlong * 8)()
+    Cm.check(lib.tm_kernel_info(kid, 64, out))
+    assert out[1] > 65536
+    buf = torch.zeros(4, dtype=torch.float32, device="cuda")
+    bufs = (ctypes.c_void_p * 1)(buf.data_ptr())
+    rc = lib.tm_launch(kid, None, bufs, 1, 0, 0, 64, 64)
+    assert rc != 0 and b"private bytes per lane" in lib.tm_last_error()
+    torch.cuda.synchronize()
+    assert float(buf.sum().item()) == 0.0

@@ -227,3 +227,19 @@ def test_fmod_matches_glibc(tmp_path):
     bad, tot = map(int, r.stdout.split()[-2:])
     assert bad == 0 and tot > 8_000_000
 
+
+def test_uniform_derived_arguments_match_glibc(libm):
+    """every argument the configs hand to logf / sinf / cosf from a uniform draw -- logf(1 - u), sinf / cosf(2 pi u)
+    for all 2^23 values jax.random.uniform produces -- bitwise glibc's results."""
+    r = subprocess.run([libm, "uniform"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+    assert f"uniform: {3 * 8388608} arguments, 0 mismatches" in r.stdout
+
+
+def test_shift_hazard_check_refuses_without_objdump(monkeypatch):
+    """with no llvm-objdump the shift-hazard check refuses the code object instead of passing it unchecked."""
+    from tallymap_amd.backend import compile as Cm
+    monkeypatch.setattr(Cm, "objdump", lambda: None)
+    with pytest.raises(Cm.BackendError, match="refusing"):
+        Cm.shift_hazards(b"\x7fELF")
+

@@ -377,3 +377,205 @@ def test_c5_gradient_matches_finite_differences(oracle):
         dy = (y[0] - y[1]) / (2 * h)
         want = float(ct[i].astype(np.float64) @ dy)
         assert abs(float(g) - want) <= 2e-3 * abs(want), (i, float(g), want)
+
+
+# ------------------------------------------------------------------------------- C2 and C3 pins (second pass)
+def _libm():
+    import ctypes
+    lm = ctypes.CDLL("libm.so.6")
+    for fn in ("logf", "sinf", "cosf"):
+        getattr(lm, fn).restype = ctypes.c_float
+        getattr(lm, fn).argtypes = [ctypes.c_float]
+    return lm
+
+
+def _giles_f32(y):
+    """f32 erf_inv as the reference's CPU target defines it (host.py:102-132): Giles (2010)'s polynomial in double
+    with glibc's log and sqrt (CPython's math module calls them), rounded once to f32."""
+    import math
+    y = float(y)
+    if y == 0.0:
+        return np.float32(y)
+    a = abs(y)
+    w = -math.log((1.0 - a) * (1.0 + a))
+    if w < 5.0:
+        w -= 2.5
+        p = 2.81022636e-08
+        for c in (3.43273939e-07, -3.5233877e-06, -4.39150654e-06, 0.00021858087, -0.00125372503, -0.00417768164,
+                  0.246640727, 1.50140941):
+            p = c + p * w
+    else:
+        w = math.sqrt(w) - 3.0
+        p = -0.000200214257
+        for c in (0.000100950558, 0.00134934322, -0.00367342844, 0.00573950773, -0.0076224613, 0.00943887047,
+                  1.00167406, 2.83297682):
+            p = c + p * w
+    return np.float32(math.copysign(p * a, y))
+
+
+def _normal_py(key):
+    """jax.random.normal(key) (partitionable threefry, f32) restated in Python: one 32-bit draw, the open-interval
+    uniform on (nextafter(-1, 0), 1), sqrt(2) erf_inv."""
+    from tallymap_amd import random as R
+    f = np.float32
+    b = np.uint32(R.bits(key))
+    fl = (np.array(b >> np.uint32(9), np.uint32) | np.uint32(0x3F800000)).view(np.float32)[()] - f(1.0)
+    lo = np.array(0xBF7FFFFF, np.uint32).view(np.float32)[()]
+    u = max(lo, f(f(fl * f(f(1.0) - lo)) + lo))
+    return f(f(np.sqrt(2.0)) * _giles_f32(u))
+
+
+def _c2_python(x0, keys, drift, M=65536):
+    """brute-force Python walker of config 2 on numpy float32 scalars: trip counts, occupancy and wall counts."""
+    from tallymap_amd import random as R
+    f = np.float32
+    occ, wall, ks = np.zeros(128, np.int64), np.zeros(2, np.int64), []
+    for i in range(len(x0)):
+        x, k = f(x0[i]), 0
+        while k < M and x >= f(0.0) and x <= f(1.0):
+            b = int(np.trunc(f(x * f(128.0))))
+            if 0 <= b < 128:
+                occ[b] += 1
+            n = _normal_py(R.fold_in(keys[i], k))
+            x = f(x + f(f(drift) + f(f(0.02) * n)))
+            k += 1
+        wall[int(x > f(1.0))] += 1
+        ks.append(k)
+    return occ, wall, np.array(ks)
+
+
+def test_c2_oracle_brute_force(oracle):
+    """config 2 on 200 items: trip counts and the occupancy and wall counts of the oracle equal a pure-Python walker
+    whose normal draws are restated independently (threefry bits -> open-interval uniform -> Giles erf_inv in
+    double with glibc's log), exactly."""
+    from tallymap_amd import configs
+    x0, keys, drift = configs.c2_inputs(200)
+    occ, wall, ks = _c2_python(x0, keys, drift)
+    r = oracle.c2_fwd(x0, keys, drift)
+    assert np.array_equal(r.per_item, ks)
+    assert np.array_equal(r.tallies64["occ"], occ.astype(np.float64))
+    assert np.array_equal(r.tallies64["wall"], wall.astype(np.float64))
+
+
+def test_c2_oracle_follows_the_drifted_brownian_exit_laws(oracle):
+    """the walk x += mu + sigma N(0, 1) (mu = 1e-3, sigma = 0.02) absorbed outside [0, 1]: over 65,536 items, the
+    fraction absorbed at 1 and the mean trip count agree with Brownian motion with drift on the interval widened by
+    Siegmund's overshoot correction rho sigma at each end (rho = -zeta(1/2) / sqrt(2 pi) = 0.5826: the mean excess of
+    a Gaussian random walk over a boundary), P1(y) = (1 - e^(-2 mu y / sigma^2)) / (1 - e^(-2 mu L / sigma^2)),
+    E[T] = (L P1(y) - y) / mu with L = 1 + 2 rho sigma, y = x0 + rho sigma, averaged over the items' own x0: within
+    5 standard errors plus 0.5 % (what the correction leaves of the discretisation).  A normal draw of the wrong
+    width (a missing sqrt(2), say) moves the mean trip count by a factor 2."""
+    from tallymap_amd import configs
+    n = 65_536
+    x0, keys, drift = configs.c2_inputs(n)
+    r = oracle.c2_fwd(x0, keys, drift)
+    assert not r.trunc.any()
+    mu, sig, rho = 1e-3, 0.02, 0.5825971579390106
+    L, y = 1.0 + 2 * rho * sig, x0.astype(np.float64) + rho * sig
+    c = 2 * mu / sig ** 2
+    p1 = -np.expm1(-c * y) / -np.expm1(-c * L)
+    et = (L * p1 - y) / mu
+    k = r.per_item.astype(np.float64)
+    se = k.std() / np.sqrt(n)
+    assert abs(k.mean() - et.mean()) <= 5 * se + 0.005 * et.mean(), (k.mean(), et.mean(), se)
+    w1 = r.tallies64["wall"][1] / n
+    assert abs(w1 - p1.mean()) <= 5 * np.sqrt(p1.mean() * (1 - p1.mean()) / n) + 0.005, (w1, p1.mean())
+
+
+def test_normal_draws_are_standard_normal(oracle):
+    """2^20 draws of the oracle's normal(): mean 0 and variance 1 within 5 standard errors, and a Kolmogorov-Smirnov
+    test against N(0, 1) with p > 1e-4 (a draw scaled by sqrt(2) or shifted by half a unit fails all three)."""
+    from scipy import stats
+    from tallymap_amd import random as R
+    n = 1 << 20
+    z = np.array([oracle.normal(k) for k in R.split(R.PRNGKey(11), n)], np.float64)
+    assert abs(z.mean()) <= 5 / np.sqrt(n)
+    assert abs(z.var() - 1.0) <= 5 * np.sqrt(2.0 / n)
+    assert stats.kstest(z, "norm").pvalue > 1e-4
+    ks = R.split(R.PRNGKey(11), 64)
+    assert np.array_equal(np.array([_normal_py(k) for k in ks], np.float32),
+                          np.array([oracle.normal(k) for k in ks], np.float32))
+
+
+def _c3_python(key, mu_a, lm, M=1024):
+    """one photon of config 3 on numpy float32 scalars, with glibc's logf / sinf / cosf (ctypes), in the item's own
+    operation order -> (deposits [(flat bin or -1, step k, roulette survivals before it, f32 value)], steps)."""
+    from tallymap_amd import random as R
+    f = np.float32
+    mu_a = f(mu_a)
+    mu_t = f(mu_a + f(0.9))
+    frac, alb = f(mu_a / mu_t), f(f(0.9) / mu_t)
+    p, d, w, k, rs = [f(0.0)] * 3, [f(0.0), f(0.0), f(1.0)], f(1.0), 0, 0
+    deps = []
+    while k < M and w > f(0.0):
+        u = R.uniform(R.fold_in(key, k), (4,))
+        s = f(f(-f(lm.logf(f(f(1.0) - u[0])))) / mu_t)
+        p = [f(p[i] + f(s * d[i])) for i in range(3)]
+        esc = p[2] < f(0.0) or p[2] > f(5.0)
+        rr = np.sqrt(f(f(p[0] * p[0]) + f(p[1] * p[1])))
+        iz, ir = int(np.trunc(f(p[2] * f(12.8)))), int(np.trunc(f(rr * f(12.8))))
+        iz = -1 if esc else iz
+        deps.append((iz * 64 + ir if (0 <= iz < 64 and 0 <= ir < 64) else -1, k, rs, f(w * frac)))
+        w = f(w * alb)
+        tmp = f(f(0.36) / f(f(0.2) + f(f(1.6) * u[1])))
+        cost = f(f(f(1.64) - f(tmp * tmp)) / f(1.6))
+        sint = np.sqrt(max(f(0.0), f(f(1.0) - f(cost * cost))))
+        phi = f(f(6.2831855) * u[2])
+        cp, sp = f(lm.cosf(phi)), f(lm.sinf(phi))
+        ux, uy, uz = d
+        temp = np.sqrt(max(f(0.0), f(f(1.0) - f(uz * uz))))
+        if abs(uz) > f(0.99999):
+            d = [f(sint * cp), f(sint * sp), f(np.sign(uz) * cost)]
+        else:
+            d = [f(f(f(sint * f(f(f(ux * uz) * cp) - f(uy * sp))) / temp) + f(ux * cost)),
+                 f(f(f(sint * f(f(f(uy * uz) * cp) + f(ux * sp))) / temp) + f(uy * cost)),
+                 f(f(f(-sint * cp) * temp) + f(uz * cost))]
+        if w < f(0.01):
+            if u[3] < f(0.1):
+                w, rs = f(w * f(10.0)), rs + 1
+            else:
+                w = f(0.0)
+        if esc:
+            w = f(0.0)
+        k += 1
+    return deps, k
+
+
+def test_c3_gradient_with_scattering_is_the_pathwise_closed_form(oracle):
+    """config 3 at its parameters (mu_a = 0.1, mu_s = 0.9, g = 0.8), photon by photon (300 of them): the oracle's
+    forward deposits equal a pure-Python restatement of the photon's path (glibc logf / sinf / cosf, float32
+    arithmetic in the item's order) bitwise, and its forward-mode d/d mu_a of sum ct[bin] x deposit equals the
+    float64 closed form along that frozen path within 1e-4 (of the terms' magnitudes): deposit k is
+    10^r_k mu_a mu_s^k / mu_t^(k+1) (r_k the roulette survivals before it), so its derivative is
+    10^r_k mu_s^k (1 / mu_t^(k+1) - (k + 1) mu_a / mu_t^(k+2)); positions, bins, escapes and roulette decisions are
+    piecewise constant in mu_a and contribute nothing pathwise (reference tests/reverse.py:280 checks such
+    gradients by agreement of independent derivations)."""
+    from tallymap_amd import configs
+    lm = _libm()
+    keys, mu_a = configs.c3_inputs(1 << 16)
+    # 280 photons, plus 20 of the few that reach Russian roulette (w = 0.9^k < 0.01 from k = 44) and survive it
+    K = oracle.c3_fwd(keys, mu_a).per_item
+    pick = list(range(280)) + [int(i) for i in np.flatnonzero(K > 46)[:20]]
+    mu_a, mu_s = float(np.float32(mu_a)), 0.9
+    mu_t = mu_a + mu_s
+    ct2 = (1.0 + np.arange(64 * 64) % 7 * 0.25 + np.arange(64 * 64) // 640 * 0.1).astype(np.float32).reshape(64, 64)
+    long_paths, survived = 0, 0
+    for i in pick:
+        deps, k_i = _c3_python(keys[i], mu_a, lm)
+        r = oracle.c3_fwd(keys[i:i + 1], mu_a)
+        assert int(r.per_item[0]) == k_i
+        want = np.zeros(64 * 64)
+        for b, _, _, v in deps:
+            if b >= 0:
+                want[b] += float(v)
+        assert np.array_equal(r.tallies64["absorbed"].ravel(), want), i
+        long_paths += k_i > 20
+        survived += max(rk for _, _, rk, _ in deps) > 0
+        for ct in (np.ones((64, 64), np.float32), ct2):
+            g, ntr = oracle.c3_grad(keys[i:i + 1], mu_a, ct)
+            assert ntr == 0
+            terms = [float(ct.ravel()[b]) * 10.0 ** rk * mu_s ** k * (mu_t ** -(k + 1) - (k + 1) * mu_a * mu_t ** -(k + 2))
+                     for b, k, rk, _ in deps if b >= 0]
+            mag = sum(abs(t) for t in terms)
+            assert abs(float(g) - sum(terms)) <= 1e-4 * max(mag, 1e-30), (i, float(g), sum(terms))
+    assert long_paths > 5 and survived >= 10     # (paths with many scatterings, and roulette survivals: 10^r_k)
