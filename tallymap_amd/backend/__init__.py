@@ -370,14 +370,16 @@ def prebuild(entries, n=64):
         for wrt in ((wp, wb), ((), wb)):
             adj = R.adjoint_program(prog, wrt)
             pl = R.plan(adj)
-            if any(pl.car_act):
-                from . import replay as RP
-                src, _ = RP.build(adj, block=K.BLOCK, tape=RP.TAPE,
-                                  refill=int(cfg.get("opts", {}).get("rev_refill", RP.REFILL)))
+            if any(pl.car_act):          # the tape adjoint: its count and reverse programs
+                from . import tape as T
+                tp = T.programs(adj, pl)
+                progs = [tp.count, tp.reverse]
             else:
-                src, _ = K.build(R.forward_only_program(adj, pl), block=K.BLOCK, schedule="step", refill=1)
-            Cm.code_object(src, name=f"tm_{adj.tag}.hip", store_pkg=True)
-            done.append((name, adj.tag + str(wrt), Cm._key(src)[:16]))
+                progs = [R.forward_only_program(adj, pl)]
+            for q in progs:
+                src, _ = K.build(q, block=K.BLOCK, schedule="step", refill=1)
+                Cm.code_object(src, name=f"tm_{q.tag}.hip", store_pkg=True)
+                done.append((name, q.tag + str(wrt), Cm._key(src)[:16]))
     return done
 
 

@@ -1,0 +1,301 @@
+"""The JAX side of the drop-in: the reference's ClosedJaxpr item programs run by this backend.
+
+The reference dispatches a traced `tallymap_call` to a kernel platform in `_primitive._run1`
+(`tallymap/_primitive.py:171-194`), gated by `KERNEL_PLATFORMS` (`:159`) and one `mlir.register_lowering` per
+platform (`:352-356`); the platform's backend is `KB.run(p, pi, bc, target, ...)` (`backends/kernel/__init__.py:
+135-185`), which returns `[out tallies in p.out_tallies order] + [stats i32[5]] + [per-item results]`.  This module
+is that backend for ROCm:
+
+  convert(cj)      the reference's item program (a JAX ClosedJaxpr: tallies, per-item leaves, broadcast leaves) as
+                   this package's IR (`_core.Jaxpr`), equation by equation.  The IR uses JAX's primitive names and
+                   parameters, so most equations are re-bound as they are (JAX-only parameters such as `sharding` or
+                   `accuracy` dropped); `pjit` / `closed_call` / `custom_jvp_call` / `custom_vjp_call` bodies are
+                   inlined; closed-over constants become literals; typed PRNG keys (`key<fry>[...]`) become
+                   uint32[..., 2] and the key primitives (`random_wrap`, `random_unwrap`, `random_fold_in`,
+                   `random_split`, `random_bits`, `threefry2x32`) are expanded with this package's own threefry
+                   layering (tallymap_amd.random), as the reference's op table expands them for its kernels
+                   (`op_table.py:1664-1761`, `_compat.py:119-154`).
+  item_program(p)  the reference's `ItemProgram` (`_api.py:231-281`) as this package's, cached per program.
+  run(p, pi, bc, target="rocm", ...)
+                   `KB.run`'s contract on torch tensors (the eager path this image can exercise): the same arguments
+                   and options (`cuda_math`, `min_blocks_per_sm` accepted and ignored, as the reference's CPU target
+                   ignores them, `kernel/__init__.py:150-154`), the same result list.
+  register(prim_module, lib)
+                   what a maintainer calls once, with JAX present, to add the ROCm platform to the reference:
+                   `KERNEL_PLATFORMS` gains "rocm", the primitive gets its ROCm lowering, and the XLA FFI handler of
+                   INTEGRATION.md is registered as `tallymap_rocm_launch` for platform "ROCM".
+
+Nothing here imports JAX at module load; `register` does.  Objects are read duck-typed (`eqn.primitive.name`,
+`eqn.params`, `var.aval.shape / dtype / weak_type`, `literal.val`, `closed.jaxpr / consts`), so the converter is
+exercised on the CPU with objects of that shape.
+"""
+import weakref
+
+import numpy as np
+
+from . import _core as C
+from . import random as R
+from ._api import ItemProgram, TSpec
+
+KEY_WORDS = 2                 # a threefry key: uint32[2]
+_DROP = {"sharding", "accuracy", "out_sharding", "algorithm", "transpose_algorithm", "preferred_element_type",
+         "unroll", "_split_transpose", "linear", "jaxpr", "name", "keep_unused", "inline", "donated_invars",
+         "in_shardings", "out_shardings", "in_layouts", "out_layouts", "resource_env", "compiler_options_kvs",
+         "ctx_mesh"}
+_INLINE = {"pjit": "jaxpr", "closed_call": "call_jaxpr", "core_call": "call_jaxpr", "custom_jvp_call": "call_jaxpr",
+           "custom_vjp_call": "call_jaxpr", "custom_vjp_call_jaxpr": "fun_jaxpr", "checkpoint": "jaxpr",
+           "remat": "jaxpr", "remat2": "jaxpr"}
+
+
+class UnsupportedError(NotImplementedError):
+    pass
+
+
+def _is_key(dtype):
+    return str(dtype).startswith("key<")
+
+
+def _aval(a):
+    """a JAX aval (shape, dtype, weak_type) -> this IR's AVal (a key: uint32[..., 2])."""
+    shape = tuple(int(s) for s in a.shape)
+    if _is_key(a.dtype):
+        return C.AVal(shape + (KEY_WORDS,), C.U32)
+    return C.AVal(shape, np.dtype(a.dtype), bool(getattr(a, "weak_type", False)))
+
+
+def _closed(x):
+    """(jaxpr, consts) of a ClosedJaxpr (or of a plain Jaxpr: no consts)."""
+    if hasattr(x, "jaxpr") and hasattr(x, "consts"):
+        return x.jaxpr, list(x.consts)
+    return x, []
+
+
+def _lit_of(val, aval):
+    a = np.asarray(val)
+    if _is_key(getattr(a, "dtype", None)):
+        raise UnsupportedError("tallymap: a PRNG key literal in an item program (pass the key as an argument)")
+    return C.literal(a.astype(aval.dtype).reshape(aval.shape) if aval.shape else a.astype(aval.dtype)[()],
+                     aval.dtype, weak=aval.weak)
+
+
+def _params(prim, params):
+    out = {}
+    for k, v in params.items():
+        if k in _DROP:
+            continue
+        if k == "new_dtype" or k == "dtype":
+            v = np.dtype(v)
+        out[k] = v
+    if prim in ("cond",) and "nconsts" not in out:
+        out["nconsts"] = 0
+    return out
+
+
+class _Conv:
+    """re-binds a JAX jaxpr's equations in the current trace (this package's Builder)."""
+
+    def __init__(self):
+        self.memo = {}
+
+    def val(self, env, v):
+        if hasattr(v, "val"):             # a Literal (a Var has no value)
+            return _lit_of(v.val, _aval(v.aval))
+        return env[id(v)]
+
+    def run(self, jx, consts, args):
+        """evaluate jaxpr `jx` (with `consts` for its constvars) on `args` (Tracers / literals) -> outputs."""
+        env = {}
+        for cv, c in zip(getattr(jx, "constvars", ()) or (), consts):
+            env[id(cv)] = _lit_of(c, _aval(cv.aval))
+        for v, a in zip(jx.invars, args):
+            env[id(v)] = a
+        for e in jx.eqns:
+            ins = [self.val(env, v) for v in e.invars]
+            outs = self.eqn(e, ins)
+            for o, x in zip(e.outvars, outs):
+                env[id(o)] = x
+        return [self.val(env, v) for v in jx.outvars]
+
+    def sub(self, closed):
+        """a sub-program (a while's cond / body, a cond branch) -> this IR's Jaxpr, its consts inlined."""
+        jx, consts = _closed(closed)
+        b = C.Builder(C.current())
+        C._STACK.append(b)
+        try:
+            ins = [C.Tracer(b.new_invar(_aval(v.aval))) for v in jx.invars]
+            outs = self.run(jx, consts, ins)
+            ov = []
+            for x, v in zip(outs, jx.outvars):
+                if C.is_traced(x):
+                    ov.append(b.local(x.var))
+                else:
+                    ov.append(x if isinstance(x, C.Lit) else C.literal(x))
+        finally:
+            C._STACK.pop()
+        if b.cap_local:
+            raise UnsupportedError("tallymap: a loop or branch body reads a value of the enclosing program "
+                                   "(JAX passes it as a constant operand; this program does not)")
+        return C.Jaxpr([t.var for t in ins], ov, b.eqns)
+
+    def eqn(self, e, ins):
+        prim = e.primitive.name
+        outav = [_aval(o.aval) for o in e.outvars]
+        if prim in _INLINE:
+            inner = e.params.get(_INLINE[prim]) or e.params.get("jaxpr") or e.params.get("call_jaxpr")
+            jx, consts = _closed(inner)
+            return self.run(jx, consts, ins)
+        if prim in ("random_wrap", "random_unwrap"):
+            return [ins[0]]
+        if prim == "reshape" and tuple(e.params.get("new_sizes", ())) == tuple(getattr(ins[0], "shape", ())) \
+                and e.params.get("dimensions") is None:
+            return [ins[0]]                       # (a reshape to the operand's own shape: JAX binds it for scalars)
+        if prim == "convert_element_type" and C.is_traced(ins[0]) and ins[0].dtype == outav[0].dtype \
+                and ins[0].aval.weak == outav[0].weak:
+            return [ins[0]]
+        if prim == "random_fold_in":
+            return [self._keys_map(ins[0], lambda k, i: R.fold_in(k, _elem(ins[1], i)))]
+        if prim == "random_split":
+            shape = tuple(e.params.get("shape", (2,)))
+            if len(shape) != 1:
+                raise UnsupportedError(f"tallymap: random_split to shape {shape}")
+            return [self._keys_map(ins[0], lambda k, i: R.split(k, shape[0]), extra=shape)]
+        if prim == "random_bits":
+            bw, shape = int(e.params["bit_width"]), tuple(e.params["shape"])
+            if bw != 32:
+                raise UnsupportedError(f"tallymap: random_bits of {bw} bits (32-bit draws are supported)")
+            return [self._keys_map(ins[0], lambda k, i: R.bits(k, shape if shape else ()), extra=shape,
+                                   dtype=C.U32)]
+        if prim == "threefry2x32":
+            return self._threefry(ins, outav)
+        if prim == "while":
+            p = dict(cond_jaxpr=self.sub(e.params["cond_jaxpr"]), body_jaxpr=self.sub(e.params["body_jaxpr"]),
+                     cond_nconsts=int(e.params["cond_nconsts"]), body_nconsts=int(e.params["body_nconsts"]))
+            return C.bind("while", [_var(x) for x in ins], outav, **p)
+        if prim == "cond":
+            p = dict(branches=tuple(self.sub(b) for b in e.params["branches"]), nconsts=0)
+            return C.bind("cond", [_var(x) for x in ins], outav, **p)
+        return C.bind(prim, [_var(x) for x in ins], outav, **_params(prim, e.params))
+
+    def _keys_map(self, keys, f, extra=(), dtype=None):
+        """f applied to each key of a (batch of) key(s), stacked."""
+        if keys.shape == (KEY_WORDS,):
+            return f(keys, None)
+        n = keys.shape[0]
+        return C.stack([f(keys[i], i) for i in range(n)])
+
+    def _threefry(self, ins, outav):
+        if all(not getattr(x, "shape", ()) for x in ins):
+            return list(R.threefry2x32(*[_tr(x) for x in ins]))
+        n = max(int(np.prod(getattr(x, "shape", ()) or (1,))) for x in ins)
+        o0, o1 = [], []
+        for i in range(n):
+            a = R.threefry2x32(*[_tr(_elem(x, i)) for x in ins])
+            o0.append(a[0])
+            o1.append(a[1])
+        return [C.stack(o0), C.stack(o1)]
+
+
+def _var(x):
+    if C.is_traced(x):
+        return C.as_var(x)
+    return x if isinstance(x, C.Lit) else C.literal(x)
+
+
+def _tr(x):
+    return x if C.is_traced(x) else (int(x.val) if isinstance(x, C.Lit) else int(x))
+
+
+def _elem(x, i):
+    if i is None or not getattr(x, "shape", ()):
+        return x
+    return x[i]
+
+
+def convert(cj, in_avals=None):
+    """the reference's item ClosedJaxpr -> this package's IR Jaxpr (invars: the item's, keys as uint32[..., 2])."""
+    jx, consts = _closed(cj)
+    b = C.Builder()
+    C._STACK.append(b)
+    try:
+        ins = [C.Tracer(b.new_invar(_aval(v.aval))) for v in jx.invars]
+        outs = _Conv().run(jx, consts, ins)
+        ov = [b.local(x.var) if C.is_traced(x) else (x if isinstance(x, C.Lit) else C.literal(x)) for x in outs]
+    finally:
+        C._STACK.pop()
+    return C.Jaxpr(b.invars, ov, b.eqns)
+
+
+_PROGS = weakref.WeakKeyDictionary()
+
+
+def item_program(p):
+    """the reference's ItemProgram (`_api.py:231-281`: cj, tallies of TSpec(name, S, dtype, lead, fixed_point, kind,
+    scale, exact), nP, nB, trunc, spawn, tag, where, nact, rec, app) -> this package's ItemProgram."""
+    try:
+        hit = _PROGS.get(p)
+    except TypeError:
+        hit = None
+    if hit is not None:
+        return hit
+    if getattr(p, "spawn", None) is not None or getattr(p, "rec", None) is not None:
+        raise UnsupportedError("tallymap: spawning programs are bound through tallymap_amd.vmap(spawn=...) here")
+    if getattr(p, "app", None) is not None:
+        raise UnsupportedError("tallymap: Records programs are bound through tallymap_amd.vmap here")
+    tallies = []
+    for s in p.tallies:
+        if tuple(getattr(s, "lead", ()) or ()):
+            raise UnsupportedError("tallymap: tangent-lane tallies (lead dims) come from tallymap_amd.jacfwd here")
+        dt = np.dtype(s.dtype)
+        exact = bool(getattr(s, "exact", False))
+        fixed = bool(getattr(s, "fixed_point", False)) and not exact
+        tallies.append(TSpec(s.name, (int(s.S),), dt, exact=exact, kind=s.kind, fixed=fixed,
+                             scale=float(getattr(s, "scale", 0.0)) if fixed else 0.0))
+    q = ItemProgram(convert(p.cj), tuple(tallies), int(p.nP), int(p.nB), p.trunc, getattr(p, "tag", "primal"),
+                    getattr(p, "where", ""))
+    try:
+        _PROGS[p] = q
+    except TypeError:
+        pass
+    return q
+
+
+def run(p, pi, bc, target="rocm", cuda_math=None, schedule="step", ndev=1, min_blocks_per_sm=None, **opts):
+    """KB.run's contract for ROCm (`backends/kernel/__init__.py:135-185`): the reference's program `p` over the
+    per-item operands `pi` ([N, ...] each) and broadcast operands `bc` -> [tallies in p.out_tallies order] +
+    [stats int32[5]] + [per-item results].  cuda_math and min_blocks_per_sm have no meaning on ROCm and are
+    ignored; `schedule` is this backend's ('step' or 'item'); ndev > 1 is not supported (one GPU)."""
+    from . import backend as B
+    if target not in ("rocm", "hip"):
+        raise UnsupportedError(f"tallymap_amd.jax_bind.run: target {target!r} (this backend runs on ROCm)")
+    if int(ndev) != 1:
+        raise UnsupportedError("tallymap_amd.jax_bind.run: one device per call (shard the items across calls)")
+    q = item_program(p)
+    N = int(pi[0].shape[0]) if pi else 0
+    o = dict(opts)
+    o["schedule"] = schedule
+    n_active = None
+    if getattr(p, "nact", None) is not None:
+        n_active = int(np.asarray(bc[p.nact].cpu() if hasattr(bc[p.nact], "cpu") else bc[p.nact]))
+    res = B.run(q, list(pi), list(bc), N, o, n_active=n_active)
+    return list(res.tallies) + [res.stats] + list(res.ys)
+
+
+def register(prim_module, lib_path=None):
+    """with JAX present: add ROCm to the reference's kernel platforms.  `prim_module` is the reference's
+    `tallymap._primitive`; `lib_path` a build of INTEGRATION.md's XLA FFI handler (the shim compiled against
+    jaxlib's `xla/ffi/api/ffi.h`, which exports TallymapRocmLaunch and forwards to this library's tm_launch).
+    Returns the platforms now served."""
+    import ctypes
+
+    import jax
+    from jax.interpreters import mlir
+    P = prim_module
+    if "rocm" not in P.KERNEL_PLATFORMS:
+        P.KERNEL_PLATFORMS = tuple(P.KERNEL_PLATFORMS) + ("rocm",)
+    for prim in (P.tallymap_call_p, P.tallymap_jvp_p):
+        mlir.register_lowering(prim, P._lowering("rocm"), platform="rocm")
+    if lib_path is not None:
+        lib = ctypes.CDLL(lib_path)
+        jax.ffi.register_ffi_target("tallymap_rocm_launch", jax.ffi.pycapsule(lib.TallymapRocmLaunch),
+                                    platform="ROCM")
+    return P.KERNEL_PLATFORMS

@@ -118,8 +118,9 @@ def fold_in(key, data):
             key = C.literal(np.asarray(key, np.uint32), C.U32)
             raise C.TraceError("fold_in of a constant key with traced data: pass the key as an argument")
         return _host_fold_in(key, data)
+    d = _u32(data)                # (converted before the key is read, in the order jax.random.fold_in binds them)
     k0, k1 = _words(key)
-    o0, o1 = threefry2x32(k0, k1, 0, _u32(data))
+    o0, o1 = threefry2x32(k0, k1, 0, d)
     return C.stack([o0, o1])
 
 

@@ -1,0 +1,213 @@
+"""The JAX-side binding (tallymap_amd.jax_bind) on objects shaped like JAX's: a ClosedJaxpr of the quickstart walker
+(config 1) written the way JAX traces it for the reference's tm.vmap -- typed PRNG keys with random_wrap /
+random_fold_in / random_unwrap / random_bits, jax.random.uniform inside a pjit, the scalar reshape JAX binds there,
+`sharding` parameters, a while loop whose body is a ClosedJaxpr with a closed-over constant, the reference's TSpec and
+ItemProgram fields -- converts to the same program (structural digest) as this package's own trace of the item, and
+run() returns KB.run's result list on the GPU, bitwise the package's own vmap."""
+import numpy as np
+import pytest
+
+from tallymap_amd import _core as C
+from tallymap_amd import configs
+from tallymap_amd import jax_bind as JB
+from tallymap_amd._api import build_program
+
+
+class Prim:
+    def __init__(self, name):
+        self.name = name
+
+
+class KeyTy:
+    def __str__(self):
+        return "key<fry>"
+
+
+class Aval:
+    def __init__(self, shape, dtype, weak=False):
+        self.shape, self.dtype, self.weak_type = tuple(shape), dtype, weak
+
+
+class Var:
+    def __init__(self, shape, dtype, weak=False):
+        self.aval = Aval(shape, dtype, weak)
+
+
+class Literal:
+    def __init__(self, val, dtype, weak=False):
+        self.val = np.asarray(val, dtype)
+        self.aval = Aval(np.shape(val), np.dtype(dtype), weak)
+
+
+class Eqn:
+    def __init__(self, prim, invars, outvars, **params):
+        self.primitive, self.invars, self.outvars, self.params = Prim(prim), invars, outvars, params
+
+
+class Jaxpr:
+    def __init__(self, invars, outvars, eqns, constvars=()):
+        self.invars, self.outvars, self.eqns, self.constvars = invars, outvars, eqns, list(constvars)
+
+
+class ClosedJaxpr:
+    def __init__(self, jaxpr, consts=()):
+        self.jaxpr, self.consts = jaxpr, list(consts)
+
+
+class RefTSpec:           # the reference's TSpec fields (_api.py:204-220)
+    def __init__(self, name, S, dtype):
+        self.name, self.S, self.dtype, self.lead, self.fixed_point = name, S, dtype, (), False
+        self.kind, self.scale, self.exact, self.slots = "sum", 2.0 ** 32, False, False
+
+
+class RefProgram:         # the reference's ItemProgram fields (_api.py:231-255)
+    def __init__(self, cj, tallies, nP, nB, trunc):
+        self.cj, self.tallies, self.nP, self.nB, self.trunc = cj, tallies, nP, nB, trunc
+        self.spawn = self.rec = self.app = self.nact = None
+        self.tag, self.where = "primal", "c1_item"
+
+
+F32, I32, U32, BOOL = np.dtype(np.float32), np.dtype(np.int32), np.dtype(np.uint32), np.dtype(bool)
+
+
+def _uniform_pjit():
+    """jax.random.uniform(raw key) as JAX traces it: pjit[_uniform] { random_wrap, random_bits, the float ops,
+    reshape to () }."""
+    key = Var((2,), U32)
+    kk = Var((), KeyTy())
+    bits = Var((), U32)
+    a, b, f, g, h, i, j, u = (Var((), U32), Var((), U32), Var((), F32), Var((), F32), Var((), F32), Var((), F32),
+                              Var((), F32), Var((), F32))
+    eqns = [Eqn("random_wrap", [key], [kk], impl="fry"),
+            Eqn("random_bits", [kk], [bits], bit_width=32, shape=()),
+            Eqn("shift_right_logical", [bits, Literal(9, U32)], [a]),
+            Eqn("or", [a, Literal(1065353216, U32)], [b]),
+            Eqn("bitcast_convert_type", [b], [f], new_dtype=F32),
+            Eqn("sub", [f, Literal(1.0, F32)], [g]),
+            Eqn("mul", [g, Literal(1.0, F32)], [h]),
+            Eqn("add", [h, Literal(0.0, F32)], [i]),
+            Eqn("reshape", [i], [j], new_sizes=(), dimensions=None, sharding=None),
+            Eqn("max", [Literal(0.0, F32), j], [u])]
+    return ClosedJaxpr(Jaxpr([key], [u], eqns))
+
+
+def _c1_closed_jaxpr():
+    """config 1's item after the reference's tm.vmap: invars [hist f32[16]] + [x, key] + [theta]; the top-level
+    loop capped at 100 steps (a counter kc; truncated = kc >= 100 & x > 0.05)."""
+    # cond
+    ckc, ck, cx, ch = Var((), I32), Var((), I32, True), Var((), F32), Var((16,), F32)
+    c1, c2, c3 = Var((), BOOL), Var((), BOOL), Var((), BOOL)
+    cond = ClosedJaxpr(Jaxpr([ckc, ck, cx, ch], [c3], [Eqn("lt", [ckc, Literal(100, I32)], [c1]),
+                                                      Eqn("gt", [cx, Literal(0.05, F32)], [c2]),
+                                                      Eqn("and", [c1, c2], [c3])]))
+    # body, with 16.0 as a closed-over constant
+    bkey, bth, bkc, bk, bx, bh = Var((2,), U32), Var((), F32), Var((), I32), Var((), I32, True), Var((), F32), \
+        Var((16,), F32)
+    c16 = Var((), F32)
+    kc1, ku, kk, fk, rk, u = Var((), I32), Var((), U32), Var((), KeyTy()), Var((), KeyTy()), Var((2,), U32), \
+        Var((), F32)
+    t87, idx, t89, val, h2, k1, t91, t92, x1 = (Var((), F32), Var((), I32), Var((), F32), Var((), F32),
+                                                Var((16,), F32), Var((), I32, True), Var((), F32), Var((), F32),
+                                                Var((), F32))
+    body_eqns = [Eqn("add", [bkc, Literal(1, I32)], [kc1]),
+                 Eqn("convert_element_type", [bk], [ku], new_dtype=U32, weak_type=False, sharding=None),
+                 Eqn("random_wrap", [bkey], [kk], impl="fry"),
+                 Eqn("random_fold_in", [kk, ku], [fk]),
+                 Eqn("random_unwrap", [fk], [rk]),
+                 Eqn("pjit", [rk], [u], jaxpr=_uniform_pjit(), name="_uniform"),
+                 Eqn("mul", [bx, c16], [t87]),
+                 Eqn("convert_element_type", [t87], [idx], new_dtype=I32, weak_type=False, sharding=None),
+                 Eqn("sub", [Literal(1.0, F32), bx], [t89]),
+                 Eqn("mul", [bth, t89], [val]),
+                 Eqn("tallymap_emit", [bh, idx, val], [h2]),
+                 Eqn("add", [bk, Literal(1, I32, True)], [k1]),
+                 Eqn("mul", [Literal(0.5, F32), u], [t91]),
+                 Eqn("add", [Literal(0.5, F32), t91], [t92]),
+                 Eqn("mul", [bx, t92], [x1])]
+    body = ClosedJaxpr(Jaxpr([bkey, bth, bkc, bk, bx, bh], [kc1, k1, x1, h2], body_eqns, [c16]),
+                       [np.float32(16.0)])
+    # top level
+    hist, x, key, th = Var((16,), F32), Var((), F32), Var((2,), U32), Var((), F32)
+    wkc, wk, wx, wh = Var((), I32), Var((), I32, True), Var((), F32), Var((16,), F32)
+    g1, g2, tr = Var((), BOOL), Var((), BOOL), Var((), BOOL)
+    eqns = [Eqn("while", [key, th, Literal(0, I32), Literal(0, I32, True), x, hist], [wkc, wk, wx, wh],
+                cond_jaxpr=cond, body_jaxpr=body, cond_nconsts=0, body_nconsts=2),
+            Eqn("gt", [wx, Literal(0.05, F32)], [g1]),
+            Eqn("ge", [wkc, Literal(100, I32)], [g2]),
+            Eqn("and", [g2, g1], [tr])]
+    return ClosedJaxpr(Jaxpr([hist, x, key, th], [wh, wk, tr], eqns))
+
+
+def _own_c1():
+    C1 = configs.C1
+    prog, _ = build_program(C1["item"], C1["outputs"], C1["in_axes"], [C.AVal((), F32), C.AVal((2,), U32)],
+                            [C.AVal((), F32)], C1["max_steps"])
+    return prog
+
+
+def _ref_c1():
+    return RefProgram(_c1_closed_jaxpr(), (RefTSpec("hist", 16, F32),), 2, 1, 1)
+
+
+def test_c1_closed_jaxpr_converts_to_the_packages_own_program():
+    own = _own_c1()
+    got = JB.item_program(_ref_c1())
+    assert got.digest() == own.digest()
+    assert [s.name for s in got.tallies] == ["hist"] and got.trunc == own.trunc
+
+
+def test_converter_expands_key_primitives_and_refuses_what_it_cannot_run():
+    """random_split and a 4-draw random_bits expand to one threefry2x32 per output row / word (the partitionable
+    layering); a cond becomes this IR's cond; a key literal, 64-bit draws and a two-device call are refused."""
+    key, kk, ks, k0 = Var((2,), U32), Var((), KeyTy()), Var((3,), KeyTy()), Var((), KeyTy())
+    b4, flag, o = Var((4,), U32), Var((), BOOL), Var((), U32)
+    br_in, br_out = Var((), U32), Var((), U32)
+    br_t = ClosedJaxpr(Jaxpr([br_in], [br_out], [Eqn("add", [br_in, Literal(1, U32)], [br_out])]))
+    bf_in = Var((), U32)
+    br_f = ClosedJaxpr(Jaxpr([bf_in], [bf_in], []))
+    s1 = Var((), U32)
+    eqns = [Eqn("random_wrap", [key], [kk], impl="fry"),
+            Eqn("random_split", [kk], [ks], shape=(3,)),
+            Eqn("slice", [ks], [Var((1,), KeyTy())], start_indices=(1,), limit_indices=(2,), strides=None)]
+    sl = eqns[-1].outvars[0]
+    eqns += [Eqn("squeeze", [sl], [k0], dimensions=(0,)),
+             Eqn("random_bits", [k0], [b4], bit_width=32, shape=(4,)),
+             Eqn("slice", [b4], [Var((1,), U32)], start_indices=(2,), limit_indices=(3,), strides=None)]
+    sl2 = eqns[-1].outvars[0]
+    eqns += [Eqn("squeeze", [sl2], [s1], dimensions=(0,)),
+             Eqn("gt", [s1, Literal(7, U32)], [flag]),
+             Eqn("convert_element_type", [flag], [Var((), I32)], new_dtype=I32, weak_type=False)]
+    ci = eqns[-1].outvars[0]
+    eqns.append(Eqn("cond", [ci, s1], [o], branches=(br_f, br_t)))
+    jx = JB.convert(ClosedJaxpr(Jaxpr([key], [o], eqns)))
+    prims = [e.prim for e in C.walk_eqns(jx)]
+    assert prims.count("threefry2x32") == 3 + 4 and "cond" in prims
+    assert not any(p.startswith("random_") for p in prims)
+    with pytest.raises(JB.UnsupportedError, match="64 bits"):
+        JB.convert(ClosedJaxpr(Jaxpr([key], [Var((), np.dtype(np.uint64))], [
+            Eqn("random_wrap", [key], [kk], impl="fry"),
+            Eqn("random_bits", [kk], [Var((), np.dtype(np.uint64))], bit_width=64, shape=())])))
+    with pytest.raises(JB.UnsupportedError, match="one device"):
+        JB.run(_ref_c1(), [np.zeros(4, F32), np.zeros((4, 2), U32)], [np.float32(2.0)], ndev=2)
+
+
+@pytest.mark.gpu
+def test_run_contract_on_the_gpu_matches_vmap():
+    """run(p, pi, bc, target='rocm', cuda_math=..., min_blocks_per_sm=...) -> [hist] + [stats int32[5]] + [k, trunc]
+    (KB.run's list), bitwise the package's own vmap of the same item."""
+    import torch
+
+    import tallymap_amd as tm
+    print("case: jax_bind.run of the C1 ClosedJaxpr, N=10000", flush=True)
+    xs, keys, theta = configs.c1_inputs()
+    out = JB.run(_ref_c1(), [xs, keys], [theta], target="rocm", cuda_math="approx", min_blocks_per_sm=4)
+    C1 = configs.C1
+    res = tm.vmap(C1["item"], outputs=C1["outputs"], in_axes=C1["in_axes"], max_steps=C1["max_steps"])(
+        xs, keys, theta)
+    torch.cuda.synchronize()
+    assert len(out) == 1 + 1 + 2
+    assert np.array_equal(out[0].cpu().numpy().view(np.uint32), res.outputs["hist"].cpu().numpy().view(np.uint32)) \
+        or np.allclose(out[0].cpu().numpy(), res.outputs["hist"].cpu().numpy(), rtol=1e-6)
+    assert out[1].dtype == torch.int32 and tuple(out[1].shape) == (5,)
+    assert np.array_equal(out[2].cpu().numpy(), res.per_item.cpu().numpy())
+    assert not out[3].cpu().numpy().any()
