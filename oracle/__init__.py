@@ -45,6 +45,8 @@ def lib():
         L.tmref_normal.argtypes = [_p]
         L.tmref_bits32.restype = _u32
         L.tmref_bits32.argtypes = [_p]
+        L.tmref_libm_f32.argtypes = [_i, _p, _p, _p, _i64]
+        L.tmref_libm_f64.argtypes = [_i, _p, _p, _p, _i64]
         L.tmref_exact_sum.restype = _f
         L.tmref_exact_sum.argtypes = [_p, _i64, _p]
         L.tmref_c1_fwd.argtypes = [_p, _p, _f, _i64, _i, _i, _p, _p, _p, _p, _p]
@@ -113,6 +115,22 @@ def normal(key):
 def bits32(key):
     key = np.ascontiguousarray(key, np.uint32)
     return int(lib().tmref_bits32(_ptr(key)))
+
+
+LIBM = ("exp", "exp2", "log", "log1p", "expm1", "log2", "sin", "cos", "tan", "asin", "acos", "atan", "sinh", "cosh",
+        "tanh", "asinh", "acosh", "atanh", "cbrt", "erf", "erfc", "lgamma", "logistic", "erf_inv", "pow", "atan2",
+        "nextafter")
+
+
+def libm(name, x, y=None, dtype=np.float32):
+    """the host glibc's `name` on the array x (and y for pow / atan2 / nextafter), in dtype (float32: expf, ...;
+    float64: exp, ...): the checker of the device's transcendentals."""
+    x = np.ascontiguousarray(x, dtype)
+    y = np.ascontiguousarray(np.zeros_like(x) if y is None else y, dtype)
+    out = np.zeros_like(x)
+    f = lib().tmref_libm_f32 if np.dtype(dtype) == np.float32 else lib().tmref_libm_f64
+    f(LIBM.index(name), _ptr(x), _ptr(y), _ptr(out), x.size)
+    return out
 
 
 def exact_sum(v):

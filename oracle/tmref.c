@@ -932,3 +932,48 @@ int tmref_c5_grad(const float* th0, const float* om0, const i32* ids, float A, i
 }
 
 int tmref_max_threads(void) { return omp_get_max_threads(); }
+
+/* ------------------------------------------------------------------------------------------- glibc evaluation
+ * The host's libm on arrays, the checker of the device's transcendentals: function `fn` indexes the list
+ * exp exp2 log log1p expm1 log2 sin cos tan asin acos atan sinh cosh tanh asinh acosh atanh cbrt erf erfc lgamma
+ * logistic erf_inv | pow atan2 nextafter (the last three binary, reading y).  logistic is the reference CPU target's
+ * 1 / (1 + exp(-x)) (op_table.py:243-247); erf_inv of float32 is this file's Giles-in-double (float64: none, NaN). */
+static float tm_libm1f(int fn, float x) {
+  switch (fn) {
+    case 0: return expf(x); case 1: return exp2f(x); case 2: return logf(x); case 3: return log1pf(x);
+    case 4: return expm1f(x); case 5: return log2f(x); case 6: return sinf(x); case 7: return cosf(x);
+    case 8: return tanf(x); case 9: return asinf(x); case 10: return acosf(x); case 11: return atanf(x);
+    case 12: return sinhf(x); case 13: return coshf(x); case 14: return tanhf(x); case 15: return asinhf(x);
+    case 16: return acoshf(x); case 17: return atanhf(x); case 18: return cbrtf(x); case 19: return erff(x);
+    case 20: return erfcf(x); case 21: return lgammaf(x); case 22: return 1.0f / (1.0f + expf(-x));
+    case 23: return tmref_erfinvf(x);
+    default: return NAN;
+  }
+}
+static double tm_libm1d(int fn, double x) {
+  switch (fn) {
+    case 0: return exp(x); case 1: return exp2(x); case 2: return log(x); case 3: return log1p(x);
+    case 4: return expm1(x); case 5: return log2(x); case 6: return sin(x); case 7: return cos(x);
+    case 8: return tan(x); case 9: return asin(x); case 10: return acos(x); case 11: return atan(x);
+    case 12: return sinh(x); case 13: return cosh(x); case 14: return tanh(x); case 15: return asinh(x);
+    case 16: return acosh(x); case 17: return atanh(x); case 18: return cbrt(x); case 19: return erf(x);
+    case 20: return erfc(x); case 21: return lgamma(x); case 22: return 1.0 / (1.0 + exp(-x));
+    default: return NAN;
+  }
+}
+void tmref_libm_f32(int fn, const float* x, const float* y, float* out, i64 n) {
+  for (i64 i = 0; i < n; ++i) {
+    if (fn == 24) out[i] = powf(x[i], y[i]);
+    else if (fn == 25) out[i] = atan2f(x[i], y[i]);
+    else if (fn == 26) out[i] = nextafterf(x[i], y[i]);
+    else out[i] = tm_libm1f(fn, x[i]);
+  }
+}
+void tmref_libm_f64(int fn, const double* x, const double* y, double* out, i64 n) {
+  for (i64 i = 0; i < n; ++i) {
+    if (fn == 24) out[i] = pow(x[i], y[i]);
+    else if (fn == 25) out[i] = atan2(x[i], y[i]);
+    else if (fn == 26) out[i] = nextafter(x[i], y[i]);
+    else out[i] = tm_libm1d(fn, x[i]);
+  }
+}

@@ -20,7 +20,7 @@ from . import lax as L
 
 ZERO_D = {"floor", "ceil", "round", "sign", "stop_gradient", "eq", "ne", "lt", "le", "gt", "ge", "and", "or",
           "not", "xor", "threefry2x32", "shift_left", "shift_right_logical", "shift_right_arithmetic",
-          "bitcast_convert_type"}
+          "bitcast_convert_type", "is_finite"}
 
 
 class ADError(NotImplementedError):
@@ -314,6 +314,83 @@ def r_logistic(g, ins, outs, e):
     return [g[0] * (a * (_f(1, a.dtype) - a))]
 
 
+def r_exp2(g, ins, outs, e):
+    return [g[0] * (outs[0] * _f(np.log(2.0), outs[0].dtype))]
+
+
+def r_log2(g, ins, outs, e):
+    return [g[0] / (ins[0] * _f(np.log(2.0), ins[0].dtype))]
+
+
+def r_tan(g, ins, outs, e):
+    a = outs[0]
+    return [g[0] * (_f(1, a.dtype) + a * a)]
+
+
+def r_atan(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] / (_f(1, x.dtype) + x * x)]
+
+
+def r_asin(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] * L.rsqrt(_f(1, x.dtype) - x * x)]
+
+
+def r_acos(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] * -L.rsqrt(_f(1, x.dtype) - x * x)]
+
+
+def r_sinh(g, ins, outs, e):
+    return [g[0] * L.cosh(ins[0])]
+
+
+def r_cosh(g, ins, outs, e):
+    return [g[0] * L.sinh(ins[0])]
+
+
+def r_asinh(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] * L.rsqrt(x * x + _f(1, x.dtype))]
+
+
+def r_acosh(g, ins, outs, e):
+    x = ins[0]
+    one = _f(1, x.dtype)
+    return [g[0] * (L.rsqrt(x - one) * L.rsqrt(x + one))]
+
+
+def r_atanh(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] / (_f(1, x.dtype) - x * x)]
+
+
+def r_cbrt(g, ins, outs, e):
+    a = outs[0]
+    return [g[0] * (_f(1.0 / 3.0, a.dtype) * C.bind("integer_pow", [a.var], [a.aval], y=-2)[0])]
+
+
+def r_erf(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] * (_f(2.0 / np.sqrt(np.pi), x.dtype) * L.exp(-(x * x)))]
+
+
+def r_erfc(g, ins, outs, e):
+    x = ins[0]
+    return [g[0] * (_f(-2.0 / np.sqrt(np.pi), x.dtype) * L.exp(-(x * x)))]
+
+
+def r_rem(g, ins, outs, e):
+    from . import numpy as jnp
+    x, y = ins
+    gy = None
+    if C.is_traced(y):
+        q = x / y
+        gy = -g[0] * (jnp.sign(q) * L.floor(jnp.abs(q)))
+    return [g[0] if C.is_traced(x) else None, gy]
+
+
 def r_atan2(g, ins, outs, e):
     y, x = ins
     den = x * x + y * y
@@ -443,4 +520,6 @@ RULES = {"add": r_add, "sub": r_sub, "mul": r_mul, "div": r_div, "neg": r_neg, "
          "pow": r_pow, "integer_pow": r_integer_pow, "erf_inv": r_erf_inv, "select_n": r_select,
          "convert_element_type": r_convert, "copy": r_copy, "slice": r_slice, "squeeze": r_reshape,
          "reshape": r_reshape, "broadcast_in_dim": r_broadcast, "concatenate": r_concatenate,
-         "dynamic_index": r_dynamic_index}
+         "dynamic_index": r_dynamic_index, "exp2": r_exp2, "log2": r_log2, "tan": r_tan, "atan": r_atan,
+         "asin": r_asin, "acos": r_acos, "sinh": r_sinh, "cosh": r_cosh, "asinh": r_asinh, "acosh": r_acosh,
+         "atanh": r_atanh, "cbrt": r_cbrt, "erf": r_erf, "erfc": r_erfc, "rem": r_rem}

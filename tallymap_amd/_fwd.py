@@ -75,7 +75,7 @@ def _rem_rule(ts, ins, outs, e):
     return [t]
 
 
-EXTRA = {"tan": _tan_rule, "rem": _rem_rule}
+EXTRA = {"rem": _rem_rule}
 
 
 def _elementwise(e, ins, outs, ts):

@@ -19,15 +19,25 @@
 //              everywhere; expf everywhere except two inputs whose glibc result lies on a rounding knife-edge of
 //              the same evaluation, listed in tm_expf.  The exp2 table is 2^(i/32) rounded to double, minus i << 47
 //              (computed from that definition); the 2/pi bit table is the binary expansion of 2/pi.
+//   tm_exp2f, tm_log2f, tm_powf
+//              the same library's exp2f / log2f / powf on the expf / logf tables.  exp2f and log2f agree with
+//              glibc on all 2^32 inputs; powf on 1.0e9 random pairs (bit patterns, x near 1 with large |y|,
+//              integer and non-integer y of both signs) and a grid of special pairs, 0 mismatches.
 //   tm_atanf, tm_atan2f
 //              fdlibm's float atanf / atan2f (Sun, freely redistributable) in float arithmetic, in glibc's form
 //              (atanf returns +-pi/2 from |x| >= 2^25).  Checked bitwise against glibc on all 2^32 atanf arguments
 //              and on random atan2f pairs over the full exponent range.
+//   tm_expm1f, tm_log1pf, tm_tanhf
+//              fdlibm's float expm1f / log1pf / tanhf, float arithmetic without contraction, as glibc 2.35's
+//              generic build compiles them: bitwise equal to glibc on all 2^32 inputs.
+//   tm_logisticf
+//              1 / (1 + tm_expf(-x)), the reference CPU target's expression: all 2^32 inputs bitwise.
 //
-// Upstream notices of the restated code (the logf / expf / sinf / cosf reductions, tables and polynomial
-// coefficients, and the atanf / atan2f code and coefficients):
+// Upstream notices of the restated code (the logf / expf / exp2f / log2f / powf / sinf / cosf reductions, tables
+// and polynomial coefficients, and the atanf / atan2f / expm1f / log1pf / tanhf code and coefficients):
 //
-//   ARM optimized-routines (math/logf.c, math/expf.c, math/sinf.c, math/cosf.c and their data files):
+//   ARM optimized-routines (math/logf.c, math/expf.c, math/exp2f.c, math/log2f.c, math/powf.c, math/sinf.c,
+//   math/cosf.c and their data files):
 //     Copyright (c) 2017-2022, Arm Limited.
 //     SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception.  Used here under the MIT license:
 //     Permission is hereby granted, free of charge, to any person obtaining a copy of this software and
@@ -41,7 +51,8 @@
 //     DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM, OUT OF OR IN
 //     CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE SOFTWARE.
 //
-//   fdlibm (s_atanf.c, e_atan2f.c; float versions by Ian Lance Taylor, Cygnus Support):
+//   fdlibm (s_atanf.c, e_atan2f.c, s_expm1f.c, s_log1pf.c, s_tanhf.c; float versions by Ian Lance Taylor,
+//   Cygnus Support):
 //     Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
 //     Developed at SunPro, a Sun Microsystems, Inc. business.
 //     Permission to use, copy, modify, and distribute this software is freely granted, provided that this notice
@@ -421,3 +432,363 @@ TM_FN float tm_atan2f(float y, float x) {
     default: return (z - pi_lo) - pi;
   }
 }
+// ----------------------------------------------------------------------------------------------- exp2f
+// the exp2f of glibc 2.35 (ARM optimized-routines): x = k/32 + r, |r| <= 1/64; 2^(k/32) from tm_expf's table, 2^r by
+// a cubic (the unscaled coefficients of tm_expf's polynomial: C_i here = C_i there x 32^(3-i)).
+TM_FN double tm_exp2_table(u64 ki) {
+  const u64 T[32] = {
+      0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+      0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+      0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+      0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+      0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+      0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+  u64 t = T[ki % 32u];
+  t += ki << 47;
+  return tm_u2d(t);
+}
+TM_FN float tm_exp2f(float x) {
+  const double SHIFT = 0x1.8p+52 / 32, C0 = 0x1.c6af84b912394p-5, C1 = 0x1.ebfce50fac4f3p-3,
+               C2 = 0x1.62e42ff0c52d6p-1;
+  const u32 ux = tm_f2u(x);
+  const u32 abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= (tm_f2u(128.0f) >> 20)) {
+    if (ux == tm_f2u(-__builtin_inff())) return 0.0f;
+    if (abstop >= (tm_f2u(__builtin_inff()) >> 20)) return x + x;
+    if (x > 0.0f) return __builtin_inff();
+    if (x <= -150.0f) return 0.0f;
+  }
+  const double xd = (double)x;
+  double kd = xd + SHIFT;
+  const u64 ki = tm_d2u(kd);
+  kd -= SHIFT;
+  const double r = xd - kd;
+  const double s = tm_exp2_table(ki);
+  const double z = __builtin_fma(C0, r, C1);
+  const double r2 = r * r;
+  double y = __builtin_fma(C2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// ----------------------------------------------------------------------------------------------- log2f
+// the log2f of glibc 2.35 (ARM optimized-routines): tm_logf's reduction and invc values; log2 c = -log2(invc)
+// rounded to double (computed from that definition, as tm_logf's log c = -log(invc) is); log1p(r) / ln2 by a
+// quartic in double.
+TM_FN float tm_log2f(float x) {
+  const double T[16][2] = {
+      {0x1.661ec79f8f3bep+0, -0x1.efec65b963019p-2}, {0x1.571ed4aaf883dp+0, -0x1.b0b6832d4fca4p-2},
+      {0x1.49539f0f010b0p+0, -0x1.7418b0a1fb77bp-2}, {0x1.3c995b0b80385p+0, -0x1.39de91a6dcf7bp-2},
+      {0x1.30d190c8864a5p+0, -0x1.01d9bf3f2b631p-2}, {0x1.25e227b0b8ea0p+0, -0x1.97c1d1b3b7af0p-3},
+      {0x1.1bb4a4a1a343fp+0, -0x1.2f9e393af3c9fp-3}, {0x1.12358f08ae5bap+0, -0x1.960cbbf788d5cp-4},
+      {0x1.0953f419900a7p+0, -0x1.a6f9db6475fcep-5}, {0x1.0000000000000p+0, 0x0.0p+0},
+      {0x1.e608cfd9a47acp-1, 0x1.338ca9f24f53dp-4}, {0x1.ca4b31f026aa0p-1, 0x1.476a9543891bap-3},
+      {0x1.b2036576afce6p-1, 0x1.e840b4ac4e4d2p-3}, {0x1.9c2d163a1aa2dp-1, 0x1.40645f0c6651cp-2},
+      {0x1.886e6037841edp-1, 0x1.88e9c2c1b9ff8p-2}, {0x1.767dcf5534862p-1, 0x1.ce0a44eb17bccp-2}};
+  const double A0 = -0x1.712b6f70a7e4dp-2, A1 = 0x1.ecabf496832ep-2, A2 = -0x1.715479ffae3dep-1,
+               A3 = 0x1.715475f35c8b8p0;
+  u32 ix = tm_f2u(x);
+  if (ix == 0x3f800000u) return 0.0f;
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+    if (ix * 2u == 0u) return -__builtin_inff();
+    if (ix == 0x7f800000u) return x;
+    if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return __builtin_nanf("");
+    ix = tm_f2u(x * 0x1p23f);
+    ix -= 23u << 23;
+  }
+  const u32 tmp = ix - 0x3f330000u;
+  const int i = (int)((tmp >> 19) % 16u);
+  const u32 top = tmp & 0xff800000u;
+  const u32 iz = ix - top;
+  const int k = (i32)tmp >> 23;
+  const double z = (double)tm_u2f(iz);
+  const double r = __builtin_fma(z, T[i][0], -1.0);
+  const double y0 = T[i][1] + (double)k;
+  const double r2 = r * r;
+  double y = __builtin_fma(A1, r, A2);
+  y = __builtin_fma(A0, r2, y);
+  const double p = __builtin_fma(A3, r, y0);
+  y = __builtin_fma(y, r2, p);
+  return (float)y;
+}
+
+// ---------------------------------------------------------------------------------------------- expm1f
+// fdlibm's float expm1f as glibc 2.35 builds it (generic code, float arithmetic, no contraction): x = k ln2 + r,
+// |r| <= ln2 / 2 (hi / lo parts), expm1(r) by a rational form with R(r^2/2) (five coefficients), then
+// 2^k (1 + expm1(r)) - 1 assembled so that no cancellation loses bits.
+TM_FN float tm_expm1f(float x) {
+  const float huge = 1.0e+30f, tiny = 1.0e-30f, o_threshold = 8.8721679688e+01f, ln2_hi = 6.9313812256e-01f,
+              ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f, Q1 = -3.3333335072e-02f,
+              Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
+  float y, hi, lo, c = 0.0f, t, e, hxs, hfx, r1;
+  i32 k;
+  u32 hx = tm_f2u(x);
+  const u32 xsb = hx & 0x80000000u;
+  hx &= 0x7fffffffu;
+  if (hx >= 0x4195b844u) {                       // |x| >= 27 ln2
+    if (hx >= 0x42b17218u) {                     // |x| >= 88.721...
+      if (hx > 0x7f800000u) return x + x;
+      if (hx == 0x7f800000u) return xsb == 0u ? x : -1.0f;
+      if (x > o_threshold) return huge * huge;
+    }
+    if (xsb != 0u) {                             // x < -27 ln2
+      if (x + tiny < 0.0f) return tiny - 1.0f;
+    }
+  }
+  if (hx > 0x3eb17218u) {                        // |x| > 0.5 ln2
+    if (hx < 0x3F851592u) {                      // and |x| < 1.5 ln2
+      if (xsb == 0u) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+      else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+    } else {
+      k = (i32)(invln2 * x + (xsb == 0u ? 0.5f : -0.5f));
+      t = (float)k;
+      hi = x - t * ln2_hi;
+      lo = t * ln2_lo;
+    }
+    x = hi - lo;
+    c = (hi - x) - lo;
+  } else if (hx < 0x33000000u) {                 // |x| < 2^-25
+    t = huge + x;
+    return x - (t - (huge + x));
+  } else {
+    k = 0;
+  }
+  hfx = 0.5f * x;
+  hxs = x * hfx;
+  r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  t = 3.0f - r1 * hfx;
+  e = hxs * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hxs);
+  e = (x * (e - c) - c);
+  e -= hxs;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) {
+    if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+    return 1.0f + 2.0f * (x - e);
+  }
+  if (k <= -2 || k > 56) {                       // suffice to return exp(x) - 1
+    i32 i;
+    y = 1.0f - (e - x);
+    i = (i32)tm_f2u(y);
+    y = tm_u2f((u32)(i + (k << 23)));
+    return y - 1.0f;
+  }
+  if (k < 23) {
+    t = tm_u2f(0x3f800000u - (0x1000000u >> k));   // 1 - 2^-k
+    y = t - (e - x);
+    y = tm_u2f((u32)((i32)tm_f2u(y) + (k << 23)));
+  } else {
+    t = tm_u2f((u32)((0x7f - k) << 23));         // 2^-k
+    y = x - (e + t);
+    y += 1.0f;
+    y = tm_u2f((u32)((i32)tm_f2u(y) + (k << 23)));
+  }
+  return y;
+}
+
+// ---------------------------------------------------------------------------------------------- log1pf
+// fdlibm's float log1pf as glibc 2.35 builds it: 1 + x = 2^k (1 + f), sqrt(2)/2 < 1 + f < sqrt(2), a correction
+// term c for the rounding of 1 + x, log(1 + f) = f - s (f - R) with s = f / (2 + f) and R a polynomial in s^2.
+TM_FN float tm_log1pf(float x) {
+  const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, two25 = 3.355443200e+07f,
+              Lp1 = 6.6666668653e-01f, Lp2 = 4.0000000596e-01f, Lp3 = 2.8571429849e-01f, Lp4 = 2.2222198546e-01f,
+              Lp5 = 1.8183572590e-01f, Lp6 = 1.5313838422e-01f, Lp7 = 1.4798198640e-01f;
+  float hfsq, f = 0.0f, c = 0.0f, s, z, R, u;
+  i32 k, hu = 0;
+  const i32 hx = (i32)tm_f2u(x);
+  const i32 ax = hx & 0x7fffffff;
+  k = 1;
+  if (hx < 0x3ed413d7) {                         // x < 0.41422
+    if (ax >= 0x3f800000) {                      // x <= -1
+      if (x == -1.0f) return -__builtin_inff();
+      return __builtin_nanf("");
+    }
+    if (ax < 0x31000000) {                       // |x| < 2^-29
+      if (ax < 0x24800000) return x;             // |x| < 2^-54
+      return x - x * x * 0.5f;
+    }
+    if (hx > 0 || hx <= (i32)0xbe95f61fu) { k = 0; f = x; hu = 1; }     // -0.2929 < x < 0.41422
+  } else if (hx >= 0x7f800000) {
+    return x + x;
+  }
+  if (k != 0) {
+    if (hx < 0x5a000000) {
+      u = 1.0f + x;
+      hu = (i32)tm_f2u(u);
+      k = (hu >> 23) - 127;
+      c = (k > 0) ? 1.0f - (u - x) : x - (u - 1.0f);      // the rounding of 1 + x
+      c /= u;
+    } else {
+      u = x;
+      hu = (i32)tm_f2u(u);
+      k = (hu >> 23) - 127;
+      c = 0.0f;
+    }
+    hu &= 0x007fffff;
+    if (hu < 0x3504f7) {
+      u = tm_u2f((u32)(hu | 0x3f800000));        // normalise u
+    } else {
+      k += 1;
+      u = tm_u2f((u32)(hu | 0x3f000000));        // normalise u / 2
+      hu = (0x00800000 - hu) >> 2;
+    }
+    f = u - 1.0f;
+  }
+  hfsq = 0.5f * f * f;
+  if (hu == 0) {                                 // |f| < 2^-20
+    if (f == 0.0f) {
+      if (k == 0) return 0.0f;
+      c += (float)k * ln2_lo;
+      return (float)k * ln2_hi + c;
+    }
+    R = hfsq * (1.0f - 0.66666666666666666f * f);
+    if (k == 0) return f - R;
+    return (float)k * ln2_hi - ((R - ((float)k * ln2_lo + c)) - f);
+  }
+  s = f / (2.0f + f);
+  z = s * s;
+  R = z * (Lp1 + z * (Lp2 + z * (Lp3 + z * (Lp4 + z * (Lp5 + z * (Lp6 + z * Lp7))))));
+  if (k == 0) return f - (hfsq - s * (hfsq + R));
+  return (float)k * ln2_hi - ((hfsq - (s * (hfsq + R) + ((float)k * ln2_lo + c))) - f);
+}
+
+// ----------------------------------------------------------------------------------------------- tanhf
+// fdlibm's float tanhf as glibc 2.35 builds it, on tm_expm1f: |x| < 1: -t / (t + 2) with t = expm1(-2|x|);
+// 1 <= |x| < 22: 1 - 2 / (expm1(2|x|) + 2); beyond, +-1.
+TM_FN float tm_tanhf(float x) {
+  const i32 jx = (i32)tm_f2u(x), ix = jx & 0x7fffffff;
+  float t, z;
+  if (ix >= 0x7f800000) return jx >= 0 ? 1.0f / x + 1.0f : 1.0f / x - 1.0f;
+  if (ix < 0x41b00000) {                         // |x| < 22
+    if (ix == 0) return x;
+    if (ix < 0x24000000) return x * (1.0f + x);  // |x| < 2^-55
+    if (ix >= 0x3f800000) {
+      t = tm_expm1f(2.0f * __builtin_fabsf(x));
+      z = 1.0f - 2.0f / (t + 2.0f);
+    } else {
+      t = tm_expm1f(-2.0f * __builtin_fabsf(x));
+      z = -t / (t + 2.0f);
+    }
+  } else {
+    z = 1.0f - 1.0e-30f;
+  }
+  return jx >= 0 ? z : -z;
+}
+
+// ---------------------------------------------------------------------------------------------- logistic
+// lax.logistic as the reference's CPU target computes it (op_table.py:243-247): 1 / (1 + expf(-x)), IEEE.
+TM_FN float tm_logisticf(float x) { return 1.0f / (1.0f + tm_expf(-x)); }
+
+// ------------------------------------------------------------------------------------------------ powf
+// the powf of glibc 2.35 (ARM optimized-routines): x^y = 2^(y log2 x), log2 x in double from tm_log2f's table by a
+// quintic, 2^t from tm_exp2f's table and cubic with the result's sign folded into the table index for negative x
+// with odd integer y; special cases first (y zero / inf / NaN, x zero / inf / NaN, negative x, subnormal x).
+TM_FN int tm_powf_checkint(u32 iy) {              // 0: not an integer, 1: odd, 2: even
+  const int e = (int)(iy >> 23 & 0xffu);
+  if (e < 0x7f) return 0;
+  if (e > 0x7f + 23) return 2;
+  if (iy & ((1u << (0x7f + 23 - e)) - 1u)) return 0;
+  if (iy & (1u << (0x7f + 23 - e))) return 1;
+  return 2;
+}
+TM_FN bool tm_zeroinfnanf(u32 ix) { return 2u * ix - 1u >= 2u * 0x7f800000u - 1u; }
+TM_FN bool tm_issnanf(u32 ix) { return (ix & 0x7fc00000u) == 0x7f800000u && (ix & 0x7fffffu) != 0u; }
+TM_FN float tm_powf(float x, float y) {
+  const double T[16][2] = {
+      {0x1.661ec79f8f3bep+0, -0x1.efec65b963019p-2}, {0x1.571ed4aaf883dp+0, -0x1.b0b6832d4fca4p-2},
+      {0x1.49539f0f010b0p+0, -0x1.7418b0a1fb77bp-2}, {0x1.3c995b0b80385p+0, -0x1.39de91a6dcf7bp-2},
+      {0x1.30d190c8864a5p+0, -0x1.01d9bf3f2b631p-2}, {0x1.25e227b0b8ea0p+0, -0x1.97c1d1b3b7af0p-3},
+      {0x1.1bb4a4a1a343fp+0, -0x1.2f9e393af3c9fp-3}, {0x1.12358f08ae5bap+0, -0x1.960cbbf788d5cp-4},
+      {0x1.0953f419900a7p+0, -0x1.a6f9db6475fcep-5}, {0x1.0000000000000p+0, 0x0.0p+0},
+      {0x1.e608cfd9a47acp-1, 0x1.338ca9f24f53dp-4}, {0x1.ca4b31f026aa0p-1, 0x1.476a9543891bap-3},
+      {0x1.b2036576afce6p-1, 0x1.e840b4ac4e4d2p-3}, {0x1.9c2d163a1aa2dp-1, 0x1.40645f0c6651cp-2},
+      {0x1.886e6037841edp-1, 0x1.88e9c2c1b9ff8p-2}, {0x1.767dcf5534862p-1, 0x1.ce0a44eb17bccp-2}};
+  const double A0 = 0x1.27616c9496e0bp-2, A1 = -0x1.71969a075c67ap-2, A2 = 0x1.ec70a6ca7baddp-2,
+               A3 = -0x1.7154748bef6c8p-1, A4 = 0x1.71547652ab82bp0;
+  const double SHIFT = 0x1.8p+52 / 32, C0 = 0x1.c6af84b912394p-5, C1 = 0x1.ebfce50fac4f3p-3,
+               C2 = 0x1.62e42ff0c52d6p-1;
+  const u64 SIGN_BIAS = 1ull << (5 + 11);
+  u64 sign_bias = 0;
+  u32 ix = tm_f2u(x);
+  const u32 iy = tm_f2u(y);
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u || tm_zeroinfnanf(iy)) {
+    if (tm_zeroinfnanf(iy)) {
+      if (2u * iy == 0u) return tm_issnanf(ix) ? x + y : 1.0f;
+      if (ix == 0x3f800000u) return tm_issnanf(iy) ? x + y : 1.0f;
+      if (2u * ix > 2u * 0x7f800000u || 2u * iy > 2u * 0x7f800000u) return x + y;
+      if (2u * ix == 2u * 0x3f800000u) return 1.0f;
+      if ((2u * ix < 2u * 0x3f800000u) == !(iy & 0x80000000u)) return 0.0f;
+      return y * y;
+    }
+    if (tm_zeroinfnanf(ix)) {
+      float x2 = x * x;
+      if ((ix & 0x80000000u) && tm_powf_checkint(iy) == 1) x2 = -x2;
+      return (iy & 0x80000000u) ? 1.0f / x2 : x2;
+    }
+    if (ix & 0x80000000u) {                      // finite x < 0
+      const int yint = tm_powf_checkint(iy);
+      if (yint == 0) return __builtin_nanf("");
+      if (yint == 1) sign_bias = SIGN_BIAS;
+      ix &= 0x7fffffffu;
+    }
+    if (ix < 0x00800000u) {                      // subnormal x: normalise
+      ix = tm_f2u(x * 0x1p23f);
+      ix &= 0x7fffffffu;
+      ix -= 23u << 23;
+    }
+  }
+  // log2 x
+  const u32 tmp = ix - 0x3f330000u;
+  const int i = (int)((tmp >> 19) % 16u);
+  const u32 top = tmp & 0xff800000u;
+  const u32 iz = ix - top;
+  const int k = (i32)top >> 23;
+  const double z = (double)tm_u2f(iz);
+  const double r = __builtin_fma(z, T[i][0], -1.0);
+  const double y0 = T[i][1] + (double)k;
+  const double r2 = r * r;
+  double yy = __builtin_fma(A0, r, A1);
+  const double p = __builtin_fma(A2, r, A3);
+  const double r4 = r2 * r2;
+  double q = __builtin_fma(A4, r, y0);
+  q = __builtin_fma(p, r2, q);
+  yy = __builtin_fma(yy, r4, q);
+  const double ylogx = (double)y * yy;
+  if (((tm_d2u(ylogx) >> 47) & 0xffffu) >= (tm_d2u(126.0) >> 47)) {
+    if (ylogx > 0x1.fffffffd1d571p+6) return sign_bias ? -__builtin_inff() : __builtin_inff();
+    if (ylogx <= -150.0) return sign_bias ? -0.0f : 0.0f;
+  }
+  // 2^ylogx
+  double kd = ylogx + SHIFT;
+  const u64 ki = tm_d2u(kd);
+  kd -= SHIFT;
+  const double rr = ylogx - kd;
+  const u64 TT[32] = {
+      0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+      0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+      0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+      0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+      0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+      0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+  u64 t = TT[ki % 32u];
+  t += (ki + sign_bias) << 47;
+  const double s = tm_u2d(t);
+  const double zz = __builtin_fma(C0, rr, C1);
+  const double rr2 = rr * rr;
+  double w = __builtin_fma(C2, rr, 1.0);
+  w = __builtin_fma(zz, rr2, w);
+  w = w * s;
+  return (float)w;
+}
+
+// lax.logistic of float64 as the reference's CPU target computes it (op_table.py:243-247): 1 / (1 + exp(-x)), with
+// the device's exp (float64 takes the device math library).
+#if defined(__HIP__) || defined(__HIPCC_RTC__)
+TM_DFN double tm_logistic_d(double x) { return 1.0 / (1.0 + exp(-x)); }
+#endif
+

@@ -339,6 +339,31 @@ erf_inv = _u("erf_inv")
 floor = _u("floor")
 ceil = _u("ceil")
 logistic = _u("logistic")
+exp2 = _u("exp2")
+log2 = _u("log2")
+atan = _u("atan")
+asin = _u("asin")
+acos = _u("acos")
+sinh = _u("sinh")
+cosh = _u("cosh")
+asinh = _u("asinh")
+acosh = _u("acosh")
+atanh = _u("atanh")
+cbrt = _u("cbrt")
+erf = _u("erf")
+erfc = _u("erfc")
+lgamma = _u("lgamma")
+
+
+def nextafter(x1, x2):
+    """lax.nextafter: the float after x1 in the direction of x2 (IEEE nextafter)."""
+    return C.binop("nextafter", C._float_of(x1), C._float_of(x2))
+
+
+def is_finite(x):
+    if not C.is_traced(x) or C._kind(x.dtype) != 2:
+        raise C.TraceError("lax.is_finite needs a traced float operand")
+    return C.bind("is_finite", [x.var], [C.AVal(x.shape, C.BOOL)])[0]
 
 
 def atan2(y, x):

@@ -16,6 +16,10 @@ exp, log, log1p, expm1 = _lax.exp, _lax.log, _lax.log1p, _lax.expm1
 sin, cos, tan, tanh = _lax.sin, _lax.cos, _lax.tan, _lax.tanh
 sqrt, floor, ceil = _lax.sqrt, _lax.floor, _lax.ceil
 arctan2 = _lax.atan2
+exp2, log2 = _lax.exp2, _lax.log2
+arctan, arcsin, arccos = _lax.atan, _lax.asin, _lax.acos
+sinh, cosh, arcsinh, arccosh, arctanh = _lax.sinh, _lax.cosh, _lax.asinh, _lax.acosh, _lax.atanh
+cbrt, nextafter, isfinite = _lax.cbrt, _lax.nextafter, _lax.is_finite
 
 
 def asarray(x, dtype=None):

@@ -35,6 +35,8 @@ static float ref_erfinvf(float y) {
   if (!(y > -1.0f && y < 1.0f)) return y == 1.0f ? INFINITY : (y == -1.0f ? -INFINITY : NAN);
   return y == 0.0f ? y : (float)copysign(ref_giles(y), (double)y); }
 
+static float ref_logistic(float x) { return 1.0f / (1.0f + expf(-x)); }   // op_table.py:243-247
+
 int main(int argc, char** argv) {
   if (argc > 1 && !strcmp(argv[1], "uniform")) {
     long n = 0, bad = 0;
@@ -104,19 +106,62 @@ int main(int argc, char** argv) {
     else if (!strcmp(argv[2], "sinf")) { mine = tm_sinf; ref = sinf; }
     else if (!strcmp(argv[2], "cosf")) { mine = tm_cosf; ref = cosf; }
     else if (!strcmp(argv[2], "atanf")) { mine = tm_atanf; ref = atanf; }
+    else if (!strcmp(argv[2], "exp2f")) { mine = tm_exp2f; ref = exp2f; }
+    else if (!strcmp(argv[2], "log2f")) { mine = tm_log2f; ref = log2f; }
+    else if (!strcmp(argv[2], "expm1f")) { mine = tm_expm1f; ref = expm1f; }
+    else if (!strcmp(argv[2], "log1pf")) { mine = tm_log1pf; ref = log1pf; }
+    else if (!strcmp(argv[2], "tanhf")) { mine = tm_tanhf; ref = tanhf; }
+    else if (!strcmp(argv[2], "logistic")) { mine = tm_logisticf; ref = ref_logistic; }
     if (!mine) return 2;
     const uint64_t stride = strtoull(argv[3], nullptr, 0), off = strtoull(argv[4], nullptr, 0);
     long n = 0, bad = 0, maxulp = 0;
-    for (uint64_t u = off; u < (1ull << 32); u += stride) {
-      const float x = tm_u2f((uint32_t)u), a = mine(x), b = ref(x);
-      ++n;
-      if (std::isnan(a) && std::isnan(b)) continue;
-      if (tm_f2u(a) == tm_f2u(b)) continue;
-      if (++bad <= 5) printf("  x=%a (0x%08x) tm=%a glibc=%a\n", x, (uint32_t)u, a, b);
-      const long d = labs((long)(int32_t)tm_f2u(a) - (long)(int32_t)tm_f2u(b));
-      if (d > maxulp) maxulp = d;
+    // (OpenMP over 2^16 blocks of bit patterns; a block's first argument is the next multiple of stride past off)
+#pragma omp parallel for reduction(+ : n, bad) reduction(max : maxulp) schedule(dynamic, 16)
+    for (int64_t blk = 0; blk < (1ll << 16); ++blk) {
+      const uint64_t lo = (uint64_t)blk << 16, hi = lo + (1ull << 16);
+      uint64_t u = lo <= off ? off : off + (lo - off + stride - 1) / stride * stride;
+      for (; u < hi; u += stride) {
+        const float x = tm_u2f((uint32_t)u), a = mine(x), b = ref(x);
+        ++n;
+        if (std::isnan(a) && std::isnan(b)) continue;
+        if (tm_f2u(a) == tm_f2u(b)) continue;
+        ++bad;
+        const long d = labs((long)(int32_t)tm_f2u(a) - (long)(int32_t)tm_f2u(b));
+        if (d > maxulp) maxulp = d;
+      }
     }
     printf("%s: %ld arguments, %ld mismatches, max %ld ulp\n", argv[2], n, bad, maxulp);
+    return 0;
+  }
+  if (argc > 3 && !strcmp(argv[1], "powf")) {
+    // n random (x, y) pairs: half over all bit patterns, half with x near 1 and |y| moderate (results in range),
+    // then every pair of a grid of special values
+    long n = atol(argv[2]);
+    srand48(atol(argv[3]));
+    long bad = 0, maxulp = 0, tot = 0;
+    auto chk = [&](float x, float y) {
+      const float a = tm_powf(x, y), b = powf(x, y);
+      ++tot;
+      if ((std::isnan(a) && std::isnan(b)) || tm_f2u(a) == tm_f2u(b)) return;
+      if (++bad <= 5) printf("  powf(%a, %a) tm=%a glibc=%a\n", x, y, a, b);
+      const long d = labs((long)(int32_t)tm_f2u(a) - (long)(int32_t)tm_f2u(b));
+      if (d > maxulp) maxulp = d;
+    };
+    for (long i = 0; i < n; ++i) {
+      const uint32_t bx = (uint32_t)mrand48(), by = (uint32_t)mrand48();
+      chk(tm_u2f(bx), tm_u2f(by));
+      const float x = (float)(0.5 + drand48() * 3.0) * (i & 1 ? 1.0f : -1.0f);
+      const float y = (float)((drand48() - 0.5) * 120.0);
+      chk(x, y);
+      chk(x, (float)(int)y);
+      chk(tm_u2f((bx & 0x007fffffu) | 0x3f800000u), (float)((drand48() - 0.5) * 2e7));
+    }
+    const float sp[] = {0.0f, -0.0f, 1.0f, -1.0f, 0.5f, -0.5f, 2.0f, -2.0f, 3.0f, -3.0f, INFINITY, -INFINITY, NAN,
+                        1e-45f, -1e-45f, 1e-40f, 3.4e38f, -3.4e38f, 1.0000001f, 0.99999994f, 126.0f, -126.0f,
+                        150.0f, -150.0f, 127.5f, 0.25f, 16777217.0f, -16777217.0f, 8388609.0f, 1e10f, -1e10f};
+    for (float x : sp)
+      for (float y : sp) chk(x, y);
+    printf("powf: %ld pairs, %ld mismatches, max %ld ulp\n", tot, bad, maxulp);
     return 0;
   }
   if (argc > 3 && !strcmp(argv[1], "atan2")) {

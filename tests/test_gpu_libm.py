@@ -1,0 +1,103 @@
+"""Every transcendental the reference's op table lowers (op_table.py:199-223, 407-427: exp exp2 log log1p expm1 log2
+sin cos tan asin acos atan atan2 sinh cosh tanh asinh acosh atanh cbrt erf erfc lgamma logistic pow nextafter
+erf_inv), float32 and float64, evaluated on the device by one item each and compared with the host's glibc (the
+reference CPU target's math library, host.py:43-48) on the same arguments: random bit patterns (every class,
+NaN and infinities included), uniform draws over each function's working range and special values.
+
+  glibc-bitwise (float32 restatements in tm_libm.h): exp exp2 log log1p expm1 log2 sin cos atan atan2 tanh pow
+      logistic erf_inv -- and nextafter (IEEE-exact) in both widths.  Bitwise, NaN == NaN.
+  the device math library (ROCm's OCML): the other float32 functions and all float64 ones.  Each within the ulp
+      bound stated in BOUNDS (measured, with margin): not glibc's bits, so an integer taken from such a result
+      can differ from the reference CPU target's when the result lies within that many ulps of an integer
+      boundary.  The fraction of bitwise-equal results is printed."""
+import numpy as np
+import pytest
+
+import tallymap_amd as tm
+from tallymap_amd import lax
+
+pytestmark = pytest.mark.gpu
+
+UNARY = ("exp", "exp2", "log", "log1p", "expm1", "log2", "sin", "cos", "tan", "asin", "acos", "atan", "sinh", "cosh",
+         "tanh", "asinh", "acosh", "atanh", "cbrt", "erf", "erfc", "lgamma", "logistic", "erf_inv")
+BINARY = ("pow", "atan2", "nextafter")
+BITWISE32 = {"exp", "exp2", "log", "log1p", "expm1", "log2", "sin", "cos", "atan", "tanh", "logistic", "erf_inv",
+             "pow", "atan2", "nextafter"}
+BITWISE64 = {"nextafter"}
+# largest ulp distance from glibc accepted for the device-library functions (non-NaN results), measured on MI355X
+# with margin: float32 tan asin acos sinh acosh atanh erf 2, cosh asinh cbrt 1, erfc 4; float64 1 to 2, cbrt 3,
+# erfc 4.  lgamma is near its zeros (x = 1, 2) and for negative arguments far in ulps of a result near 0
+# (float32 136, float64 16 measured): its own bound.
+BOUNDS = {np.float32: 4, np.float64: 4}
+LGAMMA_BOUNDS = {np.float32: 256, np.float64: 32}
+RANGES = {"asin": (-1, 1), "acos": (-1, 1), "atanh": (-1, 1), "acosh": (1, 200), "lgamma": (0.01, 40),
+          "erf_inv": (-1, 1), "log": (1e-6, 1e6), "log2": (1e-6, 1e6), "log1p": (-0.99, 100)}
+
+
+def _fn(name):
+    return {"atan2": lax.atan2, "pow": lax.pow, "nextafter": lax.nextafter,
+            "erf_inv": lax.erf_inv}.get(name) or getattr(lax, name)
+
+
+def _inputs(dt, n=1 << 15, seed=7):
+    rng = np.random.default_rng(seed)
+    it = np.uint32 if dt == np.float32 else np.uint64
+    bits = rng.integers(0, np.iinfo(it).max, n, dtype=it, endpoint=True).view(dt)
+    spec = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 2.0, 1e-30, -1e-30, 1e30, np.inf, -np.inf, np.nan, 3.0, -3.0,
+                     0.1, 10.0, 100.0, 1e-40 if dt == np.float32 else 1e-310], dt)
+    return bits, spec, rng
+
+
+def _ulps(a, b, dt):
+    it = np.int32 if dt == np.float32 else np.int64
+    ia, ib = a.view(it).astype(np.int64), b.view(it).astype(np.int64)
+    ia = np.where(ia < 0, np.iinfo(it).min - ia, ia)          # (the ordered integer line of the floats)
+    ib = np.where(ib < 0, np.iinfo(it).min - ib, ib)
+    return np.abs(ia - ib)
+
+
+def _device(items, xs, ys, dt):
+    import torch
+    f = tm.vmap(lambda t, x, y: (t, tuple(g(x, y) for g in items)), outputs={})
+    r = f(xs, ys).per_item
+    torch.cuda.synchronize()
+    return [v.cpu().numpy() for v in r]
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64], ids=["f32", "f64"])
+def test_transcendentals_against_glibc(oracle, dt):
+    print(f"case: {np.dtype(dt).name} transcendentals vs glibc", flush=True)
+    bits, spec, rng = _inputs(dt)
+    names = [n for n in UNARY if not (dt == np.float64 and n == "erf_inv")] + list(BINARY)
+    cols = {}
+    for name in names:
+        lo, hi = RANGES.get(name, (-20, 20))
+        rnd = rng.uniform(lo, hi, bits.size).astype(dt)
+        cols[name] = np.concatenate([bits, rnd, spec])
+    n = next(iter(cols.values())).size
+    ys = np.concatenate([rng.integers(0, np.iinfo(np.uint32 if dt == np.float32 else np.uint64).max, bits.size,
+                                      dtype=np.uint32 if dt == np.float32 else np.uint64, endpoint=True).view(dt),
+                         rng.uniform(-30, 30, bits.size).astype(dt), np.resize(spec, spec.size)]).astype(dt)
+    # one kernel: every function on its own column (the columns share the item's two operands by index)
+    X = np.stack([cols[k] for k in names], 1)
+    got = _device([(lambda x, y, j=j, k=k: _fn(k)(x[j], y) if k in BINARY else _fn(k)(x[j]))
+                   for j, k in enumerate(names)], X, ys, dt)
+    report = []
+    for j, name in enumerate(names):
+        want = oracle.libm(name, X[:, j], ys if name in BINARY else None, dt)
+        g = got[j]
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(g), nan), (name, np.flatnonzero(np.isnan(g) != nan)[:4])
+        same = (g.view(np.uint32 if dt == np.float32 else np.uint64) ==
+                want.view(np.uint32 if dt == np.float32 else np.uint64)) | nan
+        frac = same.mean()
+        if name in (BITWISE32 if dt == np.float32 else BITWISE64):
+            bad = np.flatnonzero(~same)
+            assert bad.size == 0, (name, X[bad[:4], j], g[bad[:4]], want[bad[:4]])
+        else:
+            ok = ~nan                        # (an overflow boundary an ulp apart: inf vs the largest float is 1 ulp)
+            u = _ulps(g[ok], want[ok], dt)
+            assert u.max(initial=0) <= (LGAMMA_BOUNDS if name == "lgamma" else BOUNDS)[dt], (name, int(u.max()))
+            frac = f"{frac:.5f} bitwise, max {int(u.max(initial=0))} ulp"
+        report.append(f"{name}: {frac}")
+    print("; ".join(report), flush=True)

@@ -121,13 +121,22 @@ def test_erfinv_log_absolute_error(libm):
     assert r.returncode == 0, r.stdout
 
 
-@pytest.mark.parametrize("fn", ["logf", "expf", "sinf", "cosf", "atanf"])
+@pytest.mark.parametrize("fn", ["logf", "expf", "sinf", "cosf", "atanf", "exp2f", "log2f", "expm1f", "log1pf",
+                                "tanhf", "logistic"])
 def test_f32_libm_bitwise_equal_to_glibc(libm, fn):
-    """tm_libm.h's float functions against this host's glibc on every 251st bit pattern (17.1M arguments: every
-    exponent, sign, NaN and infinity class; 2^32 exhaustively with `libm_check f32 <fn> 1 0`, 0 mismatches)."""
-    r = subprocess.run([libm, "f32", fn, "251", "7"], capture_output=True, text=True)
+    """tm_libm.h's float functions against this host's glibc on EVERY one of the 2^32 bit patterns (OpenMP over the
+    host's cores): 0 mismatches.  logistic is the reference CPU target's 1 / (1 + expf(-x))."""
+    r = subprocess.run([libm, "f32", fn, "1", "0"], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert ", 0 mismatches" in r.stdout, r.stdout
+    assert f"{fn}: 4294967296 arguments, 0 mismatches" in r.stdout, r.stdout
+
+
+def test_powf_bitwise_equal_to_glibc(libm):
+    """tm_powf against glibc's powf: 40M pairs (random bit patterns; x near 1 with |y| up to 1e7; moderate x with
+    integer and non-integer y, both signs) and every pair of a grid of special values (zeros, infinities, NaN,
+    subnormals, +-1, overflow and underflow edges): 0 mismatches."""
+    r = subprocess.run([libm, "powf", "10000000", "3"], capture_output=True, text=True)
+    assert r.returncode == 0 and ", 0 mismatches" in r.stdout, r.stdout
 
 
 def test_atan2f_bitwise_equal_to_glibc(libm):
