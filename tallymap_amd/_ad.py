@@ -70,14 +70,20 @@ def relevance(jx, out_rel, emits=True):
     return [isinstance(v, C.Var) and v.id in rel for v in jx.invars]
 
 
-def eval_jaxpr(jx, args, ct_read=None):
+def eval_jaxpr(jx, args, ct_read=None, ct_emit=None):
     """re-bind jx's equations on `args` (Tracers / numpy scalars) in the current trace -> its outputs.
-    ct_read(slot, idx) replaces the `tm_ct_read` primitive of a VJP program."""
+    ct_read(slot, idx) replaces the `tm_ct_read` primitive of a VJP program, ct_emit(tag, idx, value) its
+    `tm_ct_emit` (a sparse table-read cotangent: vjp_jaxpr's `sparse`)."""
     env = {v.id: a for v, a in zip(jx.invars, args)}
     for e in jx.eqns:
         ins = [_t(v, env) for v in e.invars]
         if e.prim == "tm_ct_read" and ct_read is not None:
             outs = [ct_read(e.params["slot"], ins[0])]
+        elif e.prim == "tm_ct_emit":
+            if ct_emit is None:
+                raise ADError("internal: a sparse table-read cotangent with no emit target")
+            ct_emit(e.params["tag"], ins[0], ins[1])
+            outs = []
         else:
             outs = _replay(e, ins)
         for o, x in zip(e.outvars, outs):
@@ -111,14 +117,23 @@ def _zeros_like(aval):
     return _f(0, aval.dtype)
 
 
-def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=None, with_primal=False):
+def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=None, with_primal=False,
+              sparse=None, prune=False):
     """-> (Jaxpr, ct_out_mask, ct_in_mask).
     The Jaxpr's invars: jx.invars + [cotangent of each output in ct_out_mask]; outvars: [cotangent of each input
     in ct_in_mask], preceded (with_primal) by jx's own outputs, replayed: one program for a step and its VJP.  ct_out_mask: jx's active float outputs; ct_in_mask: jx's active inputs.
     ct_read(slot, idx) -> the cotangent tally value (a Tracer) for an emit into tally `slot` at index idx; slots:
     {invar index of a tally input: its slot}.  ct_given: outputs whose cotangent may be nonzero (default: all); the
-    others get no cotangent input."""
+    others get no cotangent input.
+    sparse: {invar index: tag} for inputs that are broadcast tables whose cotangents leave the program by emits: a
+    read x[i] of such a table at a traced index sends the read's cotangent out as one `tm_ct_emit` equation per
+    element of the row (params tag; operands: flat element index (clamped row) x row + e, value), instead of a
+    dense cotangent with a select per row of the table (the reference's sparse table-read cotangent,
+    _reverse.py:1047).  Such an input keeps a dense cotangent output only if other uses give it one (ct_in_mask
+    False otherwise).  prune: the same for every input: an active input that no use gives a cotangent (a loop
+    constant the step never reads, say) has ct_in_mask False instead of a zero output."""
     tslot = {jx.invars[i].id: s for i, s in (slots or {}).items()}
+    sp_tag = {jx.invars[i].id: t for i, t in (sparse or {}).items()}
     act = activity(jx, active_in)
     ct_out_mask = [isinstance(v, C.Var) and v.id in act for v in jx.outvars]
     if ct_given is not None:
@@ -170,6 +185,10 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
                 continue
             if not any(o.id in ct for o in e.outvars):
                 continue
+            x0 = e.invars[0] if e.invars else None
+            if e.prim == "dynamic_index" and isinstance(x0, C.Var) and x0.id in sp_tag:
+                _sparse_read_ct(ct[e.outvars[0].id], ins[1], x0.aval, sp_tag[x0.id])
+                continue
             gs = [ct.get(o.id) for o in e.outvars]
             rule = RULES.get(e.prim)
             if rule is None:
@@ -186,6 +205,9 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
                 else:
                     a = np.asarray(x, v.aval.dtype)
                     res.append(C.Lit(np.broadcast_to(a, v.aval.shape).copy(), v.aval.strong()))
+        for i, v in enumerate(jx.invars):         # (a sparse table with no other use: no dense cotangent)
+            if (prune or v.id in sp_tag) and v.id not in ct:
+                ct_in_mask[i] = False
         for v, m in zip(jx.invars, ct_in_mask):
             if m:
                 c = ct.get(v.id)
@@ -503,6 +525,25 @@ def r_concatenate(g, ins, outs, e):
             res.append(None)
         off += n
     return res
+
+
+def _sparse_read_ct(g, i, xav, tag):
+    """the cotangent g of a read x[i] of a sparse table (x: xav, n rows) as emits at flat index
+    clamp(i, 0, n - 1) x row + e, one per element e of the row (a zero cotangent emits nothing)."""
+    if g is None or (not C.is_traced(g) and not np.any(np.asarray(g))):
+        return
+    n = xav.shape[0]
+    r = int(np.prod(xav.shape[1:], dtype=np.int64))
+    row = L.clamp(0, i if C.is_traced(i) else np.int32(i), n - 1) * r
+    gf = _reshape(g, (r,)) if r != 1 or (C.is_traced(g) and g.shape != ()) else g
+    for k in range(r):
+        gk = gf[k] if (C.is_traced(gf) and gf.shape != ()) or (not C.is_traced(gf) and np.ndim(gf)) else gf
+        if not C.is_traced(gk):
+            gk = C.Tracer(C.bind("copy", [C.literal(np.float32(gk), C.F32, False)], [C.AVal((), C.F32)])[0].var)
+        idx = row + k if k else row
+        if not C.is_traced(idx):
+            idx = C.Tracer(C.bind("copy", [C.literal(int(idx), C.I32, False)], [C.AVal((), C.I32)])[0].var)
+        C.bind("tm_ct_emit", [idx.var, gk.var], [], tag=tag)
 
 
 def r_dynamic_index(g, ins, outs, e):

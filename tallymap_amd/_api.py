@@ -681,16 +681,17 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
     dyn = [n for n in names if isinstance(outs_spec[n], Records) and outs_spec[n].capacity is None]
     sized_cache = {}
 
-    def sized(args):
+    def sized(args, n_active=None):
         """the mapped function with every Records capacity fixed for this call's arguments (itself when all are
-        given): the capacity-less ones sized by a count pass to the next power of two >= their record count."""
+        given): the capacity-less ones sized by a count pass to the next power of two >= their record count (over
+        the first n_active items when given, as the call itself runs)."""
         if not dyn:
             return mapped
         if spawn is not None:
             raise ValueError("tallymap: Records outputs of a spawning call need a capacity")
         from . import backend as B
         prog, _, pi, bc, N, _ = prepare(args, "count")
-        o = B.run(prog, pi, bc, N, opts)
+        o = B.run(prog, pi, bc, N, opts, n_active=n_active)
         rnames = [n for n in names if isinstance(outs_spec[n], Records)]
         caps = {}
         for j, r in enumerate(rnames):
@@ -710,14 +711,14 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
         return f
 
     def entry(*args, n_active=None):
-        return (sized(args) if dyn else mapped)(*args, n_active=n_active)
+        return (sized(args, n_active) if dyn else mapped)(*args, n_active=n_active)
 
     for g in (mapped, entry):
         g.__wrapped__ = fn
         g._prepare = prepare
         g._opts = opts
         g._names = names
-        g._sized = sized if dyn else (lambda args: mapped)
+        g._sized = sized if dyn else (lambda args, n_active=None: mapped)
     return entry
 
 
@@ -763,21 +764,25 @@ def _argnums(argnums, nargs):
     return (argnums,) if isinstance(argnums, int) else tuple(argnums)
 
 
-def vjp(mapped, *args, argnums=None):
+def vjp(mapped, *args, argnums=None, n_active=None):
     """(Result, pullback): the forward call, and pullback(ct_outputs, ct_per_item=None) -> the cotangents of the
     positional arguments in `argnums` (float32 ones; broadcast arguments' cotangents are exact float32 sums).
     ct_outputs: {name: array or scalar (broadcast to the output)}.  The pullback launches the replay adjoint: the
-    reference's jax.vjp through tallymap_call (_primitive.py:565-667, _reverse.py:1079-1180)."""
-    res = mapped(*args)
-    return res, _pullback(mapped, args, argnums)
+    reference's jax.vjp through tallymap_call (_primitive.py:565-667, _reverse.py:1079-1180).  n_active=n runs the
+    forward and the adjoint over the first n items only (the others' cotangents are zero), as the reference's
+    n_active composes with jax.vjp (_api.py:469-472)."""
+    res = mapped(*args, n_active=n_active)
+    return res, _pullback(mapped, args, argnums, n_active)
 
 
-def _pullback(mapped, args, argnums):
+def _pullback(mapped, args, argnums, n_active=None):
     from . import backend as B
     from ._tally import RSEP
-    mapped = mapped._sized(args)
+    mapped = mapped._sized(args, n_active)
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     if prog.spawn is not None:
+        if n_active is not None:
+            raise ValueError("tallymap: n_active with spawn is not supported")
         return _tree_pullback(mapped, args, argnums)
     an = _argnums(argnums, len(args))
     vprog, extra, bad = prog, [], False
@@ -787,7 +792,7 @@ def _pullback(mapped, args, argnums):
         # record's slot, so the records' cotangents reach the appended values
         import torch
         vprog = mapped._prepare(args, "adjoint")[0]
-        o = B.run(prog, pi, bc, N, mapped._opts)
+        o = B.run(prog, pi, bc, N, mapped._opts, n_active=n_active)
         for j, (r, cap, _) in enumerate(prog.records):
             extra.append(B.util.exclusive_scan(o.ys[prog.counts[j]]).clamp(max=cap).to(torch.int32))
             bad = bad or bool((o.rcount[j] > cap).item())     # (an output past its capacity: NaN, as the forward)
@@ -810,7 +815,7 @@ def _pullback(mapped, args, argnums):
             for j, x in enumerate(yl):
                 if x is not None:
                     cys[j] = x
-        g_pi, g_bc, ntr = B.run_vjp(vprog, wrt, list(pi) + extra, bc, N, cts, cys, mapped._opts)
+        g_pi, g_bc, ntr = B.run_vjp(vprog, wrt, list(pi) + extra, bc, N, cts, cys, mapped._opts, n_active=n_active)
         if bad:
             g_pi = [x.float().fill_(float("nan")) for x in g_pi]
             g_bc = [x.float().fill_(float("nan")) for x in g_bc]
@@ -900,9 +905,10 @@ def _tree_pullback(mapped, args, argnums):
 def grad(mapped, weights=None, argnums=None):
     """the gradient of sum_name <weights[name], outputs[name]> (weights: a scalar or an array per output; default
     1 for every float output, i.e. the gradient of the sum of all float tallies) w.r.t. the arguments in
-    argnums.  ONE launch of the replay adjoint, no forward launch (as jax.grad of a tallymap call under jit)."""
-    def g(*args):
-        return _pullback(mapped, args, argnums)(
+    argnums.  ONE launch of the replay adjoint, no forward launch (as jax.grad of a tallymap call under jit).  The
+    returned function takes n_active=n as the mapped call does."""
+    def g(*args, n_active=None):
+        return _pullback(mapped, args, argnums, n_active)(
             weights if weights is not None else {n: 1.0 for n in mapped._names})
     return g
 
@@ -935,15 +941,17 @@ def _match_leaves(prim, tan):
     return [tan]
 
 
-def _run_tangents(mapped, args, tans, lanes):
+def _run_tangents(mapped, args, tans, lanes, n_active=None):
     """one launch of the jvp program with `lanes` directions.  tans[pos]: None or a list of `lanes` tangent arrays
     for positional argument pos (its shape) -> (primal Result, per lane {name: tangent tally}, per lane [tangents
     of the float per-item results (None for the others)])."""
     from . import backend as B
-    mapped = mapped._sized(args)
+    mapped = mapped._sized(args, n_active)
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     recs = list(prog.records)
     rs = bool(recs) and prog.spawn is not None
+    if n_active is not None and prog.spawn is not None:
+        raise ValueError("tallymap: n_active with spawn is not supported")
     if rs:      # Records of a spawning call: the recording forward's jvp, then the fill program's over the tree
         prog = mapped._prepare(args, "record")[0]
     pt, bt, pp, pb = [], [], [], []
@@ -968,7 +976,7 @@ def _run_tangents(mapped, args, tans, lanes):
                         tv = torch.zeros(_shape(leaf), dtype=B.torch_dtype(dt), device="cuda")
                     (pt if x == 0 else bt).append(tv)
     q = _jvp_prog(prog, tuple(pp), tuple(pb), lanes)
-    o = B.run(q, list(pi) + pt, list(bc) + bt, N, mapped._opts)
+    o = B.run(q, list(pi) + pt, list(bc) + bt, N, mapped._opts, n_active=n_active)
     names = mapped._names
     nT = prog.nT
     res_out = _sum_outputs(prog, o, names)
@@ -1015,16 +1023,18 @@ def _run_tangents(mapped, args, tans, lanes):
     return primal, t_tal, [unflatten(meta["ytree"], _split_ys(prog, t)[0]) for t in t_ys], meta
 
 
-def jvp(mapped, primals, tangents):
+def jvp(mapped, primals, tangents, n_active=None):
     """(Result, tangent Result): the forward-mode derivative of the mapped call along `tangents` (jax.jvp of a
     tallymap call, reference _api.py:305-345, _primitive.py:419-436).  primals: the positional arguments;
     tangents: one per argument, None (not perturbed) or an array (pytree) of the argument's shape; only float
     leaves are perturbed.  The tangent Result holds the tangent of every float output and of every float per-item
-    result (None for the others); ONE launch of the fused jvp kernel (primal and tangents in one pass)."""
+    result (None for the others); ONE launch of the fused jvp kernel (primal and tangents in one pass).
+    n_active=n runs the first n items only, as the mapped call does."""
     primals, tangents = tuple(primals), tuple(tangents)
     if len(tangents) != len(primals):
         raise ValueError("tallymap: jvp needs one tangent (or None) per primal argument")
-    primal, t_tal, t_ys, _ = _run_tangents(mapped, primals, [None if t is None else [t] for t in tangents], 1)
+    primal, t_tal, t_ys, _ = _run_tangents(mapped, primals, [None if t is None else [t] for t in tangents], 1,
+                                           n_active)
     return primal, Result(t_tal[0], t_ys[0], None, None)
 
 
@@ -1034,8 +1044,8 @@ def jacfwd(mapped, argnums=0):
     tangents of the argument's elements run as dual lanes, up to 16 per fused kernel."""
     an = (argnums,) if isinstance(argnums, int) else tuple(argnums)
 
-    def jac(*args):
-        m = mapped._sized(args)
+    def jac(*args, n_active=None):
+        m = mapped._sized(args, n_active)
         prog, meta, pi, bc, N, axes = m._prepare(args)
         dirs = []
         for a in an:
@@ -1056,7 +1066,7 @@ def jacfwd(mapped, argnums=0):
             for a in an:
                 lanes = [d if aa == a else np.zeros_like(np.asarray(args[a])) for aa, d in chunk]
                 tans[a] = lanes
-            _, t_tal, _, _ = _run_tangents(m, args, tans, len(chunk))
+            _, t_tal, _, _ = _run_tangents(m, args, tans, len(chunk), n_active)
             for l in range(len(chunk)):
                 for n in m._names:
                     if n in t_tal[l]:

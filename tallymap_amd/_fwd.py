@@ -203,7 +203,7 @@ def _jvp_while(e, ins, tins, lanes):
     args = list(cc) + list(bc) + _flat(tbc) + list(init) + t0
     avals = [v.aval for v in e.outvars] + tav
     outs = C.bind("while", _vars(args), avals, cond_jaxpr=cj, body_jaxpr=bj, cond_nconsts=ncc,
-                  body_nconsts=nbc + nbt)
+                  body_nconsts=nbc + nbt, **({"static": True} if e.params.get("static") else {}))
     prim, rest = outs[:nc], outs[nc:]
     touts, k = [], 0
     for m in cm:

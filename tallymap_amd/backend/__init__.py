@@ -415,13 +415,15 @@ def compiled_adjoint(adj, opts):
     return c
 
 
-def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
+def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None):
     """the replay adjoint of prog: cotangents of the per-item operands wrt[0] ([N, ...] each) and the broadcast
     operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
     0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated).
     When no loop carry needs a reverse sweep the adjoint is an ordinary item program (reverse.forward_only_program)
     run by the forward template (step refill); otherwise the replay kernel opts['rev_schedule'] names: 'step' (the
-    default, replay.build: step refill over a tape) or 'item' (reverse.build: in-lane checkpoints)."""
+    default, replay.build: step refill over a tape) or 'item' (reverse.build: in-lane checkpoints).  With n_active
+    only the first n_active items run (the adjoint launches over them alone); the others get zero cotangents and
+    add nothing to the broadcast ones, as they emitted nothing in the forward."""
     import torch
 
     from . import reverse as R
@@ -446,6 +448,12 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
         a = yav[j]
         ins_p.append(device_tensor(x, a.dtype) if x is not None
                      else torch.zeros((N,) + tuple(a.shape), dtype=torch.float32, device="cuda"))
+    N_all = N
+    if n_active is not None:
+        N = int(n_active)
+        if not 0 <= N <= N_all:
+            raise ValueError(f"tallymap: n_active={N} outside [0, N={N_all}]")
+        ins_p = [t[:N] for t in ins_p]
     ins_b = [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
     for k in pl.ft:
         s = prog.tallies[k]
@@ -497,6 +505,13 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts):
         g_bc = [res[L.r_out[j] - base] for j in adj.wrt_bc]
         g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
     ntr = res[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
+    if N != N_all:
+        full = []
+        for g in g_pi:
+            z = torch.zeros((N_all,) + tuple(g.shape[1:]), dtype=g.dtype, device=g.device)
+            z[:N] = g
+            full.append(z)
+        g_pi = full
     return g_pi, g_bc, ntr
 
 

@@ -130,6 +130,10 @@ class Emitter:
         self.n = 0
         self.hooks = dict(hooks or {})      # prim -> rule(em, eqn, ins) (emit, ...: set by the kernel assembler)
         self.prims = set()
+        # the depth of `cond` branches being emitted: code there runs on a divergent subset of the wave's lanes, one
+        # branch after another, so wave-shared LDS state must not pass between branches through plain loads and
+        # first-lane stores (the kernel assembler's spawn and Records rules read it)
+        self.div = 0
 
     # -------------------------------------------------------------------------------- text helpers
     def fresh(self, p="t"):
@@ -648,7 +652,11 @@ def _cond(em, e, ins):
         head = f"if ({idx.el[0]} == {j})" if j == 0 else (f"else if ({idx.el[0]} == {j})" if j < len(brs) - 1
                                                           else "else")
         em.open(head)
-        r = em.run(br, consts + ops)
+        em.div += 1
+        try:
+            r = em.run(br, consts + ops)
+        finally:
+            em.div -= 1
         for k, (ov, x) in enumerate(zip(outs, r)):
             if isinstance(x, VTally):
                 tally_out[k] = x

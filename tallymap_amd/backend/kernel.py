@@ -62,8 +62,9 @@ class Layout:
 
 
 def _split(jx):
-    """-> (index of the only top-level while eqn) or None."""
-    ws = [i for i, e in enumerate(jx.eqns) if e.prim == "while"]
+    """-> (index of the only top-level while eqn that is not a static loop) or None.  A static-bound fori_loop or
+    long scan (equation param static=True) is ordinary straight-line work of its step, as a scan is in JAX."""
+    ws = [i for i, e in enumerate(jx.eqns) if e.prim == "while" and not e.params.get("static", False)]
     return ws[0] if len(ws) == 1 else None
 
 
@@ -379,10 +380,23 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         return t
     em.hooks["tallymap_emit"] = emit_rule
 
+    def emit_slot_rule(em_, e, ins):
+        """an emit addressed by tally slot (params slot) rather than by a threaded tally value: the adjoint's sparse
+        table-read cotangents, emitted where the read's step VJP runs."""
+        emit_rule(em_, C.Eqn("tallymap_emit", [None] + list(e.invars), [], {}), [VTally(int(e.params["slot"]))] + ins)
+        return []
+    em.hooks["tallymap_emit_slot"] = emit_slot_rule
+
     def claim_rule(em_, e, ins):
-        """a Records append's raw slot (tm_rclaim: the wave's batch), -1 when `when` is false."""
+        """a Records append's raw slot (tm_rclaim: the wave's batch), -1 when `when` is false.  Inside a cond
+        branch, tm_rclaim_direct (a counter claim per wave at this point): the batch state passes between appends
+        through plain LDS loads and first-lane stores, sound only where all the wave's lanes run the same code."""
         t, w, _ = ins
         j = int(e.params["r"])
+        if em_.div:
+            sl = em_.bind(f"(i32)tm_rclaim_direct(&((u64*)P.p[{r_rctr}])[{2 * j}], "
+                          f"(u64*)&tm_rcnt{j}[threadIdx.x >> 6], {w.el[0]}, tm_rawcap{j})", C.I32, "sl")
+            return [t, Val([sl], (), C.I32)]
         sl = em_.bind(f"(i32)tm_rclaim(&((u64*)P.p[{r_rctr}])[{2 * j}], &tm_rbase{j}[threadIdx.x >> 6], "
                       f"&tm_rleft{j}[threadIdx.x >> 6], &tm_rcnt{j}[threadIdx.x >> 6], {w.el[0]}, tm_rawcap{j})",
                       C.I32, "sl")
@@ -482,11 +496,14 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         flushes them (_qflush_lines: one ticket claim for all of them, then rows stored to the next generation's
         buffer), and each wave flushes what is left when it exits.  Direct (QS = 0): one ticket claim per wave at
         this point (tm_qclaim) and the row stored at once.  Tickets past the capacity Q are not stored (the host
-        counts them as dropped children)."""
+        counts them as dropped children).  A spawn inside a cond branch is always direct: the staging count passes
+        between spawn points through LDS, and lanes of one wave in two branches run one branch after the other;
+        the compiler, which reasons per lane, may merge the branches' trailing first-lane stores of the count into
+        one after both, so the second branch would stage over the first's rows."""
         t, w, leaves = ins[0], ins[1], ins[2:]
         if Q is None or len(leaves) != len(qav):
             raise RuntimeError("internal: a spawn in a program without a queue of its per-item operands")
-        if not QS:
+        if not QS or em_.div:
             tq = em_.bind(f"tm_qclaim(tm_qctr, {w.el[0]})", C.I64, "tq")
             em_.open(f"if ((u64){tq} < {int(Q)}ull)")
             for i, (lv, a) in enumerate(zip(leaves, qav)):

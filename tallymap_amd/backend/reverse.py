@@ -91,6 +91,9 @@ def split(prog):
     jx = prog.jaxpr
     nT = prog.nT
     ws = [i for i, e in enumerate(jx.eqns) if e.prim == "while"]
+    dyn = [i for i in ws if not jx.eqns[i].params.get("static", False)]
+    if len(ws) > 1 and len(dyn) == 1:
+        ws = dyn                 # (static loops besides it are ordinary work of PRE / POST)
     if len(ws) > 1:
         raise ReverseError(f"reverse mode needs at most one top-level while loop in the item (found {len(ws)})")
     if ws:
@@ -250,6 +253,53 @@ def _ct_reader(ft, S_of, arrays=None):
     return ct_read
 
 
+def sparse_tables(adj, sp):
+    """the differentiated broadcast tables whose table-read cotangents leave by emits (_ad.vjp_jaxpr's sparse):
+    -> (PRE's {invar index: j}, the loop body's {body const index: j}, POST's {P index: j}) for each broadcast
+    operand j in adj.wrt_bc, wherever it enters those programs as itself (a P var that is the operand)."""
+    prog = adj.prog
+    nT, nP = prog.nT, prog.nP
+    wb = set(adj.wrt_bc)
+    bin_id = {v.id: j for j, v in enumerate(sp.pre.invars[nT + nP:]) if j in wb}
+    p_of = {x: bin_id[v.id] for x, v in enumerate(sp.pre.outvars[sp.ncar:])
+            if isinstance(v, C.Var) and v.id in bin_id}
+    pre = {nT + nP + j: j for j in adj.wrt_bc}
+    body = {q: p_of[r[1]] for q, r in enumerate(sp.bconst) if r[0] == "P" and r[1] in p_of}
+    return pre, body, p_of
+
+
+def ct_emitter(adj, base):
+    """the ct_emit hook of _ad.eval_jaxpr for a program whose broadcast-cotangent tallies ct{j} (j in adj.wrt_bc
+    order) start at tally slot `base`: an emit addressed by slot."""
+    order = list(adj.wrt_bc)
+
+    def ct_emit(j, idx, val):
+        C.bind("tallymap_emit_slot", [C.as_var(idx), C.as_var(val)], [], slot=base + order.index(j))
+    return ct_emit
+
+
+def emit_dense_ct(t, v, n):
+    """a broadcast operand's dense cotangent v (a Tracer or a constant of n elements; a scalar applies to each)
+    emitted into its exact cotangent tally t, one emit per element (row-major), none for a constant zero (an
+    exact sum is unchanged by it) -> the tally value."""
+    if v is None:
+        return t
+    if C.is_traced(v):
+        vf = v if v.shape == () else AD._reshape(v, (n,))
+    else:
+        a = np.asarray(v, np.float32)
+        a = np.broadcast_to(a.reshape(()) if a.size == 1 else a.reshape(-1), (n,))
+    for e in range(n):
+        if C.is_traced(v):
+            vv = (vf if vf.shape == () else vf[e]).var
+        elif a[e] == 0.0:
+            continue
+        else:
+            vv = C.literal(np.float32(a[e]), C.F32, False)
+        t = C.bind("tallymap_emit", [t.var, C.literal(e, C.I32, False), vv], [t.aval])[0]
+    return t
+
+
 def forward_only_program(adj, pl):
     """the adjoint as an ordinary item program, when no loop carry needs a reverse sweep: PRE, the loop with the
     step VJPs of the body constants accumulated as extra carries, POST, POST's and PRE's VJPs, one exact emit per
@@ -263,12 +313,16 @@ def forward_only_program(adj, pl):
     ft, fy = pl.ft, pl.fy
     nbc = len(sp.bconst)
     S_of = {k: prog.tallies[k].S for k in ft}
+    sp_pre, sp_body, sp_post = sparse_tables(adj, sp)
     body_vjp, b_ctout, b_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + [False] * sp.ncar, _ct_reader(ft, S_of),
                                              {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
-                                             ct_given=[False] * sp.ncar)
+                                             ct_given=[False] * sp.ncar, sparse=sp_body, prune=True)
     post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, pl.P_act + [False] * sp.ncar, _ct_reader(ft, S_of),
-                                             {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None})
-    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)})
+                                             {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None},
+                                             sparse=sp_post, prune=True)
+    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)},
+                                            sparse=sp_pre, prune=True)
+    ct_emit = ct_emitter(adj, nT)
     tspecs = [dataclasses.replace(s, kind="discard") for s in prog.tallies]
     tspecs += [TSpec(f"ct{j}", tuple(bav[j].shape) or (1,), np.dtype(np.float32), exact=True) for j in adj.wrt_bc]
     b = C.Builder()
@@ -296,7 +350,7 @@ def forward_only_program(adj, pl):
 
         def body_f(c):
             cars, g = list(c[0]), list(c[1])
-            vj = AD.eval_jaxpr(body_vjp, bcv + cars, ct_read)
+            vj = AD.eval_jaxpr(body_vjp, bcv + cars, ct_read, ct_emit)
             g = [gi + vj[k] for k, gi in enumerate(g)]
             return (AD.eval_jaxpr(sp.body, bcv + cars), g)
         never = (not sp.cond.eqns and isinstance(sp.cond.outvars[0], C.Lit)
@@ -309,7 +363,7 @@ def forward_only_program(adj, pl):
             if m:
                 q = j - nT
                 post_cts.append(cyin[fy.index(q)] if q >= 0 and q in fy else np.float32(0.0))
-        pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read)
+        pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read, ct_emit)
         gP = {}
         k = 0
         for q, m in enumerate(p_ctin):
@@ -326,7 +380,7 @@ def forward_only_program(adj, pl):
             if m:
                 z = np.zeros(o.aval.shape, np.float32)[()]
                 pre_cts.append(gP.get(j - sp.ncar, z) if j >= sp.ncar else z)
-        gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read)
+        gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read, ct_emit)
         g_pi, g_bc = {}, {}
         k = 0
         for q, m in enumerate(r_ctin):
@@ -339,19 +393,7 @@ def forward_only_program(adj, pl):
         touts = [C.Tracer(b.local(t.var)) if C.is_traced(t) else t for t in post_outs[:nT]]
         ct_t = []
         for jj, j in enumerate(adj.wrt_bc):
-            t = tin[nT + jj]
-            v = g_bc.get(j)
-            n = max(1, bav[j].size)
-            for e in range(n):
-                if v is None:
-                    continue
-                ve = v if (not C.is_traced(v) or v.shape == ()) else v[e]
-                if C.is_traced(ve):
-                    vv = ve.var
-                else:
-                    vv = C.literal(np.float32(ve), C.F32, False)
-                t = C.bind("tallymap_emit", [t.var, C.literal(e, C.I32, False), vv], [t.aval])[0]
-            ct_t.append(t)
+            ct_t.append(emit_dense_ct(tin[nT + jj], g_bc.get(j), max(1, bav[j].size)))
         ys = []
         for i in adj.wrt_pi:
             v = g_pi.get(i)

@@ -35,7 +35,7 @@ from .. import _ad as AD
 from .. import _core as C
 from .. import lax as L
 from .._api import ItemProgram, TSpec, check_tallies
-from .reverse import ReverseError, _ct_reader
+from .reverse import ReverseError, _ct_reader, ct_emitter, emit_dense_ct, sparse_tables
 
 BUDGET = 16 << 30           # bytes of tape per gradient call
 CAP_MAX = 1024
@@ -140,7 +140,8 @@ def programs(adj, pl):
     car_av = [v.aval for v in sp.body.outvars]
     Wp = state_words(sp)
     post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, pl.P_act + list(pl.car_act), _ct_reader(ft, S_of),
-                                             {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None})
+                                             {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None},
+                                             prune=True)
     lam_j = [j for j in range(sp.ncar) if pl.car_act[j]]
     gp_q = [q for q in range(sp.nP) if p_ctin[q]]
     P_av = [v.aval for v in sp.pre.outvars[sp.ncar:]]
@@ -213,13 +214,18 @@ def programs(adj, pl):
     count.tape_words = Wp
 
     # ----------------------------------------------------------------------------------------- reverse
+    # (the broadcast tables read at a traced index in the loop body or PRE: their read cotangents are emitted where
+    # the read's VJP runs; POST's VJP runs in the count program, which has no cotangent tallies: dense there)
+    sp_pre, sp_body, _ = sparse_tables(adj, sp)
     body_vjp, f_ctout, f_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + list(pl.car_act), _ct_reader(ft, S_of),
                                              {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
-                                             ct_given=list(pl.car_act))
+                                             ct_given=list(pl.car_act), sparse=sp_body, prune=True)
     for ci, ca in zip(f_ctin[nbc:], pl.car_act):
         if ci and not ca:
             raise ReverseError("internal: carry activity mismatch")
-    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)})
+    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)},
+                                            sparse=sp_pre, prune=True)
+    ct_emit = ct_emitter(adj, len(disc))
     gq = [q for q in range(nbc) if f_ctin[q]]
     tspecs = disc + [TSpec(f"ct{j}", tuple(bav[j].shape) or (1,), np.dtype(np.float32), exact=True)
                      for j in adj.wrt_bc]
@@ -272,7 +278,7 @@ def programs(adj, pl):
             for jc, m in enumerate(f_ctout):
                 if m:
                     cts.append(next(it) if pl.car_act[jc] else np.zeros(car_av[jc].shape, np.float32)[()])
-            vj = AD.eval_jaxpr(body_vjp, bcv + assemble(st, tc) + cts, ct_read)
+            vj = AD.eval_jaxpr(body_vjp, bcv + assemble(st, tc) + cts, ct_read, ct_emit)
             k2, newlam, newgk = 0, {}, []
             for q, m in enumerate(f_ctin):
                 if not m:
@@ -303,7 +309,7 @@ def programs(adj, pl):
             if m:
                 z = np.zeros(o.aval.shape, np.float32)[()]
                 pre_cts.append(lam_of.get(j, z) if j < sp.ncar else gP.get(j - sp.ncar, z))
-        gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read)
+        gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read, ct_emit)
         g_pi, g_bc, k = {}, {}, 0
         for q, m in enumerate(r_ctin):
             if m:
@@ -314,15 +320,7 @@ def programs(adj, pl):
                 k += 1
         ct_t = []
         for jj_, j in enumerate(adj.wrt_bc):
-            t = tin[nT + jj_]
-            v = g_bc.get(j)
-            for e in range(max(1, bav[j].size)):
-                if v is None:
-                    continue
-                ve = v if (not C.is_traced(v) or v.shape == ()) else v[e]
-                vv = ve.var if C.is_traced(ve) else C.literal(np.float32(ve), F32, False)
-                t = C.bind("tallymap_emit", [t.var, C.literal(e, I32, False), vv], [t.aval])[0]
-            ct_t.append(t)
+            ct_t.append(emit_dense_ct(tin[nT + jj_], g_bc.get(j), max(1, bav[j].size)))
         ys = []
         for i in adj.wrt_pi:
             v = g_pi.get(i)

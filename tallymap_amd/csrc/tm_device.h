@@ -255,6 +255,24 @@ TM_DFN i64 tm_rclaim(u64* ctr, volatile u64* base_s, volatile u32* left_s, volat
   return (when && s < rawcap) ? (i64)s : -1;
 }
 
+// A Records append inside a branch of a divergent if / else: the lanes that append take consecutive raw slots with
+// one counter atomic per wave at this point; the wave's record count grows by an LDS atomic of its first lane.
+// tm_rclaim's batch passes its state from one append to the next through plain LDS loads and first-lane stores,
+// which is sound only where all the wave's lanes run the same code: lanes of one wave in two branches run one
+// branch after the other, and the compiler, which reasons per lane (where the branches never meet), may merge the
+// branches' identical trailing stores into one store after both, so the second branch would read the state from
+// before the first.  An atomic add is unaffected (merged, it still adds each branch's count).
+TM_DFN i64 tm_rclaim_direct(u64* ctr, u64* cnt_s, bool when, u64 rawcap) {
+  const u64 m = tm_ballot(when);
+  if (m == 0ull) return -1;
+  const u32 n = (u32)__builtin_popcountll(m);
+  const u64 b = tm_claim(ctr, n);
+  if (tm_lane() == (int)__builtin_ctzll(tm_ballot(true)))
+    __hip_atomic_fetch_add(cnt_s, (u64)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  const u64 s = b + tm_rank(m);
+  return (when && s < rawcap) ? (i64)s : -1;
+}
+
 // f32 atomic adds that keep subnormals (2^-102 = 0x0c800000)
 TM_DFN void tm_cas_addf(float* a, float v) {
   u32* const u = (u32*)a;

@@ -171,10 +171,31 @@ class _Conv:
             p = dict(cond_jaxpr=self.sub(e.params["cond_jaxpr"]), body_jaxpr=self.sub(e.params["body_jaxpr"]),
                      cond_nconsts=int(e.params["cond_nconsts"]), body_nconsts=int(e.params["body_nconsts"]))
             return C.bind("while", [_var(x) for x in ins], outav, **p)
+        if prim == "scan":
+            return self._scan(e, ins, outav)
         if prim == "cond":
             p = dict(branches=tuple(self.sub(b) for b in e.params["branches"]), nconsts=0)
             return C.bind("cond", [_var(x) for x in ins], outav, **p)
         return C.bind(prim, [_var(x) for x in ins], outav, **_params(prim, e.params))
+
+    def _scan(self, e, ins, outav):
+        """JAX's scan (operands: consts, carries, xs; results: carries, stacked ys) through tallymap_amd.lax.scan:
+        unrolled up to its SCAN_UNROLL steps, a static loop beyond (no xs, no ys)."""
+        from . import lax as L
+        jx, consts = _closed(e.params["jaxpr"])
+        nco, nca = int(e.params["num_consts"]), int(e.params["num_carry"])
+        n = int(e.params["length"])
+        cs, xs = ins[:nco], ins[nco + nca:]
+        init = [x if C.is_traced(x) else C.bind("copy", [_var(x)], [_var(x).aval])[0] for x in ins[nco:nco + nca]]
+
+        def f(c, x):
+            outs = self.run(jx, consts, list(cs) + list(c) + (list(x) if x is not None else []))
+            return list(outs[:nca]), list(outs[nca:])
+        carry, ys = L.scan(f, init, xs=list(xs) if xs else None, length=n, reverse=bool(e.params.get("reverse")))
+        ys = list(ys) if ys is not None else []
+        if n == 0:
+            ys = [np.zeros(a.shape, a.dtype) for a in outav[nca:]]
+        return list(carry) + ys
 
     def _keys_map(self, keys, f, extra=(), dtype=None):
         """f applied to each key of a (batch of) key(s), stacked."""

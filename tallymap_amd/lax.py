@@ -65,11 +65,13 @@ def _unify(avals_init, outs):
     return res
 
 
-def while_loop(cond_fun, body_fun, init_val):
-    """lax.while_loop: carries a pytree; captured outer values become the loop's constants."""
+def while_loop(cond_fun, body_fun, init_val, *, _static=False):
+    """lax.while_loop: carries a pytree; captured outer values become the loop's constants.  _static marks the
+    loop that a static-bound fori_loop or a long scan becomes (JAX lowers those to scan, not while): max_steps
+    does not cap it and it never becomes the item's step loop (its equation carries static=True)."""
     leaves, td = flatten(init_val)
     cur = C.current()
-    cap = _CAP[-1] if _CAP and _CAP[-1].builder is cur else None
+    cap = _CAP[-1] if _CAP and _CAP[-1].builder is cur and not _static else None
     avals = [_leaf_var(x)[1] for x in leaves]
     # trace the body once to learn the carry types (a weak init widened by a strong update), then for real
     for attempt in range(2):
@@ -92,8 +94,10 @@ def while_loop(cond_fun, body_fun, init_val):
         init_vars.append(v)
     if cap is not None:
         return _capped(cap, cjx, bjx, cb, bb, init_vars, avals, td)
+    extra = {"static": True} if _static else {}
     outs = C.bind("while", list(cb.captured) + list(bb.captured) + init_vars, avals,
-                  cond_jaxpr=cjx, body_jaxpr=bjx, cond_nconsts=len(cb.captured), body_nconsts=len(bb.captured))
+                  cond_jaxpr=cjx, body_jaxpr=bjx, cond_nconsts=len(cb.captured), body_nconsts=len(bb.captured),
+                  **extra)
     return unflatten(td, outs)
 
 
@@ -190,13 +194,20 @@ def inline_eqns(jx, ins, outs):
 
 
 def fori_loop(lower, upper, body_fun, init_val):
-    """lax.fori_loop as a while loop over (i, carry)."""
+    """lax.fori_loop as a while loop over (i, carry).  With both bounds static (not traced) JAX lowers it to a scan
+    of upper - lower steps: the loop is marked static (not capped by max_steps, not the step loop)."""
     def cond(c):
         return c[0] < upper
 
     def body(c):
         return (c[0] + 1, body_fun(c[0], c[1]))
-    return while_loop(cond, body, (lower, init_val))[1]
+    static = not C.is_traced(lower) and not C.is_traced(upper)
+    return while_loop(cond, body, (lower, init_val), _static=static)[1]
+
+
+def is_static_loop(e):
+    """True for the while equation of a static-bound fori_loop or a long scan."""
+    return e.prim == "while" and bool(e.params.get("static", False))
 
 
 def cond(pred, true_fun, false_fun, *operands):
@@ -262,6 +273,20 @@ def scan(f, init, xs=None, length=None, reverse=False, unroll=1):
     if n is None:
         raise C.TraceError("lax.scan: give xs or length")
     n = int(n)
+    if n == 0:
+        # JAX returns the ys stacked along a leading axis of length 0: trace f once, discarded, for their structure
+        il, itd = flatten(init)
+        iav = [_leaf_var(x)[1] for x in il]
+        xav = [C.AVal(tuple(C._aval(v).shape[1:]), C._aval(v).dtype, C._aval(v).weak) for v in xl]
+
+        def probe(*ls):
+            c = unflatten(itd, list(ls[:len(il)]))
+            return f(c, unflatten(xtd, list(ls[len(il):])) if xl else None)[1]
+        _, _, y = C.trace_fn(probe, iav + xav, parent=C.current())
+        yl, ytd = flatten(y)
+        if not yl:
+            return init, y
+        return init, unflatten(ytd, [np.zeros((0,) + tuple(C._aval(v).shape), C._aval(v).dtype) for v in yl])
     if n > SCAN_UNROLL:
         if xl:
             raise C.TraceError(f"lax.scan: {n} steps over xs (unrolled up to {SCAN_UNROLL} steps)")

@@ -285,6 +285,58 @@ def test_scan_and_switch_trace():
               [((), np.float32)], [], (0,))
 
 
+def test_static_loops_are_neither_capped_nor_the_step_loop():
+    """A long scan and a static-bound fori_loop are scans in JAX: max_steps does not cap them (no truncation flag,
+    no k < max_steps in their cond) and they never become the step loop; a while_loop beside them is both."""
+    from tallymap_amd.backend import kernel as K
+
+    def item(t, x):
+        c, _ = lax.scan(lambda c, _: (c + x, None), x, length=1000)
+        k = lax.fori_loop(0, 300, lambda i, a: a + 1, 0)
+        return t.add("h", 0, c), (c, k)
+    p = _prog(item, {"h": tm.Sum((1,))}, [((), np.float32)], [], (0,), max_steps=100)
+    ws = [e for e in p.jaxpr.eqns if e.prim == "while"]
+    assert len(ws) == 2 and all(lax.is_static_loop(e) for e in ws)
+    assert all(e.prim != "lt" or all(not (isinstance(v, C.Lit) and v.val == 100) for v in e.invars)
+               for w in ws for e in w.params["cond_jaxpr"].eqns)
+    tr = p.jaxpr.outvars[len(p.tallies) + p.trunc]
+    producer = [e for e in p.jaxpr.eqns if tr in e.outvars][0]
+    assert producer.prim == "copy" and isinstance(producer.invars[0], C.Lit) and not producer.invars[0].val
+    assert K._split(p.jaxpr) is None                       # (the item schedule: no step loop)
+
+    def item2(t, x):
+        c, _ = lax.scan(lambda c, _: (c + x, None), x, length=1000)
+        n = lax.while_loop(lambda a: a < c, lambda a: a + 1.0, 0.0)
+        return t.add("h", 0, n), n
+    p2 = _prog(item2, {"h": tm.Sum((1,))}, [((), np.float32)], [], (0,), max_steps=100)
+    w = K._split(p2.jaxpr)
+    assert w is not None and not lax.is_static_loop(p2.jaxpr.eqns[w])
+    lits = [v.val for e in p2.jaxpr.eqns[w].params["cond_jaxpr"].eqns if e.prim == "lt" for v in e.invars
+            if isinstance(v, C.Lit)]
+    assert 100 in lits                                     # (the while_loop is capped)
+
+    def item3(t, x):                                       # a traced bound: a while loop, capped
+        return t, lax.fori_loop(0, (x * 10.0).astype(jnp.int32), lambda i, a: a + 1, 0)
+    p3 = _prog(item3, {"h": tm.Sum((1,))}, [((), np.float32)], [], (0,), max_steps=100)
+    assert [lax.is_static_loop(e) for e in p3.jaxpr.eqns if e.prim == "while"] == [False]
+
+
+def test_scan_of_length_zero_returns_empty_stacked_ys():
+    """lax.scan over 0 steps returns the carry unchanged and ys stacked along a leading axis of length 0."""
+    got = {}
+
+    def item(t, x):
+        c, ys = lax.scan(lambda c, v: (c + v[0], (c * 2.0 + v, (c + v > 0.0).astype(jnp.int32))), x,
+                         np.zeros((0, 3), np.float32))
+        got["c"], got["ys"] = c, ys
+        return t.add("h", 0, c)
+    _prog(item, {"h": tm.Sum((1,))}, [((), np.float32)], [], (0,))
+    a, b = got["ys"]
+    assert np.shape(a) == (0, 3) and np.asarray(a).dtype == np.float32
+    assert np.shape(b) == (0, 3) and np.asarray(b).dtype == np.int32
+    assert C.is_traced(got["c"])
+
+
 def test_dynamic_index_traces():
     """x[i] with a traced integer index: one dynamic_index equation after the normalisation and clamp; a float
     index raises."""
@@ -315,3 +367,35 @@ def test_floor_divide_and_remainder_follow_jnp():
     assert len(rnd) == 1 and rnd[0].params["rounding_method"] == 0 and ps.count("rem") == 1
     ps, _ = prims(lambda a, b: a % b, np.float32)
     assert ps.count("rem") == 1 and "eq" not in ps           # (no zero-divisor guard for floats)
+
+
+def test_table_read_cotangents_are_emitted_at_the_row_read():
+    """the adjoint programs of an item reading a 1024-row broadcast table at traced indices: the read's cotangent
+    leaves by ONE slot-addressed emit where the step's VJP runs (not a select per row and an emit per row at the
+    item's end), through the tape adjoint (an active carry) and the forward-only one."""
+    from tallymap_amd.backend import reverse as R
+    from tallymap_amd.backend import tape as T
+
+    def walk(t, i, x, tab):
+        def body(c):
+            k, s, t_ = c
+            s = s * 0.5 + tab[(i * 7919 + k * 104729) % 1024] * x
+            return k + 1, s, t_.add("h", 0, s)
+        return lax.while_loop(lambda c: c[0] < 20, body, (0, np.float32(0.0), t))[2]
+
+    def reads(t, i, x, tab):
+        def body(c):
+            k, t_ = c
+            return k + 1, t_.add("h", 0, tab[(i * 7919 + k * 104729) % 1024] * x)
+        return lax.while_loop(lambda c: c[0] < 20, body, (0, t))[1]
+    pav, bav = [((), np.int32), ((), np.float32)], [((1024,), np.float32)]
+    for item, tape in ((walk, True), (reads, False)):
+        prog = _prog(item, {"h": tm.Sum((1,))}, pav, bav, (0, 0, None))
+        adj = R.adjoint_program(prog, ((), (0,)))
+        pl = R.plan(adj)
+        assert any(pl.car_act) == tape
+        progs = [T.programs(adj, pl).reverse] if tape else [R.forward_only_program(adj, pl)]
+        for q in progs:
+            prims = [e.prim for e in C.walk_eqns(q.jaxpr)]
+            assert prims.count("tallymap_emit_slot") == 1
+            assert prims.count("select_n") < 40 and prims.count("tallymap_emit") <= 2

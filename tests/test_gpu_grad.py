@@ -119,3 +119,66 @@ def test_no_stale_runtime_error_after_launches():
     x = torch.full((8,), 2.0, device="cuda") * 3.0
     torch.cuda.synchronize()
     assert float(x.sum().item()) == 48.0
+
+
+ROWS = 1024
+
+
+def _rows(i, k):
+    return (i * 7919 + k * 104729) % ROWS
+
+
+def _table_items():
+    from tallymap_amd import lax
+
+    def walk(t, i, x, tab):            # an active carry: the tape adjoint
+        def body(c):
+            k, s, t_ = c
+            s = s * 0.5 + tab[_rows(i, k)] * x
+            return k + 1, s, t_.add("h", 0, s)
+        return lax.while_loop(lambda c: c[0] < 20, body, (0, np.float32(0.0), t))[2]
+
+    def reads(t, i, x, tab):           # no active carry: the forward-only adjoint
+        def body(c):
+            k, t_ = c
+            return k + 1, t_.add("h", 0, tab[_rows(i, k)] * x)
+        return lax.while_loop(lambda c: c[0] < 20, body, (0, t))[1]
+    return walk, reads
+
+
+def _table_grad_want(i, x, geometric):
+    """d(sum h)/d tab in float64: each read at step k adds x times its weight, sum_{m >= k} 0.5^(m - k) over the
+    20 steps for the walk (the read reaches s_k .. s_19), 1 for the plain reads.  Every term is a dyadic rational
+    of at most 21 significant bits, so the float32 gradient (an exact sum rounded once) is this value rounded."""
+    w = np.array([sum(0.5 ** (m - k) for m in range(k, 20)) if geometric else 1.0 for k in range(20)])
+    g = np.zeros(ROWS)
+    for k in range(20):
+        np.add.at(g, _rows(i.astype(np.int64), k), x.astype(np.float64) * w[k])
+    return g.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["walk", "reads"])
+def test_grad_wrt_a_1024_row_table(kind):
+    """the cotangent of a broadcast table read at traced indices is emitted at the row read (one emit per read,
+    not a select and an emit per table row): d(sum h)/d tab for a 1024-row table equals the closed form bitwise,
+    through the tape adjoint (an active carry) and the forward-only adjoint; n_active=n equals the call over the
+    first n items."""
+    print(f"case: grad wrt a {ROWS}-row table ({kind}), N=8192", flush=True)
+    walk, reads = _table_items()
+    item = walk if kind == "walk" else reads
+    rng = np.random.default_rng(11)
+    n = 8192
+    i = rng.integers(0, 1 << 17, n).astype(np.int32)        # (i * 7919 + 19 * 104729 < 2^31: no wrap)
+    x = rng.choice(np.array([0.5, 1.0, 2.0, -1.0], np.float32), n)
+    tab = rng.standard_normal(ROWS).astype(np.float32)
+    f = tm.vmap(item, outputs={"h": tm.Sum((1,))}, in_axes=(0, 0, None))
+    g = tm.grad(f, argnums=2)(i, x, tab)
+    _sync()
+    want = _table_grad_want(i, x, kind == "walk")
+    assert np.array_equal(_np(g).view(np.uint32), want.view(np.uint32))
+    m = 3000
+    ga = tm.grad(f, argnums=2)(i, x, tab, n_active=m)
+    gm = tm.grad(f, argnums=2)(i[:m], x[:m], tab)
+    _sync()
+    assert np.array_equal(_np(ga).view(np.uint32), _np(gm).view(np.uint32))
+    assert np.array_equal(_np(ga).view(np.uint32), _table_grad_want(i[:m], x[:m], kind == "walk").view(np.uint32))

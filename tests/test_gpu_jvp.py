@@ -192,3 +192,29 @@ def test_jvp_through_cond_inside_loop():
     assert np.array_equal(_np(tan.per_item).view(np.uint32), dc.view(np.uint32))
     from oracle import exact as X
     assert _np(tan.outputs["h"])[0].view(np.uint32) == X.exact_sum(dc)[0].view(np.uint32)
+
+
+def test_jvp_and_jacfwd_under_n_active():
+    """n_active = n composes with forward and reverse mode as with the call: tangent and primal tallies equal those
+    of the call over the first n items (float32 sums in atomic order: 1e-5 relative), per-item cotangents and the
+    exact broadcast cotangent bitwise, and the inactive items' per-item cotangents are zero."""
+    print("case: jvp / jacfwd with n_active", flush=True)
+    xs, keys, theta = configs.c1_inputs(4096)
+    f = _mapped(configs.C1)
+    n = 1234
+    ra, ta = tm.jvp(f, (xs, keys, theta), (np.ones_like(xs), None, np.float32(1.0)), n_active=n)
+    rb, tb = tm.jvp(f, (xs[:n], keys[:n], theta), (np.ones_like(xs[:n]), None, np.float32(1.0)))
+    _sync()
+    assert np.allclose(_np(ta.outputs["hist"]), _np(tb.outputs["hist"]), rtol=1e-5, atol=0)
+    assert np.allclose(_np(ra.outputs["hist"]), _np(rb.outputs["hist"]), rtol=1e-5, atol=0)
+    ja = _np(tm.jacfwd(f, argnums=2)(xs, keys, theta, n_active=n)["hist"][2])
+    jb = _np(tm.jacfwd(f, argnums=2)(xs[:n], keys[:n], theta)["hist"][2])
+    _sync()
+    assert np.allclose(ja, jb, rtol=1e-5, atol=0)
+    res, pull = tm.vjp(f, xs, keys, theta, argnums=(0, 2), n_active=n)
+    gx, gt = pull({"hist": 1.0})
+    _, pull_b = tm.vjp(f, xs[:n], keys[:n], theta, argnums=(0, 2))
+    gxb, gtb = pull_b({"hist": 1.0})
+    _sync()
+    assert not _np(gx)[n:].any() and np.array_equal(_np(gx)[:n].view(np.uint32), _np(gxb).view(np.uint32))
+    assert np.array_equal(np.atleast_1d(_np(gt)).view(np.uint32), np.atleast_1d(_np(gtb)).view(np.uint32))

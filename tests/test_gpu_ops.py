@@ -248,3 +248,31 @@ def test_unsigned_integer_ops():
     want = [q, r, q, m, _shl(a, b, 32), _shrl(a, b, 32), np.maximum(a, b), a.astype(np.float32), a.astype(np.float64)]
     for n, g, w in zip(["div", "rem", "floordiv", "mod", "shl", "shrl", "max", "u2f32", "u2f64"], got, want):
         _same(n, g, w)
+
+
+def test_static_loops_run_past_max_steps():
+    """A 1000-step scan and a 300-step static fori_loop under max_steps=100 run to the end (JAX lowers both to
+    scan, which the cap does not touch): no item truncated, the float tally finite and exact, beside a while_loop
+    that the cap does stop."""
+    import torch
+    print("case: static loops past max_steps, N=4096", flush=True)
+
+    def item(t, x):
+        c, _ = lax.scan(lambda c, _: (c + x, None), np.float32(0.0), length=1000)
+        k = lax.fori_loop(0, 300, lambda i, a: a + 1, 0)
+        return t.add("h", 0, c), (c, k)
+    x = np.full(4096, 0.5, np.float32)
+    r = tm.vmap(item, outputs={"h": tm.Sum((1,))}, max_steps=100)(x)
+    torch.cuda.synchronize()
+    c, k = (v.cpu().numpy() for v in r.per_item)
+    assert not r.truncated.cpu().numpy().any()
+    assert (c == 500.0).all() and (k == 300).all()
+    assert r.outputs["h"].cpu().numpy()[0] == 4096 * 500.0
+
+    def item2(t, x):
+        n = lax.while_loop(lambda a: a < 1000.0, lambda a: a + x, np.float32(0.0))
+        return t.add("h", 0, n), n
+    r2 = tm.vmap(item2, outputs={"h": tm.Sum((1,))}, max_steps=100)(x)
+    torch.cuda.synchronize()
+    assert r2.truncated.cpu().numpy().all() and (r2.per_item.cpu().numpy() == 50.0).all()
+    assert np.isnan(r2.outputs["h"].cpu().numpy()[0])

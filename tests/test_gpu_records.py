@@ -246,6 +246,67 @@ def test_n_active_runs_only_the_first_items(n):
     assert np.array_equal(_np(a.outputs["steps"]["w"]).view(np.uint32), _np(b.outputs["steps"]["w"]).view(np.uint32))
 
 
+def test_records_appended_from_both_branches_of_a_cond():
+    """appends from both branches of a cond inside a loop (lanes of one wave in different branches, which run one
+    after the other): every record lands once in its item's canonical place, against the numpy enumeration."""
+    print("case: records from both cond branches", flush=True)
+    n = 6000
+    rng = np.random.default_rng(3)
+    u = rng.integers(0, 1 << 20, n).astype(np.uint32)
+    x = (rng.integers(0, 1 << 12, n) / 64.0).astype(f32)
+
+    def item(t, u, x):
+        def body(i, t):
+            def even(t):
+                return t.append("r", {"a": u * 2 + i, "w": x * 2.0})
+
+            def odd(t):
+                return t.append("r", {"a": u + i, "w": x * 0.5}, when=(u & 4) == 0)
+            return lax.cond((u + i) % 2 == 0, even, odd, t)
+        return lax.fori_loop(0, 3, body, t)
+    f = tm.vmap(item, outputs={"r": tm.Records({"a": np.uint32, "w": np.float32}, capacity=1 << 16)},
+                in_axes=(0, 0))
+    res = f(u, x)
+    _sync()
+    want_a, want_w = [], []
+    for ui, xi in zip(u.tolist(), x.tolist()):
+        for i in range(3):
+            if (ui + i) % 2 == 0:
+                want_a.append((ui * 2 + i) & 0xFFFFFFFF)
+                want_w.append(f32(xi) * f32(2.0))
+            elif (ui & 4) == 0:
+                want_a.append((ui + i) & 0xFFFFFFFF)
+                want_w.append(f32(xi) * f32(0.5))
+    m = len(want_a)
+    assert int(_np(res.stats["appended"]["r"])) == m
+    assert np.array_equal(_np(res.outputs["r"]["a"])[:m], np.array(want_a, np.uint32))
+    assert np.array_equal(_np(res.outputs["r"]["w"])[:m].view(np.uint32), np.array(want_w, f32).view(np.uint32))
+
+
+def test_records_without_capacity_under_n_active():
+    """a capacity-less Records output under n_active = n is sized by a count pass over the first n items only (the
+    reference appends n_active before its count, _api.py:838-852): the output shape and records equal the call over
+    the first n items, and the inactive items' records (here ~6x more) neither size it nor raise; reverse mode
+    through the same call agrees with the first-n call."""
+    print("case: records without capacity, n_active", flush=True)
+    xs, keys, theta = configs.c1_inputs(1 << 14)
+    outs = {"steps": tm.Records({"bin": np.int32, "w": np.float32}),
+            "ends": tm.Records({"k": np.int32, "x": np.float32}), "hist": tm.Sum((2,))}
+    f = tm.vmap(_walker, outputs=outs, in_axes=(0, 0, None), max_steps=100)
+    n = 2300
+    a = f(xs, keys, theta, n_active=n)
+    b = f(xs[:n], keys[:n], theta)
+    _sync()
+    for r, fld in (("steps", "w"), ("ends", "x")):
+        wa, wb = _np(a.outputs[r][fld]), _np(b.outputs[r][fld])
+        assert wa.shape == wb.shape, (r, wa.shape, wb.shape)
+        assert np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
+    ga = _np(tm.grad(f, weights={"steps": {"w": 1.0}}, argnums=2)(xs, keys, theta, n_active=n))
+    gb = _np(tm.grad(f, weights={"steps": {"w": 1.0}}, argnums=2)(xs[:n], keys[:n], theta))
+    _sync()
+    assert np.array_equal(np.atleast_1d(ga).view(np.uint32), np.atleast_1d(gb).view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [0, 1, 257])
 def test_small_and_empty_calls(n):
     """N = 0, 1 and one not a multiple of the block (reference edge.py:296-307): Sums, Records and per-item results

@@ -534,9 +534,11 @@ def test_spawn_records_shower_node_order():
     assert np.array_equal(_np(res.outputs["end"]["E"])[:m].view(np.uint32), e_w.view(np.uint32))
 
 
-def _mixed(t, p):
+def _mixed(t, p, traced_bound=False):
     """children of every operand kind the staging rows convert (f64 and i64 as two words, bool as one, a u32 and
-    an f32 array), spawned from inside the branches of a cond inside a loop (divergent lanes at the ballot)."""
+    an f32 array), spawned from inside both branches of a cond inside a loop (divergent lanes at the ballot; the
+    branches run one after the other).  The loop's bound is static (a scan: the item schedule) or traced (a while
+    loop: the step schedule)."""
     g = p["g"]
 
     def body(i, t):
@@ -548,7 +550,7 @@ def _mixed(t, p):
             return t.spawn(dict(g=g + 1, x=p["x"] * 0.25, m=p["m"] - i, b=p["b"], u=p["u"] * 2, v=p["v"] * 0.5),
                            when=g < 2)
         return lax.cond((p["u"][0] + i) % 2 == 0, even, odd, t)
-    t = lax.fori_loop(0, 2, body, t)
+    t = lax.fori_loop(0, g * 0 + 2 if traced_bound else 2, body, t)
     t = t.add("x", g, p["x"])
     t = t.add("m", g, p["m"])
     t = t.add("b", g, p["b"].astype(jnp.int32))
@@ -556,10 +558,11 @@ def _mixed(t, p):
     return t.add("v", g, p["v"][0] + p["v"][1] + p["v"][2])
 
 
-def test_spawn_operand_kinds_and_divergent_spawns():
+@pytest.mark.parametrize("traced_bound", [False, True], ids=["item", "step"])
+def test_spawn_operand_kinds_and_divergent_spawns(traced_bound):
     """per-generation sums of every operand against the numpy enumeration of the tree, exactly (dyadic f64 and f32
     values, integers)."""
-    print("case: spawn operand kinds", flush=True)
+    print(f"case: spawn operand kinds traced_bound={traced_bound}", flush=True)
     n = 5000
     rng = np.random.default_rng(8)
     p = dict(g=np.zeros(n, np.int32), x=rng.integers(0, 1 << 20, n).astype(np.float64) / 1024.0,
@@ -567,7 +570,7 @@ def test_spawn_operand_kinds_and_divergent_spawns():
              u=rng.integers(0, 1 << 20, (n, 2)).astype(np.uint32), v=(rng.integers(0, 1 << 10, (n, 3)) / 64.0).astype(f32))
     outs = {"x": tm.Sum((4,), np.float64), "m": tm.Sum((4,), np.int64), "b": tm.Sum((4,), np.int32),
             "u": tm.Sum((4,), np.uint32), "v": tm.Sum((4,), fixed_point=True)}
-    res = tm.vmap(_mixed, outputs=outs, spawn=tm.Queue(1 << 16))(p)
+    res = tm.vmap(lambda t, p: _mixed(t, p, traced_bound), outputs=outs, spawn=tm.Queue(1 << 16))(p)
     _sync()
     want = {k: np.zeros(4, np.float64 if k in ("x", "v") else np.int64) for k in outs}
     cur, spawned = p, 0

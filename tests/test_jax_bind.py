@@ -191,6 +191,33 @@ def test_converter_expands_key_primitives_and_refuses_what_it_cannot_run():
         JB.run(_ref_c1(), [np.zeros(4, F32), np.zeros((4, 2), U32)], [np.float32(2.0)], ndev=2)
 
 
+def test_scan_converts_unrolled_or_as_a_static_loop():
+    """JAX's scan (consts, carries, xs -> carries, stacked ys): up to the unroll limit its steps are inlined and the
+    ys stacked (no loop); a 1000-step scan without xs or ys becomes one static while loop, which max_steps does not
+    cap, as JAX's scan is not a while loop."""
+    from tallymap_amd import lax as L
+    x, xs = Var((), F32), Var((3,), F32)
+    cx, c, v = Var((), F32), Var((), F32), Var((), F32)
+    m, c2, y = Var((), F32), Var((), F32), Var((), F32)
+    body = ClosedJaxpr(Jaxpr([cx, c, v], [c2, y], [Eqn("mul", [v, cx], [m]), Eqn("add", [c, m], [c2]),
+                                                   Eqn("mul", [c, Literal(2.0, F32, True)], [y])]))
+    cf, ys = Var((), F32), Var((3,), F32)
+    scan = Eqn("scan", [x, x, xs], [cf, ys], jaxpr=body, num_consts=1, num_carry=1, length=3, reverse=False,
+               linear=(False,) * 3, unroll=1, _split_transpose=False)
+    jx = JB.convert(ClosedJaxpr(Jaxpr([x, xs], [cf, ys], [scan])))
+    prims = [e.prim for e in C.walk_eqns(jx)]
+    assert "while" not in prims and prims.count("add") == 3 and prims.count("mul") == 6
+    assert jx.outvars[1].aval.shape == (3,)
+    k, k2, one = Var((), I32), Var((), I32), Literal(1, I32, True)
+    lbody = ClosedJaxpr(Jaxpr([k], [k2], [Eqn("add", [k, one], [k2])]))
+    kf = Var((), I32)
+    long = Eqn("scan", [Literal(0, I32)], [kf], jaxpr=lbody, num_consts=0, num_carry=1, length=1000,
+               reverse=False, linear=(False,), unroll=1, _split_transpose=False)
+    jx2 = JB.convert(ClosedJaxpr(Jaxpr([x], [kf], [long])))
+    ws = [e for e in jx2.eqns if e.prim == "while"]
+    assert len(ws) == 1 and L.is_static_loop(ws[0])
+
+
 @pytest.mark.gpu
 def test_run_contract_on_the_gpu_matches_vmap():
     """run(p, pi, bc, target='rocm', cuda_math=..., min_blocks_per_sm=...) -> [hist] + [stats int32[5]] + [k, trunc]
