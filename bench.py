@@ -31,14 +31,69 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FWD_BYTES_PER_ITEM = 17
 GRAD_BYTES_PER_ITEM = 13
-# HBM bytes per launch at N = 4,194,304 from rocprofv3 counter passes (profiles/c2_random_walk_traffic.md):
-# 2 x FETCH_SIZE + 1 x WRITE_SIZE (KiB), the factors those counters read on a plain 1 GiB device copy
-MEASURED_TRAFFIC = {"forward": 77_128_984, "gradient": 56_958_568}
-# wave64 VALU instructions per launch at N = 4,194,304 (rocprofv3 --pmc SQ_INSTS_VALU, profiles/
-# c2_random_walk_sq_counters.md) and MI355X's VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per 4
-# cycles on a 16-lane SIMD, at the 2.4 GHz peak engine clock
-MEASURED_VALU_INSTS = {"forward": 7.029e9, "gradient": 6.721e9}
+# Counter-derived figures per launch at N = 4,194,304, each keyed by the code object it was measured on (the first
+# 16 hex digits of its hipRTC cache key: sha256 of compiler, options and source).  traffic: HBM bytes, 2 x FETCH_SIZE
+# + 1 x WRITE_SIZE (KiB), the factors those counters read on a plain 1 GiB device copy (profiles/
+# c2_random_walk_traffic.md); valu_insts: wave64 VALU instructions (SQ_INSTS_VALU, profiles/
+# c2_random_walk_sq_counters.md).  A kernel whose key differs from the one measured reports null with the reason,
+# so a changed kernel never carries a stale counter.
+MEASURED = {"forward": {"code": None, "traffic": None, "valu_insts": None},
+            "gradient": {"code": None, "traffic": None, "valu_insts": None}}
+# MI355X's VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per 4 cycles on a 16-lane SIMD, at the
+# 2.4 GHz peak engine clock
 VALU_PEAK = 1024 * 2.4e9 / 4
+
+
+def code_keys(f, dev):
+    """{forward, gradient: the code-object key (16 hex digits) of the kernel that launch runs} for the mapped call
+    f and its gradient w.r.t. argument 2 (run once before, so the adjoint is compiled)."""
+    from tallymap_amd import backend as B
+    from tallymap_amd.backend import compile as Cm
+    prog = f._prepare(dev)[0]
+    keys = {"forward": Cm._key(B.compiled(prog, f._opts).src)[:16], "gradient": None}
+    for (dg, _), (adj, _) in list(B._ADJ.items()):
+        if dg != prog.digest():
+            continue
+        q = B._FWD_ONLY.get(adj.digest())
+        tp = B._TAPE.get(adj.digest())
+        q = q if q is not None else (tp.reverse if tp is not None else None)
+        if q is not None:
+            keys["gradient"] = Cm._key(B.compiled(q, f._opts).src)[:16]
+    return keys
+
+
+def measured(kind, field, key, n):
+    """(the recorded counter figure, None) when it was measured on this code object at this N, else (None, reason)."""
+    m = MEASURED[kind]
+    if n != 4_194_304:
+        return None, f"measured at N = 4,194,304 only (this run: N = {n})"
+    if m["code"] is None or m[field] is None:
+        return None, "not measured"
+    if m["code"] != key:
+        return None, f"stale: measured on code object {m['code']}, this run's {kind} kernel is {key}"
+    return m[field], None
+
+
+def host_info():
+    """the host's CPU model and C library (the oracle calls its libm: glibc's bits are the CPU target's)."""
+    import ctypes
+    import platform
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        libc = ctypes.CDLL("libc.so.6")
+        libc.gnu_get_libc_version.restype = ctypes.c_char_p
+        glibc = libc.gnu_get_libc_version().decode()
+    except (OSError, AttributeError):
+        glibc = "-".join(platform.libc_ver())
+    return model, glibc
 
 
 def cpu_baseline(x0, keys, drift, max_steps, target_s=10.0):
@@ -55,9 +110,13 @@ def cpu_baseline(x0, keys, drift, max_steps, target_s=10.0):
         if dt * 4 > target_s or n * 2 > x0.size:
             break
         n = min(x0.size, max(n * 2, int(n * target_s / max(dt, 1e-3) / 2)))
+    model, glibc = host_info()
     return dict(value=n / dt, unit="items/s", cores=threads, kind="port",
                 sample=f"first {n} of the N=4,194,304 C2 items, forward + gradient (drift), {dt:.2f} s wall "
-                       f"on {threads} OpenMP threads")
+                       f"on {threads} OpenMP threads",
+                cpu_model=model, glibc=glibc,
+                gradient="forward-mode dual numbers in double (the oracle's c2_grad), not the reference CPU "
+                         "backend's checkpointed replay")
 
 
 def _cfg_runs(name, n, dev_inputs):
@@ -390,6 +449,10 @@ def main():
     achieved = bpi * N / (dom_ms * 1e-3) / 1e9
     pi = B.compiled(f._prepare(dev)[0], f._opts)
     info = B.kernel_info(pi)
+    ckeys = code_keys(f, dev)
+    traffic, t_why = (a.traffic_bytes, None) if a.traffic_bytes is not None else \
+        measured(dom, "traffic", ckeys[dom], N)
+    vinsts, v_why = measured(dom, "valu_insts", ckeys[dom], N)
     out = {
         "metric": "items/s fwd+grad at N=4,194,304 (C2 random walk)",
         "value": N / (ms * 1e-3),
@@ -411,18 +474,19 @@ def main():
         "grad_ms": grad_ms,
         "mean_trip_count": float(r.per_item.double().mean().item()),
         "kernel": {"name": "tm_main (" + dom + ")", **info},
+        "code_objects": ckeys,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": a.traffic_bytes if a.traffic_bytes is not None
-                     else (MEASURED_TRAFFIC[dom] if N == 4_194_304 else None),
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": bpi * N},
         # the resource that binds: VALU issue (the HBM roofline above is the contract's; this kernel reads 17 B and
         # runs ~406 steps of ~230 VALU instructions per item)
-        "valu_roofline": ({"bound": "valu", "achieved": MEASURED_VALU_INSTS[dom] / (dom_ms * 1e-3),
+        "valu_roofline": ({"bound": "valu", "achieved": vinsts / (dom_ms * 1e-3),
                            "peak": VALU_PEAK, "unit": "wave64 VALU instructions/s",
-                           "frac": MEASURED_VALU_INSTS[dom] / (dom_ms * 1e-3) / VALU_PEAK,
-                           "insts_per_launch": MEASURED_VALU_INSTS[dom]} if N == 4_194_304 else None),
+                           "frac": vinsts / (dom_ms * 1e-3) / VALU_PEAK,
+                           "insts_per_launch": vinsts} if vinsts is not None else {"bound": "valu", "null": v_why}),
     }
+    if t_why:
+        out["roofline"]["traffic_null"] = t_why
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(x0, keys, drift, cfg["max_steps"])
     if not a.headline_only:
