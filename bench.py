@@ -1,12 +1,16 @@
 """Benchmark: items/s of the tallymap hot path (forward + replay gradient) on one MI355X.
 
 Workload: BASELINE config 2, the 1-D random walk (C2) at N = 4,194,304 items, inputs resident in HBM.  One step is
-one forward launch (occupancy and wall tallies, per-item trip counts) plus one replay-gradient launch (d sum(tallies)
-/ d drift, exact float32), both queued on torch's current stream; `value` = N / (time per step).
+the forward's outputs (occupancy and wall tallies, per-item trip counts, truncation flags) plus the gradient
+d sum(tallies) / d drift (exact float32), through tm.value_and_grad on torch's current stream: C2's adjoint needs no
+reverse sweep, and the forward-only adjoint replays the whole forward anyway, so one fused launch returns both;
+`value` = N / (time per step).  The same quantities from two launches (the forward call, then tm.grad) are timed
+beside it (fwd_ms, grad_ms, two_launch_items_per_s).
 
 roofline: the dominant kernel's algorithmic HBM bytes per launch (per item: x0 4 B + key 8 B read, trip count 4 B +
-truncation flag 1 B written = 17 B; the gradient launch: 12 B read + 1 B written = 13 B) over its average launch
-duration (HIP events on the launch stream), against MI355X's 8 TB/s.  The path is VALU-bound (threefry, erf_inv in
+truncation flag 1 B written = 17 B, for the fused launch as for the forward; the separate gradient launch: 12 B
+read + 1 B written = 13 B) over its average launch duration (HIP events on the launch stream), against MI355X's
+8 TB/s.  The path is VALU-bound (threefry, erf_inv in
 double), not HBM-bound: the fraction is reported as measured.  traffic: FETCH_SIZE + WRITE_SIZE per dispatch from
 rocprofv3 counter runs of this bench, scaled by what the same counters read on a plain copy of known size
 (--copy-probe); the recorded measurement at the default N unless --traffic-bytes gives another.
@@ -37,7 +41,8 @@ GRAD_BYTES_PER_ITEM = 13
 # c2_random_walk_traffic.md); valu_insts: wave64 VALU instructions (SQ_INSTS_VALU, profiles/
 # c2_random_walk_sq_counters.md).  A kernel whose key differs from the one measured reports null with the reason,
 # so a changed kernel never carries a stale counter.
-MEASURED = {"forward": {"code": None, "traffic": None, "valu_insts": None},
+MEASURED = {"fused": {"code": None, "traffic": None, "valu_insts": None},
+            "forward": {"code": None, "traffic": None, "valu_insts": None},
             "gradient": {"code": None, "traffic": None, "valu_insts": None}}
 # MI355X's VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per 4 cycles on a 16-lane SIMD, at the
 # 2.4 GHz peak engine clock
@@ -45,21 +50,32 @@ VALU_PEAK = 1024 * 2.4e9 / 4
 
 
 def code_keys(f, dev):
-    """{forward, gradient: the code-object key (16 hex digits) of the kernel that launch runs} for the mapped call
-    f and its gradient w.r.t. argument 2 (run once before, so the adjoint is compiled)."""
+    """{fused, forward, gradient: the code-object key (16 hex digits) of the kernel that launch runs} for the mapped
+    call f, its value_and_grad and its gradient w.r.t. argument 2 (each run once before, so all are compiled)."""
     from tallymap_amd import backend as B
     from tallymap_amd.backend import compile as Cm
     prog = f._prepare(dev)[0]
-    keys = {"forward": Cm._key(B.compiled(prog, f._opts).src)[:16], "gradient": None}
+    keys = {"fused": None, "forward": Cm._key(B.compiled(prog, f._opts).src)[:16], "gradient": None}
     for (dg, _), (adj, _) in list(B._ADJ.items()):
         if dg != prog.digest():
             continue
-        q = B._FWD_ONLY.get(adj.digest())
-        tp = B._TAPE.get(adj.digest())
-        q = q if q is not None else (tp.reverse if tp is not None else None)
-        if q is not None:
-            keys["gradient"] = Cm._key(B.compiled(q, f._opts).src)[:16]
+        for kind, suffix in (("gradient", ""), ("fused", "|vg")):
+            q = B._FWD_ONLY.get(adj.digest() + suffix)
+            tp = B._TAPE.get(adj.digest() + suffix)
+            q = q if q is not None else (tp.reverse if tp is not None else None)
+            if q is not None:
+                keys[kind] = Cm._key(B.compiled(q, f._opts).src)[:16]
     return keys
+
+
+def vg_kernel(f, dev):
+    """the compiled kernel of f's value_and_grad w.r.t. argument 2 (the forward-only adjoint keeping the forward)."""
+    from tallymap_amd import backend as B
+    prog = f._prepare(dev)[0]
+    for (dg, _), (adj, _) in list(B._ADJ.items()):
+        if dg == prog.digest() and B._FWD_ONLY.get(adj.digest() + "|vg") is not None:
+            return B.compiled(B._FWD_ONLY[adj.digest() + "|vg"], f._opts)
+    raise RuntimeError("bench: value_and_grad's kernel is not compiled")
 
 
 def measured(kind, field, key, n):
@@ -360,6 +376,25 @@ def bench_configs(steps, warmup, with_cpu):
         torch.cuda.synchronize()
         d["jvp_ms"] = float(np.mean([e[0].elapsed_time(e[1]) for e in jev]))
         d["jvp_items_per_s"] = n / (d["jvp_ms"] * 1e-3)
+        # value_and_grad: the forward's outputs from the adjoint's own launches (one for C1's forward-only
+        # adjoint, the count + reverse pair for the tape adjoint of C3 and C4)
+        if name in ("c1", "c3", "c4"):
+            vg = tm.value_and_grad(f, argnums=pos)
+            for _ in range(warmup):
+                vg(*dev)
+            torch.cuda.synchronize()
+            vev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+            for e in vev:
+                e[0].record(stream)
+                rv, _ = vg(*dev)
+                e[1].record(stream)
+            torch.cuda.synchronize()
+            assert np.array_equal(rv.per_item.cpu().numpy(), r.per_item.cpu().numpy())
+            d["vg_ms"] = float(np.mean([e[0].elapsed_time(e[1]) for e in vev]))
+            d["vg_items_per_s"] = n / (d["vg_ms"] * 1e-3)
+        else:
+            d["vg_ms"] = None
+            d["vg_note"] = "C5's cotangent (sin theta, omega) is a function of the forward's final states"
         if with_cpu:
             v, m, dt = _cpu_sample(name, inputs, 8.0)
             d["cpu_items_per_s"] = v
@@ -413,39 +448,53 @@ def main():
     dev = [torch.from_numpy(x0).cuda(), torch.from_numpy(keys).cuda(), torch.tensor(drift).cuda()]
     f = tm.vmap(cfg["item"], outputs=cfg["outputs"], in_axes=cfg["in_axes"], max_steps=cfg["max_steps"])
     g = tm.grad(f, argnums=2)
+    vg = tm.value_and_grad(f, argnums=2)
     stream = torch.cuda.current_stream()
 
     def step(ev=None):
         if ev:
             ev[0].record(stream)
-        r = f(*dev)
+        r, gr = vg(*dev)
         if ev:
             ev[1].record(stream)
+        return r, gr
+
+    def two(ev):
+        ev[0].record(stream)
+        r = f(*dev)
+        ev[1].record(stream)
         gr = g(*dev)
-        if ev:
-            ev[2].record(stream)
+        ev[2].record(stream)
         return r, gr
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(a.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
         r, gr = step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    grad_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    fused_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     ms = wall * 1e3 / a.steps
     N = a.n
     # sanity: the step computed what it should (no truncation, every item absorbed once, zero gradient)
     assert int(r.stats["n_truncated"].item()) == 0
     assert abs(float(r.outputs["wall"].sum().item()) - N) <= 1e-5 * N
     assert float(gr.item()) == 0.0
-    dom = "forward" if fwd_ms >= grad_ms else "gradient"
-    dom_ms = max(fwd_ms, grad_ms)
-    bpi = FWD_BYTES_PER_ITEM if dom == "forward" else GRAD_BYTES_PER_ITEM
+    # the same quantities from two launches (outside the timed region above)
+    two([torch.cuda.Event(enable_timing=True) for _ in range(3)])
+    ev2 = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(max(3, a.steps // 2))]
+    torch.cuda.synchronize()
+    for e in ev2:
+        r2, gr2 = two(e)
+    torch.cuda.synchronize()
+    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev2]))
+    grad_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev2]))
+    assert float(gr2.item()) == 0.0
+    assert np.array_equal(r2.per_item.cpu().numpy(), r.per_item.cpu().numpy())
+    dom, dom_ms, bpi = "fused", fused_ms, FWD_BYTES_PER_ITEM
     achieved = bpi * N / (dom_ms * 1e-3) / 1e9
     pi = B.compiled(f._prepare(dev)[0], f._opts)
     info = B.kernel_info(pi)
@@ -466,14 +515,18 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded threefry keys, x0 ~ U(0.2, 0.8))",
-        "config": {"workload": "C2: 1-D random walk, N=4,194,304, forward + replay gradient w.r.t. drift",
+        "config": {"workload": "C2: 1-D random walk, N=4,194,304, forward outputs + replay gradient w.r.t. drift "
+                               "per step (tm.value_and_grad: one fused launch)",
                    "n_items": N, "max_steps": cfg["max_steps"], "parallelism": "single GPU"},
+        "fused_ms": fused_ms,
+        "two_launch_items_per_s": N / ((fwd_ms + grad_ms) * 1e-3),
         "fwd_items_per_s": N / (fwd_ms * 1e-3),
         "grad_items_per_s": N / (grad_ms * 1e-3),
         "fwd_ms": fwd_ms,
         "grad_ms": grad_ms,
         "mean_trip_count": float(r.per_item.double().mean().item()),
-        "kernel": {"name": "tm_main (" + dom + ")", **info},
+        "kernel": {"name": "tm_adjoint (value_and_grad, fused)", **B.kernel_info(vg_kernel(f, dev))},
+        "forward_kernel": {"name": "tm_main (forward)", **info},
         "code_objects": ckeys,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,

@@ -8,8 +8,9 @@ reverse sweep) through the same path; forward-mode derivatives (jvp, jacfwd) run
 that spawn children (Queue) run generation by generation, one launch of the same kernel per generation.
 """
 from . import lax, numpy, random
-from ._api import STATS, Queue, Records, Result, Sum, TallyError, UnsupportedError, grad, jacfwd, jvp, vjp, vmap
+from ._api import (STATS, Queue, Records, Result, Sum, TallyError, UnsupportedError, grad, jacfwd, jvp,
+                   value_and_grad, vjp, vmap)
 from ._tally import Tally
 
 __version__ = "0.1.0"
-__all__ = ["vmap", "vjp", "grad", "jvp", "jacfwd", "Sum", "Queue", "Records", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]
+__all__ = ["vmap", "vjp", "grad", "value_and_grad", "jvp", "jacfwd", "Sum", "Queue", "Records", "Result", "STATS", "Tally", "TallyError", "UnsupportedError", "lax", "numpy", "random"]

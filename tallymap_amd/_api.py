@@ -551,6 +551,18 @@ def _tree_records_out(res_out, rt, recs, bad, over, sfx):
                     v.fill_(float("nan"))
 
 
+def _result(prog, meta, o, names, N):
+    """the Result of a forward launch's Outputs."""
+    res_out = _sum_outputs(prog, o, names)
+    stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
+    if prog.spawn is not None:
+        stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
+    ys, trunc = _split_ys(prog, list(o.ys))
+    trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
+    _record_outputs(prog, o, res_out, stats)
+    return Result(res_out, unflatten(meta["ytree"], ys), trunc, stats)
+
+
 def _split_ys(prog, ys):
     """the backend's per-item results -> (the item's own results, the truncation flag or None): the hidden
     per-item record counts are removed."""
@@ -667,15 +679,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
                 raise ValueError("tallymap: n_active with spawn is not supported")
             return _records_spawn(prepare, opts, names, args)
         o = B.run(prog, pi, bc, N, opts, n_active=None if n_active is None else int(n_active))
-        res_out = _sum_outputs(prog, o, names)
-        stats = {n: o.stats[ST[n]] for n in ("fixed_point_overflow", "dropped_emits")}
-        if prog.spawn is not None:
-            stats.update((n, o.stats[ST[n]]) for n in ("spawned", "children_dropped", "children_truncated"))
-        ys, trunc = _split_ys(prog, list(o.ys))
-        trunc, stats["n_truncated"] = _truncation(trunc, o.n_truncated, N)
-        _record_outputs(prog, o, res_out, stats)
-        per_item = unflatten(meta["ytree"], ys)
-        return Result(res_out, per_item, trunc, stats)
+        return _result(prog, meta, o, names, N)
 
     # Records outputs without a capacity: each call runs a count pass first and then the call sized by it
     dyn = [n for n in names if isinstance(outs_spec[n], Records) and outs_spec[n].capacity is None]
@@ -777,7 +781,6 @@ def vjp(mapped, *args, argnums=None, n_active=None):
 
 def _pullback(mapped, args, argnums, n_active=None):
     from . import backend as B
-    from ._tally import RSEP
     mapped = mapped._sized(args, n_active)
     prog, meta, pi, bc, N, axes = mapped._prepare(args)
     if prog.spawn is not None:
@@ -799,16 +802,7 @@ def _pullback(mapped, args, argnums, n_active=None):
     spec, wrt = _arg_leaves(vprog, args, axes, an)
 
     def pullback(ct_outputs=None, ct_per_item=None):
-        cts = {}
-        for k, s in enumerate(vprog.tallies):
-            if not ct_outputs:
-                break
-            if s.name in ct_outputs:
-                cts[k] = ct_outputs[s.name]
-            elif RSEP in s.name:                     # a Records field: ct_outputs[name][field]
-                r, f = s.name.split(RSEP, 1)
-                if isinstance(ct_outputs.get(r), dict) and f in ct_outputs[r]:
-                    cts[k] = ct_outputs[r][f]
+        cts = _tally_cts(vprog, ct_outputs)
         cys = {}
         if ct_per_item is not None:
             yl, _ = flatten(ct_per_item)
@@ -821,6 +815,22 @@ def _pullback(mapped, args, argnums, n_active=None):
             g_bc = [x.float().fill_(float("nan")) for x in g_bc]
         return _arg_cotangents(spec, wrt, g_pi, g_bc)
     return pullback
+
+
+def _tally_cts(prog, ct_outputs):
+    """{tally slot: cotangent} of prog from {output name: cotangent} (a Records field: {name: {field: ...}})."""
+    from ._tally import RSEP
+    cts = {}
+    for k, s in enumerate(prog.tallies):
+        if not ct_outputs:
+            break
+        if s.name in ct_outputs:
+            cts[k] = ct_outputs[s.name]
+        elif RSEP in s.name:
+            r, f = s.name.split(RSEP, 1)
+            if isinstance(ct_outputs.get(r), dict) and f in ct_outputs[r]:
+                cts[k] = ct_outputs[r][f]
+    return cts
 
 
 def _tree_pullback(mapped, args, argnums):
@@ -910,6 +920,27 @@ def grad(mapped, weights=None, argnums=None):
     def g(*args, n_active=None):
         return _pullback(mapped, args, argnums, n_active)(
             weights if weights is not None else {n: 1.0 for n in mapped._names})
+    return g
+
+
+def value_and_grad(mapped, weights=None, argnums=None):
+    """(Result, gradient) of the mapped call: the forward's outputs and the gradient grad(mapped, weights, argnums)
+    gives, from the adjoint's launches alone where the adjoint replays the whole forward anyway (jax.value_and_grad
+    of a tallymap call).  The forward-only adjoint (no loop carry needs a reverse sweep) returns both from ONE
+    launch; the tape adjoint's count launch returns the forward's outputs beside the tape, so the pair takes two
+    launches instead of a forward launch and two adjoint ones.  Records outputs, spawn and the checkpointed replay
+    schedules run the forward and the adjoint separately.  The returned function takes n_active=n as the call does."""
+    def g(*args, n_active=None):
+        w = weights if weights is not None else {n: 1.0 for n in mapped._names}
+        m = mapped._sized(args, n_active)
+        prog, meta, pi, bc, N, axes = m._prepare(args)
+        if prog.records or prog.spawn is not None or m._opts.get("rev_schedule", "tape") != "tape":
+            return m(*args, n_active=n_active), _pullback(m, args, argnums, n_active)(w)
+        from . import backend as B
+        spec, wrt = _arg_leaves(prog, args, axes, _argnums(argnums, len(args)))
+        g_pi, g_bc, _, fo = B.run_vjp(prog, wrt, pi, bc, N, _tally_cts(prog, w), {}, m._opts, n_active=n_active,
+                                      forward=True)
+        return _result(prog, meta, fo, m._names, N), _arg_cotangents(spec, wrt, g_pi, g_bc)
     return g
 
 

@@ -370,12 +370,12 @@ def prebuild(entries, n=64):
         for wrt in ((wp, wb), ((), wb)):
             adj = R.adjoint_program(prog, wrt)
             pl = R.plan(adj)
-            if any(pl.car_act):          # the tape adjoint: its count and reverse programs
-                from . import tape as T
+            if any(pl.car_act):          # the tape adjoint: its count and reverse programs (and value_and_grad's
+                from . import tape as T  # count program, which keeps the forward's outputs)
                 tp = T.programs(adj, pl)
-                progs = [tp.count, tp.reverse]
+                progs = [tp.count, tp.reverse, T.programs(adj, pl, keep=True).count]
             else:
-                progs = [R.forward_only_program(adj, pl)]
+                progs = [R.forward_only_program(adj, pl), R.forward_only_program(adj, pl, keep=True)]
             for q in progs:
                 src, _ = K.build(q, block=K.BLOCK, schedule="step", refill=1)
                 Cm.code_object(src, name=f"tm_{q.tag}.hip", store_pkg=True)
@@ -415,7 +415,18 @@ def compiled_adjoint(adj, opts):
     return c
 
 
-def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None):
+def _forward_outputs(prog, c, res, ys):
+    """the forward's Outputs read from a value_and_grad launch of c (whose tally slots < prog.nT are the forward's,
+    ys its per-item results)."""
+    import torch
+    L = c.layout
+    base = L.n_in
+    tallies = [res[L.r_out[k] - base] for k in prog.out_tallies]
+    ntr = res[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
+    return Outputs(tallies, res[L.r_stats - base], list(ys), ntr, {}, [])
+
+
+def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forward=False):
     """the replay adjoint of prog: cotangents of the per-item operands wrt[0] ([N, ...] each) and the broadcast
     operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
     0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated).
@@ -423,7 +434,10 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None):
     run by the forward template (step refill); otherwise the replay kernel opts['rev_schedule'] names: 'step' (the
     default, replay.build: step refill over a tape) or 'item' (reverse.build: in-lane checkpoints).  With n_active
     only the first n_active items run (the adjoint launches over them alone); the others get zero cotangents and
-    add nothing to the broadcast ones, as they emitted nothing in the forward."""
+    add nothing to the broadcast ones, as they emitted nothing in the forward.
+    forward: value_and_grad -- the launches that replay the forward (the forward-only adjoint; the tape adjoint's
+    count program) also return the forward's outputs, so no separate forward launch is needed: -> (g_pi, g_bc,
+    n_truncated, Outputs of the forward)."""
     import torch
 
     from . import reverse as R
@@ -465,30 +479,40 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None):
         else:
             ins_b.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
                                        else x, np.float32).reshape(-1))
+    fo = None
     if not any(pl.car_act):
-        q = _FWD_ONLY.get(adj.digest())
+        fkey = adj.digest() + ("|vg" if forward else "")
+        q = _FWD_ONLY.get(fkey)
         if q is None:
-            q = _FWD_ONLY[adj.digest()] = R.forward_only_program(adj, pl)
+            q = _FWD_ONLY[fkey] = R.forward_only_program(adj, pl, keep=forward)
         c = compiled(q, opts)
         res = launch(c, ins_p + ins_b, N)
         L = c.layout
         base = L.n_in
-        g_bc = [res[L.r_out[k] - base].reshape(prog.b_avals()[j].shape)
-                for k, j in zip(q.out_tallies, adj.wrt_bc)]
+        nT = prog.nT
+        g_bc = [res[L.r_out[nT + jj] - base].reshape(prog.b_avals()[j].shape) for jj, j in enumerate(adj.wrt_bc)]
         ys = [res[r - base] for r in L.r_ys]
         g_pi = ys[:len(adj.wrt_pi)]
+        if forward:
+            fo = _forward_outputs(prog, c, res, ys[len(adj.wrt_pi):])
     elif opts.get("rev_schedule", "tape") == "tape":
         from . import tape as T
-        tp = _TAPE.get(adj.digest())
+        tkey = adj.digest() + ("|vg" if forward else "")
+        tp = _TAPE.get(tkey)
         if tp is None:
-            tp = _TAPE[adj.digest()] = T.programs(adj, pl)
+            tp = _TAPE[tkey] = T.programs(adj, pl, keep=forward)
         cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"))
         capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
         tape = torch.empty((max(1, N * cap * tp.Wp),), dtype=torch.uint32, device="cuda")
-        # count: the loop with its states taped, POST's VJP -> K, lambda, P cotangents, truncation
+        # count: the loop with its states taped, POST's VJP -> K, lambda, P cotangents, truncation (and with
+        # `forward`, the forward's own outputs)
         c1 = compiled(tp.count, opts)
         r1 = launch(c1, ins_p + ins_b + [capt], N, tape=tape)
         hand = [r1[r - c1.layout.n_in] for r in c1.layout.r_ys]
+        if forward:
+            nh = 1 + len(tp.n_lam) + len(tp.n_gp)
+            fo = _forward_outputs(prog, c1, r1, hand[nh:])
+            hand = hand[:nh] + ([hand[tp.count.trunc]] if prog.trunc is not None else [])
         # reverse: the steps' VJPs newest first from the tape, PRE's VJP -> the cotangents
         c = compiled(tp.reverse, opts)
         res = launch(c, ins_p + hand + ins_b + [capt], N, tape=tape)
@@ -498,6 +522,8 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None):
                 for k, j in zip(tp.reverse.out_tallies, adj.wrt_bc)]
         g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
     else:
+        if forward:
+            raise ValueError("tallymap_amd: value_and_grad in one pass runs the default (tape) replay schedule")
         c = compiled_adjoint(adj, opts)
         res = launch(c, ins_p + ins_b, N)
         L = c.layout
@@ -505,13 +531,20 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None):
         g_bc = [res[L.r_out[j] - base] for j in adj.wrt_bc]
         g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
     ntr = res[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
-    if N != N_all:
+
+    def pad(xs):
         full = []
-        for g in g_pi:
+        for g in xs:
             z = torch.zeros((N_all,) + tuple(g.shape[1:]), dtype=g.dtype, device=g.device)
             z[:N] = g
             full.append(z)
-        g_pi = full
+        return full
+    if N != N_all:
+        g_pi = pad(g_pi)
+        if fo is not None:
+            fo.ys = pad(fo.ys)
+    if forward:
+        return g_pi, g_bc, ntr, fo
     return g_pi, g_bc, ntr
 
 

@@ -767,9 +767,13 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             ct = ctype(s.dtype)
             post.append(f"if (tm_bad) for (i64 i = g; i < {s.S}; i += st) "
                         f"(({ct}*)P.p[{r_out[k]}])[i] = __builtin_nanf(\"\");")
-    if getattr(prog, "poison_ys", False) and prog.trunc is not None:
-        # a derived program (the adjoint): every float per-item result is NaN when an item was truncated
+    pz = getattr(prog, "poison_ys", False)
+    if pz and prog.trunc is not None:
+        # a derived program (the adjoint): every float per-item result (True) or those listed (the cotangents of a
+        # value_and_grad launch) is NaN when an item was truncated
         for j, a in enumerate(yav):
+            if pz is not True and j not in pz:
+                continue
             if a.dtype in (C.F32, C.F64):
                 n = max(1, a.size)
                 post.append(f"if (TM_CTL[2] != 0u) for (i64 i = g; i < n_items * {n}; i += st) "
@@ -784,7 +788,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body = []
     # the gradient launch of a forward-only adjoint is named tm_adjoint like the checkpointed one (profiles tell the
     # forward and gradient launches apart by name; the launcher accepts either entry)
-    entry = "tm_adjoint" if getattr(prog, "poison_ys", False) else "tm_main"
+    entry = "tm_adjoint" if getattr(prog, "poison_ys", False) is not False else "tm_main"
     lb = f"{block}, {max(1, int(min_blocks) * block // 256)}" if min_blocks else f"{block}"
     body.append(f"extern \"C\" __global__ void __launch_bounds__({lb}) {entry}(const TmParams P, "
                 "const i64 n_items) {")

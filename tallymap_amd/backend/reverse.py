@@ -300,13 +300,17 @@ def emit_dense_ct(t, v, n):
     return t
 
 
-def forward_only_program(adj, pl):
+def forward_only_program(adj, pl, keep=False):
     """the adjoint as an ordinary item program, when no loop carry needs a reverse sweep: PRE, the loop with the
     step VJPs of the body constants accumulated as extra carries, POST, POST's and PRE's VJPs, one exact emit per
     differentiated broadcast element.  It runs through the forward kernel template (step refill).
     invars: tallies [forward tallies, discarded][ct of each differentiated broadcast operand, exact] + per-item
     [operands][result cotangents] + broadcast [operands][tally cotangents]; per-item results [operand
-    cotangents][truncated]."""
+    cotangents][truncated].
+    keep: the forward's own outputs too, for value_and_grad in one launch (the program replays the whole forward
+    anyway): the forward tallies keep their kinds and the per-item results are [operand cotangents] + [the
+    forward's per-item results, its truncation flag among them]; only the cotangents are NaN-poisoned by a
+    truncation, the forward's results are as the forward returns them."""
     prog, sp = adj.prog, pl.sp
     nT, nP, nB = prog.nT, prog.nP, prog.nB
     pav, bav, yav = prog.p_avals(), prog.b_avals(), prog.y_avals()
@@ -323,7 +327,7 @@ def forward_only_program(adj, pl):
     pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)},
                                             sparse=sp_pre, prune=True)
     ct_emit = ct_emitter(adj, nT)
-    tspecs = [dataclasses.replace(s, kind="discard") for s in prog.tallies]
+    tspecs = [s if keep else dataclasses.replace(s, kind="discard") for s in prog.tallies]
     tspecs += [TSpec(f"ct{j}", tuple(bav[j].shape) or (1,), np.dtype(np.float32), exact=True) for j in adj.wrt_bc]
     b = C.Builder()
     C._STACK.append(b)
@@ -401,8 +405,17 @@ def forward_only_program(adj, pl):
                 v = C.Tracer(C.bind("copy", [C.literal(np.zeros(pav[i].shape, np.float32), C.F32)],
                                     [C.AVal(pav[i].shape, C.F32)])[0].var)
             ys.append(v)
+        ng = len(ys)
         trunc = None
-        if prog.trunc is not None:
+        if keep:
+            for j, a in enumerate(yav):
+                v = post_outs[nT + j]
+                if not C.is_traced(v):
+                    v = C.Tracer(C.bind("copy", [C.literal(np.broadcast_to(np.asarray(v, a.dtype), a.shape).copy(),
+                                                           a.dtype)], [a.strong()])[0].var)
+                ys.append(v)
+            trunc = ng + prog.trunc if prog.trunc is not None else None
+        elif prog.trunc is not None:
             ys.append(post_outs[nT + prog.trunc])
             trunc = len(ys) - 1
         outs = [b.local(t.var) for t in touts + ct_t] + [b.local(y.var) for y in ys]
@@ -411,8 +424,9 @@ def forward_only_program(adj, pl):
     jx = C.Jaxpr(b.invars, outs, b.eqns)
     from .._api import check_tallies
     check_tallies(jx, len(tspecs), adj.where)
-    q = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft), trunc, adj.tag, adj.where)
-    q.poison_ys = True
+    q = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft), trunc, adj.tag + ("-vg" if keep else ""),
+                    adj.where)
+    q.poison_ys = tuple(range(ng)) if keep else True
     return q
 
 

@@ -123,9 +123,12 @@ class TapePrograms:
     n_gp: list              # per P var q with a cotangent from POST: (q, aval)
 
 
-def programs(adj, pl):
+def programs(adj, pl, keep=False):
     """-> TapePrograms of adj (reverse.Adjoint) under pl (reverse.Plan); raises ReverseError when no loop carry
-    needs the reverse sweep (the forward-only adjoint applies then)."""
+    needs the reverse sweep (the forward-only adjoint applies then).  keep: the count program (which replays the
+    whole forward) also returns the forward's own outputs, for value_and_grad in two launches instead of three:
+    its tallies keep their kinds and its per-item results are [K, lambda, P cotangents] + [the forward's per-item
+    results, its truncation flag among them]."""
     if not any(pl.car_act):
         raise ReverseError("internal: the tape adjoint is for programs with an active loop carry")
     prog, sp = adj.prog, pl.sp
@@ -149,7 +152,7 @@ def programs(adj, pl):
     I32, F32 = C.I32, C.F32
 
     # ------------------------------------------------------------------------------------------ count
-    tspecs = disc + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
+    tspecs = (list(prog.tallies) if keep else disc) + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
     b = C.Builder()
     C._STACK.append(b)
     try:
@@ -201,7 +204,12 @@ def programs(adj, pl):
         for q in gp_q:
             ys.append(tracer_of(got[q], C.AVal(P_av[q].shape, F32)))
         trunc = None
-        if prog.trunc is not None:
+        if keep:
+            nh = len(ys)
+            for j, a in enumerate(yav):
+                ys.append(tracer_of(post_outs[nT + j], a))
+            trunc = nh + prog.trunc if prog.trunc is not None else None
+        elif prog.trunc is not None:
             ys.append(post_outs[nT + prog.trunc])
             trunc = len(ys) - 1
         touts = [C.Tracer(b.local(t.var)) if C.is_traced(t) else t for t in post_outs[:nT]] + [tok]
@@ -210,7 +218,8 @@ def programs(adj, pl):
         C._STACK.pop()
     jx = C.Jaxpr(b.invars, outs, b.eqns)
     check_tallies(jx, len(tspecs), adj.where)
-    count = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft) + 1, trunc, adj.tag + "-count", adj.where)
+    count = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft) + 1, trunc,
+                        adj.tag + "-count" + ("-vg" if keep else ""), adj.where)
     count.tape_words = Wp
 
     # ----------------------------------------------------------------------------------------- reverse

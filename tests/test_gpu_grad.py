@@ -182,3 +182,39 @@ def test_grad_wrt_a_1024_row_table(kind):
     _sync()
     assert np.array_equal(_np(ga).view(np.uint32), _np(gm).view(np.uint32))
     assert np.array_equal(_np(ga).view(np.uint32), _table_grad_want(i[:m], x[:m], kind == "walk").view(np.uint32))
+
+
+def _vg_cases():
+    """(config name, inputs, argnums, weights) of the value_and_grad checks: C1 (forward-only adjoint), C3 and C5 (the
+    tape adjoint's count launch returns the forward)."""
+    n3, n5 = 65_536, 4096
+    return [("c1", lambda: configs.c1_inputs(20_000), 2, None),
+            ("c3", lambda: configs.c3_inputs(n3), 1, None),
+            ("c5", lambda: configs.c5_inputs(n5), 3, {"state": 1.0})]
+
+
+@pytest.mark.parametrize("name,inputs,argnums,weights", _vg_cases(), ids=["c1", "c3", "c5"])
+def test_value_and_grad_in_fewer_launches(name, inputs, argnums, weights):
+    """value_and_grad: the forward's outputs (tallies bitwise where exact, else within the float32 atomic-order
+    tolerance; per-item results and truncation flags bitwise) and the gradient (bitwise: the same kernels' exact
+    sums) equal the separate forward call and grad."""
+    import torch
+    print(f"case: value_and_grad {name}", flush=True)
+    cfg = configs.SIZED[name](len(inputs()[0])) if name in configs.SIZED else configs.CONFIGS[name]
+    f = _mapped(cfg)
+    args = inputs()
+    res, g = tm.value_and_grad(f, weights=weights, argnums=argnums)(*args)
+    ref = f(*args)
+    g_ref = tm.grad(f, weights=weights, argnums=argnums)(*args)
+    torch.cuda.synchronize()
+    assert np.array_equal(np.atleast_1d(_np(g)).view(np.uint32), np.atleast_1d(_np(g_ref)).view(np.uint32))
+    for k in ref.outputs:
+        a, b = _np(res.outputs[k]), _np(ref.outputs[k])
+        assert a.shape == b.shape and np.allclose(a, b, rtol=1e-5, atol=1e-6 * float(np.abs(b).max())), k
+    ya = [_np(y) for y in (res.per_item if isinstance(res.per_item, (tuple, list)) else [res.per_item])] \
+        if res.per_item is not None else []
+    yb = [_np(y) for y in (ref.per_item if isinstance(ref.per_item, (tuple, list)) else [ref.per_item])] \
+        if ref.per_item is not None else []
+    assert len(ya) == len(yb) and all(np.array_equal(x.view(np.uint8), y.view(np.uint8)) for x, y in zip(ya, yb))
+    assert np.array_equal(_np(res.truncated), _np(ref.truncated))
+    assert int(_np(res.stats["n_truncated"])) == int(_np(ref.stats["n_truncated"]))
