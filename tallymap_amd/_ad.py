@@ -70,10 +70,11 @@ def relevance(jx, out_rel, emits=True):
     return [isinstance(v, C.Var) and v.id in rel for v in jx.invars]
 
 
-def eval_jaxpr(jx, args, ct_read=None, ct_emit=None):
+def eval_jaxpr(jx, args, ct_read=None, ct_emit=None, want=None):
     """re-bind jx's equations on `args` (Tracers / numpy scalars) in the current trace -> its outputs.
     ct_read(slot, idx) replaces the `tm_ct_read` primitive of a VJP program, ct_emit(tag, idx, value) its
-    `tm_ct_emit` (a sparse table-read cotangent: vjp_jaxpr's `sparse`)."""
+    `tm_ct_emit` (a sparse table-read cotangent: vjp_jaxpr's `sparse`).  want: var ids of jx (invars or equation
+    outputs) whose values are returned too -> (outputs, [their values])."""
     env = {v.id: a for v, a in zip(jx.invars, args)}
     for e in jx.eqns:
         ins = [_t(v, env) for v in e.invars]
@@ -88,6 +89,8 @@ def eval_jaxpr(jx, args, ct_read=None, ct_emit=None):
             outs = _replay(e, ins)
         for o, x in zip(e.outvars, outs):
             env[o.id] = x
+    if want is not None:
+        return [_t(v, env) for v in jx.outvars], [env[i] for i in want]
     return [_t(v, env) for v in jx.outvars]
 
 
@@ -118,7 +121,7 @@ def _zeros_like(aval):
 
 
 def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=None, with_primal=False,
-              sparse=None, prune=False):
+              sparse=None, prune=False, info=None):
     """-> (Jaxpr, ct_out_mask, ct_in_mask).
     The Jaxpr's invars: jx.invars + [cotangent of each output in ct_out_mask]; outvars: [cotangent of each input
     in ct_in_mask], preceded (with_primal) by jx's own outputs, replayed: one program for a step and its VJP.  ct_out_mask: jx's active float outputs; ct_in_mask: jx's active inputs.
@@ -131,7 +134,9 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
     dense cotangent with a select per row of the table (the reference's sparse table-read cotangent,
     _reverse.py:1047).  Such an input keeps a dense cotangent output only if other uses give it one (ct_in_mask
     False otherwise).  prune: the same for every input: an active input that no use gives a cotangent (a loop
-    constant the step never reads, say) has ct_in_mask False instead of a zero output."""
+    constant the step never reads, say) has ct_in_mask False instead of a zero output.
+    info: a dict that receives n_replay (the Jaxpr's first n_replay equations replay jx's own, in order; the rest
+    are the backward pass) and env ({jx var id: its value in the replay})."""
     tslot = {jx.invars[i].id: s for i, s in (slots or {}).items()}
     sp_tag = {jx.invars[i].id: t for i, t in (sparse or {}).items()}
     act = activity(jx, active_in)
@@ -158,6 +163,8 @@ def vjp_jaxpr(jx, active_in, ct_read, slots=None, emits_active=True, ct_given=No
             for o, x in zip(e.outvars, outs):
                 env[o.id] = x
             recs.append((e, ins, outs))
+        if info is not None:
+            info["n_replay"], info["env"] = len(b.eqns), dict(env)
         ct = {}
 
         def add(v, c):

@@ -24,7 +24,7 @@ MAX_ITEMS = 2 ** 31 - 1
 SUM_DTYPES = (C.F32, C.F64, C.I32, C.U32, C.I64, C.U64)
 PROG_CACHE = 64
 OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact", "rev_schedule",
-        "rev_tape", "rev_refill")
+        "rev_tape", "rev_refill", "rev_residual")
 
 
 class UnsupportedError(NotImplementedError):
@@ -618,7 +618,9 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
                (iterations between the tail-phase repacks of a workgroup's live items, default 16; 0: off);
                rev_schedule (reverse mode: 'step', the default, a step-refilled replay over a tape in HBM, or
                'item', one item per lane with in-lane checkpoints); rev_tape (states a lane's tape holds, default
-               512; longer items are swept from checkpoints); rev_refill (free lanes a wave waits for before the
+               512; longer items are swept from checkpoints); rev_residual (the tape adjoint's tape: None, the
+               default, tapes what the step's VJP reads when that is no wider than the step's state, True / False
+               force the residual / state tape); rev_refill (free lanes a wave waits for before the
                step-scheduled replay hands it items, default 32; 64 suits items of equal length); rev_checkpoints (the 'item' schedule's C states per
                checkpoint buffer); cuda_math and min_blocks_per_sm
                are accepted for drop-in compatibility and have no meaning on ROCm.

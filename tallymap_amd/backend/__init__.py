@@ -497,13 +497,14 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
             fo = _forward_outputs(prog, c, res, ys[len(adj.wrt_pi):])
     elif opts.get("rev_schedule", "tape") == "tape":
         from . import tape as T
-        tkey = adj.digest() + ("|vg" if forward else "")
+        rres = opts.get("rev_residual")
+        tkey = adj.digest() + ("|vg" if forward else "") + f"|{rres}"
         tp = _TAPE.get(tkey)
         if tp is None:
-            tp = _TAPE[tkey] = T.programs(adj, pl, keep=forward)
-        cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"))
+            tp = _TAPE[tkey] = T.programs(adj, pl, keep=forward, residual=rres)
+        cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"), tp.Wck)
         capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
-        tape = torch.empty((max(1, N * cap * tp.Wp),), dtype=torch.uint32, device="cuda")
+        tape = torch.empty((max(1, N * (cap * tp.Wp + tp.Wck)),), dtype=torch.uint32, device="cuda")
         # count: the loop with its states taped, POST's VJP -> K, lambda, P cotangents, truncation (and with
         # `forward`, the forward's own outputs)
         c1 = compiled(tp.count, opts)

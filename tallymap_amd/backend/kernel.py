@@ -306,6 +306,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     # the tape adjoint's programs (backend/tape.py): a u32 buffer of N x cap x Wp words (cap: an operand), written
     # by the count program's tape puts and read by the reverse program's gets; the caller allocates it
     tape_w = int(getattr(prog, "tape_words", 0) or 0)
+    tape_ck = int(getattr(prog, "tape_ck_words", 0) or 0)     # (the residual tape's checkpoint after the slots)
     r_tape = result((tape_w,), np.uint32, per_item=("itape",)) if tape_w else None
     R = n_in + len(res)
 
@@ -431,21 +432,26 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                 ws.append(f"(u32)({el})")
         return ws
 
-    def tape_row(em_, k, cap, const):
+    def tape_row(em_, k, cap, const, ck=False):
+        """slot k of the item's tape row (a row: cap slots of tape_w words, then tape_ck words of checkpoint), or
+        (ck) the row's checkpoint."""
         p = em_.fresh("tp")
-        em_.line(f"{const}u32* const {p} = ({const}u32*)P.p[{r_tape}] + ((u64)tm_item * (u64)(u32)({cap}) + "
-                 f"(u64)(u32)({k})) * {tape_w}ull;")
+        at = f"(u64)(u32)({cap}) * {tape_w}ull" if ck else f"(u64)(u32)({k}) * {tape_w}ull"
+        em_.line(f"{const}u32* const {p} = ({const}u32*)P.p[{r_tape}] + (u64)tm_item * ((u64)(u32)({cap}) * "
+                 f"{tape_w}ull + {tape_ck}ull) + {at};")
         return p
 
     def tape_put_rule(em_, e, ins):
-        """the state before step k into slot k of the item's tape row, when k < cap (whole 16-byte units)."""
+        """leaves into slot k of the item's tape row when k < cap, or (ck) into the row's checkpoint when k == cap
+        (whole 16- or 8-byte units)."""
         t, k, cap = ins[0], ins[1], ins[2]
+        W, ck = int(e.params["words"]), bool(e.params.get("ck", False))
         ws = [w_ for v in ins[3:] for w_ in _words_of(em_, v)]
-        ws += ["0u"] * (tape_w - len(ws))
-        em_.open(f"if ((u32)({k.el[0]}) < (u32)({cap.el[0]}))")
-        p = tape_row(em_, k.el[0], cap.el[0], "")
-        u = 4 if tape_w % 4 == 0 else (2 if tape_w % 2 == 0 else 1)
-        for q in range(0, tape_w, u):
+        ws += ["0u"] * (W - len(ws))
+        em_.open(f"if ((u32)({k.el[0]}) {'==' if ck else '<'} (u32)({cap.el[0]}))")
+        p = tape_row(em_, k.el[0], cap.el[0], "", ck)
+        u = 4 if W % 4 == 0 else (2 if W % 2 == 0 else 1)
+        for q in range(0, W, u):
             if u == 1:
                 em_.line(f"{p}[{q}] = {ws[q]};")
             else:
@@ -455,12 +461,13 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     em.hooks["tallymap_tape_put"] = tape_put_rule
 
     def tape_get_rule(em_, e, ins):
-        """the state stored in slot j (< cap) of the item's tape row."""
+        """the leaves stored in slot j (< cap) of the item's tape row, or (ck) in its checkpoint."""
         j, cap = ins
-        p = tape_row(em_, j.el[0], cap.el[0], "const ")
+        W, ck = int(e.params["words"]), bool(e.params.get("ck", False))
+        p = tape_row(em_, j.el[0], cap.el[0], "const ", ck)
         words = []
-        u = 4 if tape_w % 4 == 0 else (2 if tape_w % 2 == 0 else 1)
-        for q in range(0, tape_w, u):
+        u = 4 if W % 4 == 0 else (2 if W % 2 == 0 else 1)
+        for q in range(0, W, u):
             if u == 1:
                 words.append(em_.bind(f"{p}[{q}]", C.U32, "tq"))
                 continue
@@ -786,9 +793,11 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
 
     # tm_main
     body = []
-    # the gradient launch of a forward-only adjoint is named tm_adjoint like the checkpointed one (profiles tell the
-    # forward and gradient launches apart by name; the launcher accepts either entry)
-    entry = "tm_adjoint" if getattr(prog, "poison_ys", False) is not False else "tm_main"
+    # the item loop is named for its role (profiles tell the launches apart by name; the launcher accepts each):
+    # tm_main a forward, tm_adjoint a gradient launch (forward-only or checkpointed), tm_count the tape adjoint's
+    # counting pass, tm_fused an adjoint launch that also returns the forward (value_and_grad); prog.entry sets it
+    entry = getattr(prog, "entry", None) or ("tm_adjoint" if getattr(prog, "poison_ys", False) is not False
+                                             else "tm_main")
     lb = f"{block}, {max(1, int(min_blocks) * block // 256)}" if min_blocks else f"{block}"
     body.append(f"extern \"C\" __global__ void __launch_bounds__({lb}) {entry}(const TmParams P, "
                 "const i64 n_items) {")

@@ -427,6 +427,7 @@ def forward_only_program(adj, pl, keep=False):
     q = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft), trunc, adj.tag + ("-vg" if keep else ""),
                     adj.where)
     q.poison_ys = tuple(range(ng)) if keep else True
+    q.entry = "tm_fused" if keep else "tm_adjoint"
     return q
 
 

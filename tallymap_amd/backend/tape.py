@@ -82,24 +82,117 @@ def state_words(sp):
     stored and loaded in 16-byte units when its words are a multiple of 4, else in 8-byte units (C5's six words:
     24 bytes, not 32)."""
     W = sum(max(1, sp.body.outvars[j].aval.size) * _nwords(sp.body.outvars[j].aval.dtype) for j in stored_carries(sp))
-    return max(1, W) if W <= 2 else W + (W & 1)
+    return _pad_words(W)
 
 
-def tape_cap(N, Wp, want=None):
-    """the tape slots per item at N items (`want`: a caller's choice, clamped to >= 1)."""
+def tape_cap(N, Wp, want=None, Wck=0):
+    """the tape slots per item at N items (`want`: a caller's choice, clamped to >= 1); a row is cap slots of Wp
+    words and a checkpoint of Wck."""
     if want:
         return max(1, int(want))
-    per = BUDGET // max(1, int(N) * Wp * 4)
+    per = (BUDGET // max(1, int(N) * 4) - Wck) // max(1, Wp)
     return int(max(CAP_MIN, min(CAP_MAX, per // 16 * 16)))
 
 
-def _put(tok, k, cap, leaves, Wp):
+def _pad_words(W):
+    return max(1, W) if W <= 2 else W + (W & 1)
+
+
+@dataclasses.dataclass
+class Residuals:
+    """what the step's VJP reads of the forward step, taped instead of the state (the residual tape):
+    back       the backward half of the step's VJP program: invars [loop constants] + [the residual values] +
+               [carry cotangents]; outvars the VJP program's
+    body_vars  per residual, the loop body's var that holds it (an invar: a carry; else an equation's output)
+    avals      per residual, its aval
+    Wv         u32 words of one tape slot: the non-boolean residuals, then the boolean ones as bits of one word"""
+    back: C.Jaxpr
+    body_vars: list
+    avals: list
+    Wv: int
+
+    def _split(self):
+        b = [i for i, a in enumerate(self.avals) if a.dtype == C.BOOL and a.shape == ()]
+        o = [i for i in range(len(self.avals)) if i not in b]
+        return o, b
+
+    def slot_avals(self):
+        o, b = self._split()
+        return [self.avals[i] for i in o] + ([C.AVal((), C.U32)] if b else [])
+
+    def pack(self, vals):
+        """the residual values -> the tape slot's leaves (scalar booleans packed into the last word)."""
+        o, b = self._split()
+        leaves = [vals[i] for i in o]
+        if b:
+            w = None
+            for bit, i in enumerate(b):
+                x = C.convert(vals[i], C.U32) << bit if bit else C.convert(vals[i], C.U32)
+                w = x if w is None else w | x
+            leaves.append(w)
+        return leaves
+
+    def unpack(self, leaves):
+        o, b = self._split()
+        vals = [None] * len(self.avals)
+        for i, x in zip(o, leaves):
+            vals[i] = x
+        if b:
+            w = leaves[len(o)]
+            for bit, i in enumerate(b):
+                vals[i] = ((w >> bit) & 1) != 0 if bit else (w & 1) != 0
+        return vals
+
+
+def residual_plan(sp, body_vjp, info, nbc):
+    """-> Residuals of the step VJP program body_vjp (vjp_jaxpr of sp.body with info), or None when its backward
+    half holds sub-programs or reads a value the loop body cannot name."""
+    nr = info["n_replay"]
+    back = body_vjp.eqns[nr:]
+    if any(C.subjaxprs(e) for e in back):
+        return None
+    used = set()
+    for e in back:
+        used |= {v.id for v in e.invars if isinstance(v, C.Var)}
+    used |= {v.id for v in body_vjp.outvars if isinstance(v, C.Var)}
+    n_in = len(sp.body.invars)
+    carry_at = {v.id: i for i, v in enumerate(body_vjp.invars[:n_in]) if i >= nbc}
+    res = [o for e in body_vjp.eqns[:nr] for o in e.outvars if o.id in used]
+    res += [v for v in body_vjp.invars[nbc:n_in] if v.id in used]
+    replay_of = {}                               # replay var id -> the body var it replays
+    body_var = {v.id: v for v in sp.body.invars}
+    for e in sp.body.eqns:
+        for o in e.outvars:
+            body_var[o.id] = o
+    for bid, x in info["env"].items():
+        if C.is_traced(x):
+            replay_of.setdefault(x.var.id, bid)
+    bvars = []
+    for v in res:
+        if v.id in carry_at:
+            bvars.append(sp.body.invars[carry_at[v.id]])
+            continue
+        bid = replay_of.get(v.id)
+        if bid is None or bid not in body_var:
+            return None
+        bvars.append(body_var[bid])
+    cts = body_vjp.invars[n_in:]
+    back_jx = C.Jaxpr(list(body_vjp.invars[:nbc]) + res + list(cts), list(body_vjp.outvars), list(back))
+    avals = [v.aval for v in res]
+    nb = sum(1 for a in avals if a.dtype == C.BOOL and a.shape == ())
+    W = sum(max(1, a.size) * _nwords(a.dtype) for a in avals if not (a.dtype == C.BOOL and a.shape == ()))
+    return Residuals(back_jx, bvars, avals, _pad_words(W + (1 if nb else 0)))
+
+
+def _put(tok, k, cap, leaves, Wp, ck=False):
+    """leaves into slot k of the item's tape row when k < cap, or (ck) into its checkpoint when k == cap."""
     ins = [C.as_var(tok), C.as_var(k), C.as_var(cap)] + [C.as_var(x) for x in leaves]
-    return C.bind("tallymap_tape_put", ins, [tok.aval], words=Wp)[0]
+    return C.bind("tallymap_tape_put", ins, [tok.aval], words=Wp, ck=bool(ck))[0]
 
 
-def _get(j, cap, avals, Wp):
-    return C.bind("tallymap_tape_get", [C.as_var(j), C.as_var(cap)], list(avals), words=Wp)
+def _get(j, cap, avals, Wp, ck=False):
+    """slot j (< cap) of the item's tape row, or (ck) its checkpoint."""
+    return C.bind("tallymap_tape_get", [C.as_var(j), C.as_var(cap)], list(avals), words=Wp, ck=bool(ck))
 
 
 def _consts(sp, Pv):
@@ -118,17 +211,19 @@ def _never(sp):
 class TapePrograms:
     count: ItemProgram
     reverse: ItemProgram
-    Wp: int
+    Wp: int                 # u32 words of a tape slot
     n_lam: list             # per active carry j (in order): its cotangent per-item result of `count`
     n_gp: list              # per P var q with a cotangent from POST: (q, aval)
+    Wck: int = 0            # u32 words of a row's checkpoint (the residual tape: the state before step cap)
 
 
-def programs(adj, pl, keep=False):
+def programs(adj, pl, keep=False, residual=None):
     """-> TapePrograms of adj (reverse.Adjoint) under pl (reverse.Plan); raises ReverseError when no loop carry
     needs the reverse sweep (the forward-only adjoint applies then).  keep: the count program (which replays the
     whole forward) also returns the forward's own outputs, for value_and_grad in two launches instead of three:
     its tallies keep their kinds and its per-item results are [K, lambda, P cotangents] + [the forward's per-item
-    results, its truncation flag among them]."""
+    results, its truncation flag among them].  residual: True / False forces the residual / state tape (None: the
+    residual tape when its slot is no wider)."""
     if not any(pl.car_act):
         raise ReverseError("internal: the tape adjoint is for programs with an active loop carry")
     prog, sp = adj.prog, pl.sp
@@ -150,6 +245,25 @@ def programs(adj, pl, keep=False):
     P_av = [v.aval for v in sp.pre.outvars[sp.ncar:]]
     disc = [dataclasses.replace(s, kind="discard") for s in prog.tallies]
     I32, F32 = C.I32, C.F32
+    # the step's VJP and PRE's (the broadcast tables read at a traced index in the loop body or PRE: their read
+    # cotangents are emitted where the read's VJP runs; POST's VJP runs in the count program, which has no
+    # cotangent tallies: dense there)
+    sp_pre, sp_body, _ = sparse_tables(adj, sp)
+    info = {}
+    body_vjp, f_ctout, f_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + list(pl.car_act), _ct_reader(ft, S_of),
+                                             {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
+                                             ct_given=list(pl.car_act), sparse=sp_body, prune=True, info=info)
+    for ci, ca in zip(f_ctin[nbc:], pl.car_act):
+        if ci and not ca:
+            raise ReverseError("internal: carry activity mismatch")
+    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)},
+                                            sparse=sp_pre, prune=True)
+    # the residual tape when a slot of residuals is no wider than a slot of state: the reverse step then reads what
+    # the step's VJP needs instead of replaying the step from its state
+    rp = residual_plan(sp, body_vjp, info, nbc)
+    if rp is not None and (residual is False or (residual is None and rp.Wv > Wp)):
+        rp = None
+    Wt, Wck = (rp.Wv, Wp) if rp is not None else (Wp, 0)
 
     # ------------------------------------------------------------------------------------------ count
     tspecs = (list(prog.tallies) if keep else disc) + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
@@ -172,8 +286,12 @@ def programs(adj, pl, keep=False):
 
         def body_f(c):
             cars, k, tok = list(c[0]), c[1], c[2]
-            tok = _put(tok, k, cap, [cars[j] for j in stc], Wp)
-            return (AD.eval_jaxpr(sp.body, bcv + cars), k + 1, tok)
+            if rp is None:
+                tok = _put(tok, k, cap, [cars[j] for j in stc], Wp)
+                return (AD.eval_jaxpr(sp.body, bcv + cars), k + 1, tok)
+            tok = _put(tok, k, cap, [cars[j] for j in stc], Wp, ck=True)     # (the state before step cap)
+            outs, vals = AD.eval_jaxpr(sp.body, bcv + cars, want=[v.id for v in rp.body_vars])
+            return (outs, k + 1, _put(tok, k, cap, rp.pack(vals), Wt))
         tok0 = tin[nT]
         if sp.ncar and not _never(sp):
             cars_f, K_, tok = L.while_loop(cond_f, body_f, (cars0, np.int32(0), tok0))
@@ -220,20 +338,10 @@ def programs(adj, pl, keep=False):
     check_tallies(jx, len(tspecs), adj.where)
     count = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft) + 1, trunc,
                         adj.tag + "-count" + ("-vg" if keep else ""), adj.where)
-    count.tape_words = Wp
+    count.tape_words, count.tape_ck_words = Wt, Wck
+    count.entry = "tm_fused" if keep else "tm_count"
 
     # ----------------------------------------------------------------------------------------- reverse
-    # (the broadcast tables read at a traced index in the loop body or PRE: their read cotangents are emitted where
-    # the read's VJP runs; POST's VJP runs in the count program, which has no cotangent tallies: dense there)
-    sp_pre, sp_body, _ = sparse_tables(adj, sp)
-    body_vjp, f_ctout, f_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + list(pl.car_act), _ct_reader(ft, S_of),
-                                             {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
-                                             ct_given=list(pl.car_act), sparse=sp_body, prune=True)
-    for ci, ca in zip(f_ctin[nbc:], pl.car_act):
-        if ci and not ca:
-            raise ReverseError("internal: carry activity mismatch")
-    pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)},
-                                            sparse=sp_pre, prune=True)
     ct_emit = ct_emitter(adj, len(disc))
     gq = [q for q in range(nbc) if f_ctin[q]]
     tspecs = disc + [TSpec(f"ct{j}", tuple(bav[j].shape) or (1,), np.dtype(np.float32), exact=True)
@@ -269,25 +377,41 @@ def programs(adj, pl, keep=False):
         def rcond(c):
             return c[0] >= 0
 
+        def recompute(j0, j, st, tc):
+            """the state before step j from the state before step j0 (< j): the steps between, replayed."""
+            def step(_, x):
+                o = AD.eval_jaxpr(sp.body, bcv + assemble(list(x[0]), list(x[1])))
+                return [o[q] for q in sc], [o[q] for q in tcj]
+            st, tc = L.fori_loop(0, j - j0, step, (list(st), list(tc)))
+            return list(st), list(tc)
+
         def rbody(c):
             j, lam, gk, tc = c[0], list(c[1]), list(c[2]), list(c[3])
-            jj = L.min(j, cap - 1)
-            got_ = dict(zip(stc, _get(jj, cap, st_av, Wp)))
-            st = [got_[q] if q in got_ else jj + aff[q] for q in sc]
-
-            def recompute(s, t):
-                def step(_, x):
-                    o = AD.eval_jaxpr(sp.body, bcv + assemble(list(x[0]), list(x[1])))
-                    return [o[q] for q in sc], [o[q] for q in tcj]
-                return L.fori_loop(0, j - jj, step, (list(s), list(t)))
-            st, tc = L.cond(j > jj, recompute, lambda s, t: (list(s), list(t)), list(st), tc)
-            st, tc = list(st), list(tc)
             cts = []
             it = iter(lam)
             for jc, m in enumerate(f_ctout):
                 if m:
                     cts.append(next(it) if pl.car_act[jc] else np.zeros(car_av[jc].shape, np.float32)[()])
-            vj = AD.eval_jaxpr(body_vjp, bcv + assemble(st, tc) + cts, ct_read, ct_emit)
+            if rp is None:
+                jj = L.min(j, cap - 1)
+                got_ = dict(zip(stc, _get(jj, cap, st_av, Wp)))
+                st = [got_[q] if q in got_ else jj + aff[q] for q in sc]
+                st, tc = L.cond(j > jj, lambda s, t: recompute(jj, j, s, t), lambda s, t: (list(s), list(t)),
+                                list(st), tc)
+                st, tc = list(st), list(tc)
+                vj = AD.eval_jaxpr(body_vjp, bcv + assemble(st, tc) + cts, ct_read, ct_emit)
+            else:
+                def from_tape(t):
+                    vals = rp.unpack(_get(j, cap, rp.slot_avals(), Wt))
+                    return list(AD.eval_jaxpr(rp.back, bcv + vals + cts, ct_read, ct_emit)), list(t)
+
+                def from_checkpoint(t):       # (a step past the tape: replayed from the state before step cap)
+                    got_ = dict(zip(stc, _get(cap, cap, st_av, Wp, ck=True)))
+                    st = [got_[q] if q in got_ else cap + aff[q] for q in sc]
+                    st, t = recompute(cap, j, st, t)
+                    return list(AD.eval_jaxpr(body_vjp, bcv + assemble(st, t) + cts, ct_read, ct_emit)), list(t)
+                vj, tc = L.cond(j >= cap, from_checkpoint, from_tape, tc)
+                vj, tc = list(vj), list(tc)
             k2, newlam, newgk = 0, {}, []
             for q, m in enumerate(f_ctin):
                 if not m:
@@ -351,5 +475,5 @@ def programs(adj, pl, keep=False):
     nPr = nP + len(fy) + 1 + len(lam_j) + len(gp_q) + (1 if trin is not None else 0)
     rev = ItemProgram(jx, tuple(tspecs), nPr, nB + len(ft) + 1, trunc, adj.tag + "-reverse", adj.where)
     rev.poison_ys = True
-    rev.tape_words = Wp
-    return TapePrograms(count, rev, Wp, lam_j, [(q, P_av[q]) for q in gp_q])
+    rev.tape_words, rev.tape_ck_words = Wt, Wck
+    return TapePrograms(count, rev, Wt, lam_j, [(q, P_av[q]) for q in gp_q], Wck)

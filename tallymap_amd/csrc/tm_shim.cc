@@ -149,7 +149,9 @@ int loaded(long long id, std::shared_ptr<Loaded>* out) {
   auto L = std::make_shared<Loaded>();
   e = g_rt.hipModuleLoadData(&L->mod, pr->second->image.data());
   if (e != hipSuccess) return fail("tallymap_rocm: loading %s on device %d: %s", pr->second->note.c_str(), dev, herr(e));
-  // the item loop: tm_main (a forward program) or tm_adjoint (a replay adjoint); tm_zero / tm_post are optional.
+  // the item loop, named for its role in profiles: tm_main (a forward program), tm_adjoint (a replay adjoint),
+  // tm_count (the tape adjoint's counting pass), tm_fused (an adjoint launch that also returns the forward's
+  // outputs: value_and_grad); tm_zero / tm_post are optional.
   // A lookup that fails leaves the runtime's per-thread last error set, which the caller's framework would later
   // report from an unrelated call: every probe that may fail is followed by hipGetLastError to clear it.
   auto probe = [&](hipFunction_t* f, const char* name) {
@@ -158,8 +160,10 @@ int loaded(long long id, std::shared_ptr<Loaded>* out) {
     (void)g_rt.hipGetLastError();
     return false;
   };
-  if (!probe(&L->main, "tm_main") && !probe(&L->main, "tm_adjoint"))
-    return fail("tallymap_rocm: %s has neither tm_main nor tm_adjoint", pr->second->note.c_str());
+  if (!probe(&L->main, "tm_main") && !probe(&L->main, "tm_adjoint") && !probe(&L->main, "tm_count") &&
+      !probe(&L->main, "tm_fused"))
+    return fail("tallymap_rocm: %s has no item loop (tm_main, tm_adjoint, tm_count or tm_fused)",
+                pr->second->note.c_str());
   probe(&L->zero, "tm_zero");
   probe(&L->post, "tm_post");
   if ((e = g_rt.hipDeviceGetAttribute(&L->cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess ||
@@ -292,7 +296,8 @@ int tm_launch_aux(long long id, const char* name, void* stream, void* const* buf
   if (!g_hip_ok) return fail("tallymap_rocm: tm_init was not called");
   if (!name || n < 1 || block < 64 || block > 1024 || block % 64 || grid < 1 || grid > (1u << 20))
     return fail("tallymap_rocm: bad auxiliary launch");
-  if (!strcmp(name, "tm_main") || !strcmp(name, "tm_zero") || !strcmp(name, "tm_post") || !strcmp(name, "tm_adjoint"))
+  if (!strcmp(name, "tm_main") || !strcmp(name, "tm_zero") || !strcmp(name, "tm_post") || !strcmp(name, "tm_adjoint") ||
+      !strcmp(name, "tm_count") || !strcmp(name, "tm_fused"))
     return fail("tallymap_rocm: %s is launched by tm_launch", name);
   std::shared_ptr<Loaded> L;
   if (loaded(id, &L)) return 1;

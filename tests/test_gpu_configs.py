@@ -63,8 +63,8 @@ def test_c3_slab_transport_parity(oracle, n):
 
 @pytest.mark.parametrize("n", [65_536, 4_194_304])
 def test_c3_grad_mu_a(oracle, n):
-    """d sum(absorbed) / d mu_a: the replay adjoint (the weight is a loop carry) vs forward mode; the one-item-per-lane
-    replay gives bitwise the same exact sum."""
+    """d sum(absorbed) / d mu_a: the replay adjoint (the weight is a loop carry) vs the oracle; the other replay
+    schedules and tapes give bitwise the same exact sum."""
     print(f"case: C3 grad mu_a N={n}", flush=True)
     keys, mu_a = configs.c3_inputs(n)
     g = tm.grad(_mapped(configs.C3), argnums=1)(keys, mu_a)
@@ -73,9 +73,13 @@ def test_c3_grad_mu_a(oracle, n):
     assert ntr == 0
     assert _rel(_np(g), want) <= GTOL, (float(_np(g)), float(want))
     if n == 65_536:
-        gi = tm.grad(_mapped(configs.C3, rev_schedule="item"), argnums=1)(keys, mu_a)
-        _sync()
-        assert np.float32(_np(gi)).view(np.uint32) == np.float32(_np(g)).view(np.uint32)
+        # the one-item-per-lane replay; the state tape instead of the residual one (C3's default: 4 words of what
+        # the step's VJP reads against 8 of state); the residual tape with 4 slots (steps past 4 replayed from the
+        # checkpoint): the same exact sum
+        for opts in (dict(rev_schedule="item"), dict(rev_residual=False), dict(rev_residual=True, rev_tape=4)):
+            gi = tm.grad(_mapped(configs.C3, **opts), argnums=1)(keys, mu_a)
+            _sync()
+            assert np.float32(_np(gi)).view(np.uint32) == np.float32(_np(g)).view(np.uint32), opts
 
 
 # ------------------------------------------------------------------------------------------------- C4

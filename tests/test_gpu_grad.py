@@ -40,20 +40,22 @@ def test_c1_grad_theta(oracle):
 
 
 VARIANTS = [dict(), dict(rev_tape=4), dict(rev_tape=2), dict(rev_tape=1), dict(schedule="item"),
+            dict(rev_residual=True), dict(rev_residual=True, rev_tape=4), dict(rev_residual=True, rev_tape=1),
             dict(rev_schedule="step"), dict(rev_schedule="step", rev_tape=4), dict(rev_schedule="step", rev_tape=2),
             dict(rev_schedule="step", rev_refill=1), dict(rev_schedule="step", rev_refill=64),
             dict(rev_schedule="item"), dict(rev_schedule="item", rev_checkpoints=4),
             dict(rev_schedule="item", rev_checkpoints=1)]
 
 
-@pytest.mark.parametrize("opts", VARIANTS, ids=["tape", "tape4", "tape2", "tape1", "tape-itemsched", "step",
-                                                "step-tape4", "step-tape2", "step-refill1", "step-refill64", "item16",
-                                                "item4", "item1"])
+@pytest.mark.parametrize("opts", VARIANTS, ids=["tape", "tape4", "tape2", "tape1", "tape-itemsched", "resid",
+                                                "resid-tape4", "resid-tape1", "step", "step-tape4", "step-tape2",
+                                                "step-refill1", "step-refill64", "item16", "item4", "item1"])
 def test_c1_grad_xs_and_replay_variants(oracle, opts):
     """cotangents of xs (per item, through the loop state: the replay) and of theta with weights ct, against the
     oracle; the replay variants give bitwise the same per-item cotangents and broadcast cotangent (reference
     tests/reverse.py:216): the two-launch tape adjoint (the default; a 4-, 2- or 1-slot tape makes the ~8-step
-    items recompute the states past the tape inside the reverse step; the item schedule of the forward template),
+    items recompute the states past the tape inside the reverse step; the item schedule of the forward template;
+    the residual tape forced, alone and with 4- and 1-slot tapes whose later steps replay from the checkpoint),
     the single-kernel step-scheduled replay (an item overflowing a 4- or 2-slot tape takes the checkpointed sweep;
     waves refilled by 1 or 64 free lanes) and the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its
     segment re-runs)."""
