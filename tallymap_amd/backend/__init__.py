@@ -502,7 +502,7 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
         tp = _TAPE.get(tkey)
         if tp is None:
             tp = _TAPE[tkey] = T.programs(adj, pl, keep=forward, residual=rres)
-        cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"), tp.Wck)
+        cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"), tp.Wck, tp.block)
         capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
         tape = torch.empty((max(1, N * (cap * tp.Wp + tp.Wck)),), dtype=torch.uint32, device="cuda")
         # count: the loop with its states taped, POST's VJP -> K, lambda, P cotangents, truncation (and with

@@ -85,11 +85,14 @@ def state_words(sp):
     return _pad_words(W)
 
 
-def tape_cap(N, Wp, want=None, Wck=0):
+BLOCK = 4                   # slots per block read of the residual tape's reverse step
+
+
+def tape_cap(N, Wp, want=None, Wck=0, block=1):
     """the tape slots per item at N items (`want`: a caller's choice, clamped to >= 1); a row is cap slots of Wp
-    words and a checkpoint of Wck."""
+    words and a checkpoint of Wck; cap is a multiple of `block` (the block reads stay inside the row)."""
     if want:
-        return max(1, int(want))
+        return -(-max(1, int(want)) // block) * block
     per = (BUDGET // max(1, int(N) * 4) - Wck) // max(1, Wp)
     return int(max(CAP_MIN, min(CAP_MAX, per // 16 * 16)))
 
@@ -131,6 +134,15 @@ class Residuals:
                 w = x if w is None else w | x
             leaves.append(w)
         return leaves
+
+    def from_words(self, ws):
+        """the slot's leaves from its u32 words (a traced u32[Wv]; scalar 32-bit leaves only)."""
+        return [ws[w] if a.dtype == C.U32 else L.bitcast_convert_type(ws[w], a.dtype)
+                for w, a in enumerate(self.slot_avals())]
+
+    def words32(self):
+        """True when every slot leaf is a 32-bit scalar (the block reads rebuild them from u32 words)."""
+        return all(a.dtype.itemsize == 4 and a.shape == () for a in self.slot_avals())
 
     def unpack(self, leaves):
         o, b = self._split()
@@ -215,6 +227,7 @@ class TapePrograms:
     n_lam: list             # per active carry j (in order): its cotangent per-item result of `count`
     n_gp: list              # per P var q with a cotangent from POST: (q, aval)
     Wck: int = 0            # u32 words of a row's checkpoint (the residual tape: the state before step cap)
+    block: int = 1          # slots per block read (the residual tape's reverse reads BLOCK slots at once)
 
 
 def programs(adj, pl, keep=False, residual=None):
@@ -263,7 +276,9 @@ def programs(adj, pl, keep=False, residual=None):
     rp = residual_plan(sp, body_vjp, info, nbc)
     if rp is not None and (residual is False or (residual is None and rp.Wv > Wp)):
         rp = None
-    Wt, Wck = (rp.Wv, Wp) if rp is not None else (Wp, 0)
+    # (the residual row: cap slots, then the checkpoint padded to 64 bytes, so every row and block is 64-byte aligned)
+    Wt, Wck = (rp.Wv, -(-Wp // 16) * 16) if rp is not None else (Wp, 0)
+    blk = rp is not None and rp.words32() and BLOCK * Wt <= 32       # (the block's words as registers)
 
     # ------------------------------------------------------------------------------------------ count
     tspecs = (list(prog.tallies) if keep else disc) + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
@@ -387,6 +402,15 @@ def programs(adj, pl, keep=False, residual=None):
 
         def rbody(c):
             j, lam, gk, tc = c[0], list(c[1]), list(c[2]), list(c[3])
+            if blk:
+                # the block of BLOCK slots holding slot j, read once per BLOCK steps into registers: a lane's
+                # reads of one 64-byte block no longer depend on the block staying in L2 between its steps
+                bj, tb = c[4], c[5]
+                b = j >> 2
+                need = (b != bj) & (j < cap)
+                tb = L.cond(need, lambda t: _get(b * BLOCK, cap, [C.AVal((BLOCK, Wt), C.U32)], BLOCK * Wt)[0],
+                            lambda t: t, tb)
+                bj = L.select(need, b, bj)
             cts = []
             it = iter(lam)
             for jc, m in enumerate(f_ctout):
@@ -402,7 +426,10 @@ def programs(adj, pl, keep=False, residual=None):
                 vj = AD.eval_jaxpr(body_vjp, bcv + assemble(st, tc) + cts, ct_read, ct_emit)
             else:
                 def from_tape(t):
-                    vals = rp.unpack(_get(j, cap, rp.slot_avals(), Wt))
+                    if blk:
+                        vals = rp.unpack(rp.from_words(tb[j & (BLOCK - 1)]))
+                    else:
+                        vals = rp.unpack(_get(j, cap, rp.slot_avals(), Wt))
                     return list(AD.eval_jaxpr(rp.back, bcv + vals + cts, ct_read, ct_emit)), list(t)
 
                 def from_checkpoint(t):       # (a step past the tape: replayed from the state before step cap)
@@ -423,11 +450,16 @@ def programs(adj, pl, keep=False, residual=None):
                 k2 += 1
             lam2 = [newlam.get(jc, np.zeros(car_av[jc].shape, np.float32)[()]) for jc in lam_j]
             gk2 = [g + d for g, d in zip(gk, newgk)]
+            if blk:
+                return j - 1, lam2, gk2, tc, bj, tb
             return j - 1, lam2, gk2, tc
         g0 = [np.zeros(sp.body.invars[q].aval.shape, np.float32)[()] for q in gq]
         tc0 = [cars0[j] for j in tcj]
         if sp.ncar and not _never(sp):
-            _, lam_f, gk_f, tc_f = L.while_loop(rcond, rbody, (kin - 1, list(lamin), g0, tc0))
+            init = (kin - 1, list(lamin), g0, tc0)
+            if blk:
+                init += (np.int32(-1), np.zeros((BLOCK, Wt), np.uint32))
+            _, lam_f, gk_f, tc_f = L.while_loop(rcond, rbody, init)[:4]
         else:
             lam_f, gk_f, tc_f = list(lamin), g0, tc0
         lam_f, gk_f, tc_f = list(lam_f), list(gk_f), list(tc_f)
@@ -476,4 +508,4 @@ def programs(adj, pl, keep=False, residual=None):
     rev = ItemProgram(jx, tuple(tspecs), nPr, nB + len(ft) + 1, trunc, adj.tag + "-reverse", adj.where)
     rev.poison_ys = True
     rev.tape_words, rev.tape_ck_words = Wt, Wck
-    return TapePrograms(count, rev, Wt, lam_j, [(q, P_av[q]) for q in gp_q], Wck)
+    return TapePrograms(count, rev, Wt, lam_j, [(q, P_av[q]) for q in gp_q], Wck, BLOCK if blk else 1)
