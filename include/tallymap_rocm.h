@@ -56,7 +56,7 @@ int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, 
 int tm_launch_aux(long long id, const char* name, void* stream, void* const* bufs, int n, long long n_items,
                   unsigned grid, int block);
 
-/* out[8]: registers per lane of the item loop (tm_main, or tm_adjoint in a replay adjoint), private (scratch) bytes per lane, static LDS bytes per block, achieved
+/* out[8]: registers per lane of the item loop (tm_main, or tm_adjoint / tm_count / tm_fused in an adjoint), private (scratch) bytes per lane, static LDS bytes per block, achieved
  * blocks per CU at `block` threads, resident threads on the device, compute units, max threads per block, and the
  * grid tm_launch uses for 2^31 - 1 items. */
 int tm_kernel_info(long long id, int block, long long out[8]);
