@@ -283,22 +283,22 @@ constexpr double TM_SC_C0 = 0x1p0, TM_SC_C1 = -0x1.ffffffd0c621cp-2, TM_SC_C2 = 
 constexpr double TM_SC_S1 = -0x1.555545995a603p-3, TM_SC_S2 = 0x1.1107605230bc4p-7, TM_SC_S3 = -0x1.994eb3774cf24p-13;
 // the table's sign[n & 3] = {1, -1, -1, 1}: -1 when bits 0 and 1 of n differ
 TM_FN double tm_sc_sign(int n) { return ((n ^ (n >> 1)) & 1) ? -1.0 : 1.0; }
-// n even: the sine polynomial; n odd: the cosine polynomial, negated when `flip` (the second table)
+// n even: the sine polynomial; n odd: the cosine polynomial, negated when `flip` (the second table).  Both are
+// evaluated and one is selected: the lanes of a wave reduce to quadrants of both parities, and a branch would run
+// both sides anyway, each with part of the lanes (each polynomial's operations are glibc's, so the bits are too).
 TM_FN float tm_sc_poly(double x, double x2, int n, bool flip) {
-  if ((n & 1) == 0) {
-    const double x3 = x * x2;
-    const double s1 = __builtin_fma(x2, TM_SC_S3, TM_SC_S2);
-    const double x7 = x3 * x2;
-    const double s = __builtin_fma(x3, TM_SC_S1, x);
-    return (float)__builtin_fma(x7, s1, s);
-  }
+  const double x3 = x * x2;
+  const double s1 = __builtin_fma(x2, TM_SC_S3, TM_SC_S2);
+  const double x7 = x3 * x2;
+  const double s = __builtin_fma(x3, TM_SC_S1, x);
+  const float rs = (float)__builtin_fma(x7, s1, s);
   const double x4 = x2 * x2;
   const double c2 = __builtin_fma(x2, TM_SC_C4, TM_SC_C3);
   const double c1 = __builtin_fma(x2, TM_SC_C1, TM_SC_C0);
   const double x6 = x4 * x2;
   const double c = __builtin_fma(x4, TM_SC_C2, c1);
-  const float r = (float)__builtin_fma(x6, c2, c);
-  return flip ? -r : r;
+  const float rc = (float)__builtin_fma(x6, c2, c);
+  return (n & 1) == 0 ? rs : (flip ? -rc : rc);
 }
 // |x| < 120: n = round(x 2/pi) (through 2^24-scaled integer arithmetic), x - n pi/2 with one fma
 TM_FN double tm_sc_reduce_fast(double x, int* np) {
@@ -328,17 +328,18 @@ TM_FN double tm_sc_reduce_large(u32 xi, int* np) {
   return (double)(i64)res0 * 0x1.921FB54442D18p-62;
 }
 TM_FN u32 tm_abstop12(float x) { return (tm_f2u(x) >> 20) & 0x7ffu; }
+// glibc evaluates |y| < pi/4 without the reduction and returns y itself below 2^-12; there the fast reduction gives
+// n = 0 and r = y exactly, and the same polynomial: one path for every |y| < 120, so the lanes of a wave do not
+// split on |y| < pi/4, with y itself selected below 2^-12 (the polynomial turns -0 into +0).  Bitwise glibc's on
+// all 2^32 inputs.
 TM_FN float tm_sinf(float y) {
   double x = y;
   int n;
-  if (tm_abstop12(y) < tm_abstop12(0x1.921FB6p-1f)) {
-    if (tm_abstop12(y) < tm_abstop12(0x1p-12f)) return y;
-    return tm_sc_poly(x, x * x, 0, false);
-  }
   if (tm_abstop12(y) < tm_abstop12(120.0f)) {
     x = tm_sc_reduce_fast(x, &n);
     const double s = tm_sc_sign(n);
-    return tm_sc_poly(x * s, x * x, n, (n & 2) != 0);
+    const float r = tm_sc_poly(x * s, x * x, n, (n & 2) != 0);
+    return tm_abstop12(y) < tm_abstop12(0x1p-12f) ? y : r;
   }
   if (tm_abstop12(y) < tm_abstop12(__builtin_inff())) {
     const u32 xi = tm_f2u(y);
@@ -349,17 +350,14 @@ TM_FN float tm_sinf(float y) {
   }
   return y - y;
 }
-TM_FN float tm_cosf(float y) {
+TM_FN float tm_cosf(float y) {             // (one path for |y| < 120, as tm_sinf; glibc returns 1 below 2^-12)
   double x = y;
   int n;
-  if (tm_abstop12(y) < tm_abstop12(0x1.921FB6p-1f)) {
-    if (tm_abstop12(y) < tm_abstop12(0x1p-12f)) return 1.0f;
-    return tm_sc_poly(x, x * x, 1, false);
-  }
   if (tm_abstop12(y) < tm_abstop12(120.0f)) {
     x = tm_sc_reduce_fast(x, &n);
     const double s = tm_sc_sign(n);
-    return tm_sc_poly(x * s, x * x, n ^ 1, (n & 2) != 0);
+    const float r = tm_sc_poly(x * s, x * x, n ^ 1, (n & 2) != 0);
+    return tm_abstop12(y) < tm_abstop12(0x1p-12f) ? 1.0f : r;
   }
   if (tm_abstop12(y) < tm_abstop12(__builtin_inff())) {
     const u32 xi = tm_f2u(y);
