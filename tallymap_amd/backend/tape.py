@@ -136,13 +136,12 @@ class Residuals:
         return leaves
 
     def from_words(self, ws):
-        """the slot's leaves from its u32 words (a traced u32[Wv]; scalar 32-bit leaves only)."""
-        return [ws[w] if a.dtype == C.U32 else L.bitcast_convert_type(ws[w], a.dtype)
-                for w, a in enumerate(self.slot_avals())]
+        """the slot's leaves from its u32 words (a traced u32[Wv])."""
+        return _from_words(ws, self.slot_avals())
 
     def words32(self):
-        """True when every slot leaf is a 32-bit scalar (the block reads rebuild them from u32 words)."""
-        return all(a.dtype.itemsize == 4 and a.shape == () for a in self.slot_avals())
+        """True when the block reads can rebuild the slot's leaves from u32 words."""
+        return _words32(self.slot_avals())
 
     def unpack(self, leaves):
         o, b = self._split()
@@ -154,6 +153,22 @@ class Residuals:
             for bit, i in enumerate(b):
                 vals[i] = ((w >> bit) & 1) != 0 if bit else (w & 1) != 0
         return vals
+
+
+def _words32(avals):
+    """True when every leaf is a 32-bit scalar or vector (a slot rebuilt from u32 words by _from_words)."""
+    return all(a.dtype.itemsize == 4 and len(a.shape) <= 1 for a in avals)
+
+
+def _from_words(ws, avals):
+    """leaves of the given avals from consecutive u32 words (a traced u32[W], W >= their words)."""
+    out, w = [], 0
+    for a in avals:
+        n = max(1, a.size)
+        parts = [ws[w + i] if a.dtype == C.U32 else L.bitcast_convert_type(ws[w + i], a.dtype) for i in range(n)]
+        w += n
+        out.append(parts[0] if a.shape == () else C.stack(parts))
+    return out
 
 
 def residual_plan(sp, body_vjp, info, nbc):
@@ -278,7 +293,10 @@ def programs(adj, pl, keep=False, residual=None):
         rp = None
     # (the residual row: cap slots, then the checkpoint padded to 64 bytes, so every row and block is 64-byte aligned)
     Wt, Wck = (rp.Wv, -(-Wp // 16) * 16) if rp is not None else (Wp, 0)
-    blk = rp is not None and rp.words32() and BLOCK * Wt <= 32       # (the block's words as registers)
+    # block reads (BLOCK slots per lane at once, kept in registers) when a slot's leaves are 32-bit scalars or
+    # vectors and the block's words fit: the residual tape's slots, or the state's
+    st_av = [car_av[j] for j in stc]
+    blk = BLOCK * Wt <= 32 and (rp.words32() if rp is not None else _words32(st_av))
 
     # ------------------------------------------------------------------------------------------ count
     tspecs = (list(prog.tallies) if keep else disc) + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
@@ -406,8 +424,9 @@ def programs(adj, pl, keep=False, residual=None):
                 # the block of BLOCK slots holding slot j, read once per BLOCK steps into registers: a lane's
                 # reads of one 64-byte block no longer depend on the block staying in L2 between its steps
                 bj, tb = c[4], c[5]
-                b = j >> 2
-                need = (b != bj) & (j < cap)
+                jb = j if rp is not None else L.min(j, cap - 1)      # (the state tape: slot cap-1 past the tape)
+                b = jb >> 2
+                need = (b != bj) & (j < cap) if rp is not None else (b != bj)
                 tb = L.cond(need, lambda t: _get(b * BLOCK, cap, [C.AVal((BLOCK, Wt), C.U32)], BLOCK * Wt)[0],
                             lambda t: t, tb)
                 bj = L.select(need, b, bj)
@@ -418,7 +437,10 @@ def programs(adj, pl, keep=False, residual=None):
                     cts.append(next(it) if pl.car_act[jc] else np.zeros(car_av[jc].shape, np.float32)[()])
             if rp is None:
                 jj = L.min(j, cap - 1)
-                got_ = dict(zip(stc, _get(jj, cap, st_av, Wp)))
+                if blk:
+                    got_ = dict(zip(stc, _from_words(tb[jj & (BLOCK - 1)], st_av)))
+                else:
+                    got_ = dict(zip(stc, _get(jj, cap, st_av, Wp)))
                 st = [got_[q] if q in got_ else jj + aff[q] for q in sc]
                 st, tc = L.cond(j > jj, lambda s, t: recompute(jj, j, s, t), lambda s, t: (list(s), list(t)),
                                 list(st), tc)
