@@ -160,6 +160,19 @@ def _words32(avals):
     return all(a.dtype.itemsize == 4 and len(a.shape) <= 1 for a in avals)
 
 
+def _to_words(leaves, W):
+    """the u32 words of 32-bit scalar or vector leaves, zero-padded to W (traced u32 scalars)."""
+    out = []
+    for x in leaves:
+        els = [x] if not C.is_traced(x) or x.shape == () else [x[i] for i in range(x.shape[0])]
+        for e in els:
+            if not C.is_traced(e):
+                e = C.Tracer(C.bind("copy", [C.literal(np.asarray(e))], [C.literal(np.asarray(e)).aval.strong()])[0].var)
+            out.append(e if e.dtype == C.U32 else L.bitcast_convert_type(e, C.U32))
+    zero = C.Tracer(C.bind("copy", [C.literal(0, C.U32, False)], [C.AVal((), C.U32)])[0].var) if len(out) < W else None
+    return out + [zero] * (W - len(out))
+
+
 def _from_words(ws, avals):
     """leaves of the given avals from consecutive u32 words (a traced u32[W], W >= their words)."""
     out, w = [], 0
@@ -320,14 +333,30 @@ def programs(adj, pl, keep=False, residual=None):
         def body_f(c):
             cars, k, tok = list(c[0]), c[1], c[2]
             if rp is None:
-                tok = _put(tok, k, cap, [cars[j] for j in stc], Wp)
-                return (AD.eval_jaxpr(sp.body, bcv + cars), k + 1, tok)
-            tok = _put(tok, k, cap, [cars[j] for j in stc], Wp, ck=True)     # (the state before step cap)
-            outs, vals = AD.eval_jaxpr(sp.body, bcv + cars, want=[v.id for v in rp.body_vars])
-            return (outs, k + 1, _put(tok, k, cap, rp.pack(vals), Wt))
+                leaves = [cars[j] for j in stc]
+                outs = AD.eval_jaxpr(sp.body, bcv + cars)
+            else:
+                tok = _put(tok, k, cap, [cars[j] for j in stc], Wp, ck=True)     # (the state before step cap)
+                outs, vals = AD.eval_jaxpr(sp.body, bcv + cars, want=[v.id for v in rp.body_vars])
+                leaves = rp.pack(vals)
+            if not blk:
+                return (outs, k + 1, _put(tok, k, cap, leaves, Wt))
+            # the slot goes into row k mod BLOCK of the lane's block buffer; a full block is stored at once (64 or
+            # 96 bytes), so a lane's tape stores complete their lines instead of landing as partial-line writes
+            ws = _to_words(leaves, Wt)
+            wb, r = c[3], k & (BLOCK - 1)
+            wb = C.stack([C.stack([L.select(r == q, ws[w], wb[q][w]) for w in range(Wt)]) for q in range(BLOCK)])
+            tok = L.cond(r == BLOCK - 1, lambda t: _put(t, k - (BLOCK - 1), cap, [wb], BLOCK * Wt), lambda t: t, tok)
+            return (outs, k + 1, tok, wb)
         tok0 = tin[nT]
         if sp.ncar and not _never(sp):
-            cars_f, K_, tok = L.while_loop(cond_f, body_f, (cars0, np.int32(0), tok0))
+            init = (cars0, np.int32(0), tok0) + ((np.zeros((BLOCK, Wt), np.uint32),) if blk else ())
+            fin = L.while_loop(cond_f, body_f, init)
+            cars_f, K_, tok = fin[0], fin[1], fin[2]
+            if blk:                  # the last, partial block
+                wbf = fin[3]
+                tok = L.cond((K_ & (BLOCK - 1)) != 0,
+                             lambda t: _put(t, K_ - (K_ & (BLOCK - 1)), cap, [wbf], BLOCK * Wt), lambda t: t, tok)
         else:
             cars_f, K_, tok = cars0, C.Tracer(C.bind("copy", [C.literal(0, I32, False)], [C.AVal((), I32)])[0].var), tok0
         cars_f = list(cars_f)
