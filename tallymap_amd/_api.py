@@ -160,10 +160,16 @@ class ItemProgram:
         return [v.aval for v in self.jaxpr.outvars[self.nT:]]
 
     def p_avals(self):
-        return [v.aval for v in self.jaxpr.invars[self.nT:self.nT + self.nP]]
+        a = self.__dict__.get("_pav")
+        if a is None:
+            a = self.__dict__["_pav"] = [v.aval for v in self.jaxpr.invars[self.nT:self.nT + self.nP]]
+        return a
 
     def b_avals(self):
-        return [v.aval for v in self.jaxpr.invars[self.nT + self.nP:]]
+        a = self.__dict__.get("_bav")
+        if a is None:
+            a = self.__dict__["_bav"] = [v.aval for v in self.jaxpr.invars[self.nT + self.nP:]]
+        return a
 
     @property
     def out_tallies(self):
@@ -297,18 +303,27 @@ def digest(jx, tallies=(), extra=()):
 _PROGS = collections.OrderedDict()
 
 
+_NPDT = {}
+
+
 def _np_dtype(x):
-    try:
-        import torch
-        if isinstance(x, torch.Tensor):
-            return np.dtype(str(x.dtype).replace("torch.", "").replace("bool", "bool_"))
-    except ImportError:
-        pass
-    return np.asarray(x).dtype if not hasattr(x, "dtype") else np.dtype(x.dtype)
+    dt = getattr(x, "dtype", None)
+    if dt is None:
+        return np.asarray(x).dtype
+    hit = _NPDT.get(dt)
+    if hit is None:
+        name = str(dt)
+        hit = np.dtype(name.replace("torch.", "").replace("bool", "bool_")) if name.startswith("torch.") \
+            else np.dtype(dt)
+        _NPDT[dt] = hit
+    return hit
 
 
 def _shape(x):
-    return tuple(int(s) for s in x.shape) if hasattr(x, "shape") else np.shape(x)
+    sh = getattr(x, "shape", None)
+    if sh is None:
+        return np.shape(x)
+    return sh if type(sh) is tuple else tuple(int(s) for s in sh)
 
 
 def item_name(fn):
@@ -640,6 +655,8 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
     outs_spec = {k: (v if isinstance(v, (Sum, Records)) else Sum(v)) for k, v in outputs.items()}
     names = sorted(outs_spec)
 
+    spec_key = tuple(sorted((n, repr(v)) for n, v in outs_spec.items()))     # (the program cache key's outputs)
+
     def prepare(args, spawn_mode=None):
         axes = in_axes if isinstance(in_axes, (tuple, list)) else (in_axes,) * len(args)
         if len(axes) != len(args) or any(a not in (0, None) for a in axes):
@@ -658,8 +675,7 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
             raise ValueError(f"tallymap: N={N} items exceeds 2^31-1; split the call")
         pav = [C.AVal(_shape(x)[1:], _np_dtype(x)) for x in pi]
         bav = [C.AVal(_shape(x), _np_dtype(x)) for x in bc]
-        key = (tuple(pav), tuple(bav), tuple(axes), str(ptree), str(btree), max_steps,
-               tuple(sorted((n, repr(v)) for n, v in outs_spec.items())), spawn, spawn_mode)
+        key = (tuple(pav), tuple(bav), tuple(axes), repr(ptree), repr(btree), max_steps, spec_key, spawn, spawn_mode)
         hit = _PROGS.get((id(fn), key))
         if hit is not None and hit[0] is fn:
             _PROGS.move_to_end((id(fn), key))

@@ -41,20 +41,33 @@ class Outputs:
     rcount: list = None    # per Records output: records appended (int64 scalar tensor)
 
 
+_TDT = {}
+_GPU = []                   # [True] once a GPU was seen (the check runs until then)
+
+
 def torch_dtype(dt):
-    import torch
-    return {"float32": torch.float32, "float64": torch.float64, "int32": torch.int32, "uint32": torch.uint32,
-            "int64": torch.int64, "uint64": torch.uint64, "bool": torch.bool, "uint8": torch.uint8}[np.dtype(dt).name]
+    t = _TDT.get(dt)
+    if t is None:
+        import torch
+        t = {"float32": torch.float32, "float64": torch.float64, "int32": torch.int32, "uint32": torch.uint32,
+             "int64": torch.int64, "uint64": torch.uint64, "bool": torch.bool,
+             "uint8": torch.uint8}[np.dtype(dt).name]
+        _TDT[dt] = t
+    return t
 
 
 def device_tensor(x, dtype):
     """x as a contiguous tensor of `dtype` on the current GPU (a numpy array or scalar is copied there)."""
     import torch
     td = torch_dtype(dtype)
-    if not torch.cuda.is_available():
-        raise Cm.BackendError("tallymap_amd: no GPU is visible (torch.cuda.is_available() is False); the HIP backend "
-                              "has no CPU fallback")
+    if not _GPU:
+        if not torch.cuda.is_available():
+            raise Cm.BackendError("tallymap_amd: no GPU is visible (torch.cuda.is_available() is False); the HIP "
+                                  "backend has no CPU fallback")
+        _GPU.append(True)
     if isinstance(x, torch.Tensor):
+        if x.is_cuda and x.dtype == td and x.is_contiguous():
+            return x
         if x.device.type != "cuda":
             x = x.to("cuda")
         if x.dtype != td:
@@ -97,16 +110,35 @@ def launch(c, ins, N, stream=None, tape=None):
     return outs
 
 
+_SPECS = {}                 # (kernel id, N) -> the result tensors' (shape, torch dtype), None for the tape
+
+
 def _alloc(c, N, tape=None):
     """c's result tensors for a launch over N items (uninitialised: tm_zero clears what must start at zero)."""
     import torch
+    specs = _SPECS.get((c.id, N))
+    if specs is None:
+        specs = _alloc_specs(c, N)
+        if len(_SPECS) > 4096:
+            _SPECS.clear()
+        _SPECS[(c.id, N)] = specs
+    outs = []
+    for sp in specs:
+        if sp is None:
+            if tape is None:
+                raise ValueError("tallymap_amd: a tape program launched without its tape buffer")
+            outs.append(tape)
+        else:
+            outs.append(torch.empty(sp[0], dtype=sp[1], device="cuda"))
+    return outs
+
+
+def _alloc_specs(c, N):
     L = c.layout
     outs = []
     for shape, dt, per_item in L.res:
         if per_item == ("itape",):
-            if tape is None:
-                raise ValueError("tallymap_amd: a tape program launched without its tape buffer")
-            outs.append(tape)
+            outs.append(None)
             continue
         if per_item == "tape":          # per launched lane (the launcher's persistent grid at this N)
             sh = (_lanes(c, N),) + tuple(shape)
@@ -119,7 +151,7 @@ def _alloc(c, N, tape=None):
             sh = (1 + 2 * (_lanes(c, N) // 64),)
         else:
             sh = ((N,) + tuple(shape)) if per_item else tuple(shape)
-        outs.append(torch.empty(sh, dtype=torch_dtype(dt), device="cuda"))
+        outs.append((sh, torch_dtype(dt)))
     return outs
 
 
