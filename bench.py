@@ -41,9 +41,9 @@ GRAD_BYTES_PER_ITEM = 13
 # c2_random_walk_traffic.md); valu_insts: wave64 VALU instructions (SQ_INSTS_VALU, profiles/
 # c2_random_walk_sq_counters.md).  A kernel whose key differs from the one measured reports null with the reason,
 # so a changed kernel never carries a stale counter.
-MEASURED = {"fused": {"code": "758555b7542d3bf6", "traffic": 76_461_455, "valu_insts": 7.0263e9},
-            "forward": {"code": "3af69f29ed86161a", "traffic": 77_249_529, "valu_insts": 7.0265e9},
-            "gradient": {"code": "219306933a578bce", "traffic": 56_476_024, "valu_insts": 6.7205e9}}
+MEASURED = {"fused": {"code": "73639312187f5055", "traffic": 76_491_312, "valu_insts": 7.0269e9},
+            "forward": {"code": "d7584779552f8ac6", "traffic": 77_243_849, "valu_insts": 7.0288e9},
+            "gradient": {"code": "d8efcabe853d96db", "traffic": 56_446_088, "valu_insts": 6.7209e9}}
 # MI355X's VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per 4 cycles on a 16-lane SIMD, at the
 # 2.4 GHz peak engine clock
 VALU_PEAK = 1024 * 2.4e9 / 4
