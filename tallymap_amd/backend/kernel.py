@@ -29,6 +29,7 @@ from .codegen import Emitter, Val, VTally, assign_carries, ctype, lit
 
 BLOCK = 256
 LDS_BYTES = 32768          # privatised tallies per block (MI355X: 160 KB LDS per CU)
+REG_BINS = 2               # privatised tallies of at most this many bins accumulate in each lane's registers
 XW = 5                     # int64 words per exact bin
 CHUNK = 64
 RESERVE = 4                # chunks a wave reserves per claim while far from the end (short items)
@@ -322,8 +323,14 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             budget -= nbytes
             priv.append(k)
 
+    # the smallest privatised tallies (a wall tally's bins, say) accumulate in each lane's registers, one register
+    # per bin, merged into the workgroup's copy once when the lane exits: no LDS atomic per emit.  (An exact tally
+    # would take ten registers per bin in every lane: measured slower on C5's reverse launch, so it stays in LDS.)
+    rpriv = [k for k in priv if prog.tallies[k].S <= REG_BINS and not prog.tallies[k].fixed
+             and not prog.tallies[k].exact and prog.tallies[k].dtype in (C.F32, C.I32, C.U32)]
     em = Emitter()
     counts = {}                 # (tally slot, f32 bits of a constant emitted value) -> (LDS u64 counter array, value)
+    rcounts = {}                # the same, for a lane-register tally: -> (the lane's u32 counter names per bin, value)
 
     def emit_rule(em_, e, ins):
         t, idx, val = ins
@@ -338,6 +345,26 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         em_.ind += 1
         v = val.el[0]
         lv = e.invars[2]
+        if k in rpriv:
+            bins = range(s.S)
+            if (s.dtype == C.F32 and not s.exact and isinstance(lv, C.Lit) and np.isfinite(float(lv.val))
+                    and float(lv.val) != 0.0):
+                c = np.float32(lv.val)
+                key = (k, int(c.view(np.uint32)))
+                if key not in rcounts:
+                    rcounts[key] = ([f"tm_rn{k}_{len(rcounts)}_{b}" for b in bins], c)
+                names = rcounts[key][0]
+                em_.line(" else ".join(f"if ({ei} == {b}) ++{names[b]};" if b < s.S - 1 else f"++{names[b]};"
+                                       for b in bins))
+            elif s.exact:
+                em_.line(" else ".join((f"if ({ei} == {b}) " if b < s.S - 1 else "")
+                                       + f"{{ if (tm_xemit_lane(tm_xr{k}_{b}, {v})) tm_xrf{k}_{b} = true; }}"
+                                       for b in bins))
+            else:
+                em_.line(" else ".join((f"if ({ei} == {b}) " if b < s.S - 1 else "") + f"tm_r{k}_{b} += {v};"
+                                       for b in bins))
+            em_.close()
+            return t
         if (k in priv and s.dtype == C.F32 and not s.exact and isinstance(lv, C.Lit)
                 and np.isfinite(float(lv.val)) and float(lv.val) != 0.0):
             # a constant f32 emit into a privatised tally: count it (integer LDS atomics run far faster than f32
@@ -866,6 +893,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append("  i32 tm_drop = 0;")
     body.append("  u32 tm_ntr = 0;")
     body += decls
+    body.append("//TM_LANE_DECLS")
     if compact_on:
         body.append("  u32* const tm_pool = tm_lds;                  // the repack pool, one column per word")
         body.append("  __shared__ u32 tm_pn[2];                 // pool counts, alternating between rounds")
@@ -1014,6 +1042,31 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         body.append(f"    if (tm_w == 0) {fin}[0] = (u64)gridDim.x * {w};")
         body.append("  }")
     body.append("  if (tm_ntr) atomicAdd(&TM_CTL[2], tm_ntr);")
+    ldecl = []
+    for k in rpriv:             # each lane's register copy into the workgroup's (LDS) one
+        s = prog.tallies[k]
+        ct = ctype(s.dtype)
+        for b in range(s.S):
+            if s.exact:
+                ldecl.append(f"  u64 tm_xr{k}_{b}[{XW}] = {{{', '.join(['0ull'] * XW)}}};")
+                ldecl.append(f"  bool tm_xrf{k}_{b} = false;")
+                body.append(f"  for (int w = 0; w < {XW}; ++w) {{ const i64 x = (i64)tm_xr{k}_{b}[w]; "
+                            f"if (x != 0 && tm_xadd(&tm_xsh{k}[{b * XW}], w, x)) tm_xrf{k}_{b} = true; }}")
+                body.append(f"  if (tm_xrf{k}_{b}) atomicOr(&tm_xfl{k}[{b >> 5}], {1 << (b & 31)}u);")
+            elif s.dtype == C.F32:
+                ldecl.append(f"  float tm_r{k}_{b} = 0.0f;")
+                body.append(f"  if (tm_r{k}_{b} != 0.0f) tm_ladd_f32(&tm_sh{k}[{b}], tm_r{k}_{b});")
+            else:
+                ldecl.append(f"  {ct} tm_r{k}_{b} = 0;")
+                body.append(f"  if (tm_r{k}_{b} != 0) atomicAdd(&tm_sh{k}[{b}], tm_r{k}_{b});")
+    for (k, cbits), (names, c) in rcounts.items():
+        key = (k, cbits)
+        if key not in counts:          # (the workgroup's counters of this constant: the lanes' counts land there)
+            counts[key] = (f"tm_cn{k}_{len(counts)}", c)
+        for b, nm in enumerate(names):
+            ldecl.append(f"  u32 {nm} = 0u;")
+            body.append(f"  if ({nm} != 0u) atomicAdd(&{counts[key][0]}[{b}], (u64){nm});")
+    body[body.index("//TM_LANE_DECLS")] = "\n".join(ldecl)
     if priv:
         body.append("  __syncthreads();")
         for k in priv:

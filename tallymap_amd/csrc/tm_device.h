@@ -376,6 +376,15 @@ struct TmAtomicAdd64 {
 };
 TM_DFN bool tm_xadd(u64* a, int j, i64 q) { return tm_xadd_with(a, j, q, TmAtomicAdd64()); }
 TM_DFN bool tm_xemit(u64* a, float v) { return tm_xemit_with(a, v, TmAtomicAdd64()); }
+// a lane's own exact accumulator (the words in registers: a tally of one bin privatised per lane)
+struct TmLaneAdd64 {
+  __device__ i64 operator()(u64* a, int j, i64 q) const {
+    const i64 o = (i64)a[j];
+    a[j] = (u64)(o + q);
+    return o;
+  }
+};
+TM_DFN bool tm_xemit_lane(u64* a, float v) { return tm_xemit_with(a, v, TmLaneAdd64()); }
 #endif  // device only
 
 // the readout: sum_j word_j 2^(63 j) as a 384-bit two's-complement integer, its magnitude rounded once to f32
