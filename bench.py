@@ -271,8 +271,9 @@ def _shower_particle(t, p, theta):
 
 def bench_spawn(steps, warmup):
     """spawn throughput: the shower from 1,048,576 roots (about 67M particles in 7 generations, Queue 2^25): one
-    call is a launch per generation with a device-to-host read of the ticket count between them; timed with HIP
-    events on torch's current stream around the whole call (the host's generation loop included).  Then the tree
+    call is a launch per generation, each sized on the device from the previous one's tickets (the host reads the
+    next generation's size after each to know when the tree ends); timed with HIP events on torch's current stream
+    around the whole call (the host's generation loop included).  Then the tree
     adjoint's gradient w.r.t. theta, timed the same way (recording forward + one adjoint launch per generation)."""
     import torch
 

@@ -44,7 +44,10 @@ int tm_register(long long id, const void* image, size_t n, const char* note);
 /* Launch program `id` on `stream` (a hipStream_t; NULL: the null stream) over n_items items.  bufs: the n buffer
  * pointers in the program's layout ([per-item operands][broadcast operands][results]).  n_zero > 0: run tm_zero
  * first (it clears the program's accumulators and counters); flags bit 1: run tm_post after tm_main (exact
- * readout, truncation poison).  block: threads per block of tm_main (the program's compiled block size).
+ * readout, truncation poison); flags bit 2 (value 4, spawning programs only, without tm_zero and tm_post): a later
+ * generation of a spawn tree, whose item count tm_main reads from the program's control words (written by
+ * tm_qnext after the previous generation), n_items its upper bound (the queue capacity), which sizes the grid.
+ * block: threads per block of tm_main (the program's compiled block size).
  * Asynchronous: nothing waits for the kernels. */
 int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, int flags, long long n_items,
               int block);
@@ -52,7 +55,10 @@ int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, 
 /* Launch the auxiliary entry `name` of program `id` (grid x block threads, the same buffer list and n_items as
  * tm_launch): the passes that move a Records output's raw records to their canonical slots after tm_launch
  * (tm_rscan<j>, tm_rtop<j>, tm_rcanon<j>).  Replaces the reference's canonicalisation after each one-pass launch,
- * done there in XLA ops (_records.py:45-74, canon).  Asynchronous like tm_launch. */
+ * done there in XLA ops (_records.py:45-74, canon).  A spawning program's tm_qnext (grid 1, n_items 1 after the
+ * roots' launch, else 0) turns a generation's ticket count into the next generation's item count, so the
+ * generations of a tree queue back to back without a host read (the reference runs them inside one launch through
+ * its ticket ring, backends/kernel/kernel.py:1006-1040).  Asynchronous like tm_launch. */
 int tm_launch_aux(long long id, const char* name, void* stream, void* const* bufs, int n, long long n_items,
                   unsigned grid, int block);
 

@@ -24,7 +24,7 @@ MAX_ITEMS = 2 ** 31 - 1
 SUM_DTYPES = (C.F32, C.F64, C.I32, C.U32, C.I64, C.U64)
 PROG_CACHE = 64
 OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact", "rev_schedule",
-        "rev_tape", "rev_refill", "rev_residual")
+        "rev_tape", "rev_refill", "rev_residual", "post_batch")
 
 
 class UnsupportedError(NotImplementedError):

@@ -429,6 +429,8 @@ def conv(x, f, t):
         if fn is None:
             raise CodegenError(f"conversion {f} -> {t} is not supported")
         return f"{fn}({x})"
+    if t == "float" and f in ("i64", "u64"):
+        return f"tm_{f[0]}64f({x})"
     return f"(({t})({x}))"
 
 

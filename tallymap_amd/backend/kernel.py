@@ -26,6 +26,7 @@ import numpy as np
 
 from .. import _core as C
 from .codegen import Emitter, Val, VTally, assign_carries, ctype, lit
+from . import simplify
 
 BLOCK = 256
 LDS_BYTES = 32768          # privatised tallies per block (MI355X: 160 KB LDS per CU)
@@ -35,7 +36,11 @@ CHUNK = 64
 RESERVE = 4                # chunks a wave reserves per claim while far from the end (short items)
 CLAIM_NS = 50              # reserve when a chunk lasted less than this many ns per resident wave (claims from every
                            # wave at that pace would take a quarter of the counter's ~83M claims/s)
-COMPACT = 16               # iterations between the tail-phase repacks of a workgroup's live items                 # items per wave claim
+COMPACT = 16               # iterations between the tail-phase repacks of a workgroup's live items
+POST_BATCH = 1.0           # finished items wait for their POST until the wave's waiting lane-iterations reach this
+                           # many times the (POST + refill) / step cost ratio x 64 (0: each item's POST at once) ...
+POST_BATCH_MIN = 24        # ... when that wait is at least this long: below it the wave's per-step bookkeeping costs
+                           # more than the shared passes save (C2's 11: 2.5 % slower; C4's 37-42: 16-20 % faster)
 BCAST_REG = 16             # broadcast operands up to this many elements are loaded into registers
 
 
@@ -93,6 +98,36 @@ def _free_vars(jx):
         for o in e.outvars:
             defined.add(o.id)
     return free
+
+
+_HEAVY = {"exp", "log", "sin", "cos", "tan", "atan", "atan2", "asin", "acos", "sinh", "cosh", "tanh", "asinh", "acosh",
+          "atanh", "log1p", "expm1", "exp2", "log2", "pow", "erf", "erfc", "erf_inv", "lgamma", "cbrt", "logistic"}
+_FREE = {"slice", "squeeze", "reshape", "broadcast_in_dim", "concatenate", "copy", "stop_gradient"}
+
+
+def cost(eqns, loop=4):
+    """a rough count of the VALU instructions one evaluation of `eqns` issues (static weights: a libm call 30, the
+    threefry2x32 hash 72 per pair, a division or square root 8, an effect 6, other element operations 1; a nested
+    loop counts `loop` trips).  It sets how long finished items wait for their POST (build's post_batch)."""
+    c = 0
+    for e in eqns:
+        n = max([1] + [max(1, o.aval.size) for o in e.outvars])
+        p = e.prim
+        if p == "while":
+            c += loop * (cost(e.params["cond_jaxpr"].eqns, loop) + cost(e.params["body_jaxpr"].eqns, loop))
+        elif p == "cond":
+            c += 2 + max(cost(b.eqns, loop) for b in e.params["branches"])
+        elif p in _HEAVY:
+            c += 30 * n
+        elif p == "threefry2x32":
+            c += 72 * n
+        elif p in ("div", "rem", "sqrt", "rsqrt"):
+            c += 8 * n
+        elif p.startswith("tallymap_"):
+            c += 6
+        elif p not in _FREE:
+            c += n
+    return c
 
 
 def _records_passes(ri, r_rctr, r_out, r_cnt, r_rex, r_rbs, prog, bad):
@@ -242,15 +277,22 @@ def _repack_code(decls, cap):
     return pack, unpack, w
 
 
-def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COMPACT, min_blocks=0):
+def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COMPACT, min_blocks=0,
+          post_batch=POST_BATCH):
     """-> (HIP source, Layout) of prog's module.  chunk: items a wave claims with one atomic (their per-item operands
     are staged in LDS by one coalesced load, and idle lanes take them from there at step granularity).  compact:
     once every wave of a workgroup has drained the item queue, the waves meet every `compact` iterations and
     repack their live items densely onto the first waves (0: off; step schedule only).  min_blocks: workgroups per
-    CU the compiler must leave registers for (as waves per SIMD in __launch_bounds__; 0: its own choice)."""
+    CU the compiler must leave registers for (as waves per SIMD in __launch_bounds__; 0: its own choice).
+    post_batch (step schedule): an item whose loop condition fails waits, its lane idle, until the wave's waiting
+    lane-iterations reach post_batch x 64 x (the POST's + a refill's cost) / (a step's cost), and then every
+    waiting lane runs its POST at once and is refilled together: lanes that finish at different steps then
+    share one pass through POST and the refill, where each finishing step cost the whole wave both.  With the
+    queue drained, waiting items run their POST in the step they finish (0, or a wait below POST_BATCH_MIN:
+    always so)."""
     chunk = max(1, int(chunk))
     compact = max(0, int(compact))
-    jx = prog.jaxpr
+    jx = simplify.cse(prog.jaxpr, _split(prog.jaxpr))
     nT, nP, nB = prog.nT, prog.nP, prog.nB
     pav, bav = prog.p_avals(), prog.b_avals()
     yav = prog.y_avals()
@@ -284,7 +326,9 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                              fin=None))
     Q = getattr(prog, "spawn", None)
     # ctl: the item claim counter (words 0-1), truncations (word 2); a spawning program's ticket counter sits at
-    # words 32-33, on its own 128-byte line (two counters that every wave hits serialise on a shared line)
+    # words 32-33, on its own 128-byte line (two counters that every wave hits serialise on a shared line), and
+    # tm_qnext's generation state after it: the next generation's item count (words 40-41), children spawned and
+    # dropped so far (42-43, 44-45), the roots' truncations (word 48)
     n_ctl = 64 if Q is not None else 8
     r_ctl = result((n_ctl,), np.uint32)
     r_stats = result((5,), np.int32)
@@ -635,7 +679,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                        a.shape, a.dtype)
         return Val([f"(({'const ' + ct}*)P.p[{i}])[tm_item * {n} + {e}]" for e in range(n)], a.shape, a.dtype)
 
-    decls, pre_lines, step_lines = [], [], []
+    decls, pre_lines, step_lines, post_lines = [], [], [], []
+    pb_h = 0
 
     def write_ys(vals, trunc_idx):
         lines = []
@@ -721,6 +766,12 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
             if isinstance(x, VTally):
                 return x
             raise RuntimeError("internal: a loop operand is neither state nor broadcast")
+        # the wait before POST, in lane-iterations (0: each item's POST in the step its condition fails)
+        step_c = cost(we.params["cond_jaxpr"].eqns) + cost(we.params["body_jaxpr"].eqns)
+        fin_c = cost(post_e) + cost(pre_e) + W + 16 + 2 * len(yav)
+        pb_h = int(round(float(post_batch or 0) * 64 * fin_c / max(1, step_c)))
+        if pb_h < POST_BATCH_MIN:
+            pb_h = 0
         # ---- one step: cond; body or post
         em.lines, em.ind = [], 3
         pr = em.run(we.params["cond_jaxpr"], [sval(v) for v in cc_v] + cars)[0]
@@ -729,6 +780,12 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         assign_carries(em, cars, bouts)
         em.close("} else {")
         em.ind += 1
+        if pb_h:
+            em.line("tm_live = false;")
+            em.line("tm_pend = true;")
+            em.close()
+            step_lines = em.lines
+            em.lines, em.ind = [], 6
         penv = {}
         for v in jx.invars[:nT]:
             penv[v.id] = env[v.id]
@@ -745,9 +802,12 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         outv = [em.value_of(penv, v) for v in jx.outvars]
         for ln in write_ys(outv[nT:], prog.trunc):
             em.line(ln)
-        em.line("tm_live = false;")
-        em.close()
-        step_lines = em.lines
+        if pb_h:
+            post_lines = em.lines
+        else:
+            em.line("tm_live = false;")
+            em.close()
+            step_lines = em.lines
 
     # ------------------------------------------------------------------------------------ assemble
     from . import compile as Cm
@@ -791,7 +851,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     bad = ["TM_CTL[2] != 0u"] if prog.trunc is not None else []
     # a Records output past its capacity poisons every float output of the call (reference _api.py:120-131)
     bad += [f"((const u64*)P.p[{r_rctr}])[{2 * ri['ctr'] + 1}] > {ri['capacity']}ull" for ri in rec_info]
-    if Q is not None:          # a dropped child (set by the host from the generations' ticket counts)
+    if Q is not None:          # a dropped child (tm_qnext counts them from the generations' tickets)
         bad.append("TM_STATS[1] != 0")
     if bad and poison:
         # (the readout and the poison visit a bin from the same thread, in program order)
@@ -817,6 +877,22 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         src.append("extern \"C\" __global__ void tm_post(const TmParams P, const i64 n_items) {\n"
                    "  const i64 g = (i64)blockIdx.x * blockDim.x + threadIdx.x, st = (i64)gridDim.x * blockDim.x;\n  "
                    + "\n  ".join(post) + "\n}")
+    if Q is not None:
+        # tm_qnext, one thread between two generations: the next generation's item count min(tickets, Q), the
+        # spawned / dropped totals and the stats they give (children_truncated: truncations past the roots'), and
+        # the claim and ticket counters cleared.  `first` (after the roots' launch) keeps the roots' truncations.
+        big = 2 ** 31 - 1
+        src.append("extern \"C\" __global__ void tm_qnext(const TmParams P, const i64 first) {\n"
+                   "  if (blockIdx.x != 0 || threadIdx.x != 0) return;\n"
+                   f"  u64* const c = (u64*)P.p[{r_ctl}];\n"
+                   f"  const u64 cnt = c[16], n = cnt < {Q}ull ? cnt : {Q}ull;\n"
+                   "  if (first) TM_CTL[48] = TM_CTL[2];\n"
+                   "  const u64 sp = c[21] + n, dr = c[22] + (cnt - n);\n"
+                   "  c[20] = n; c[21] = sp; c[22] = dr; c[0] = 0ull; c[16] = 0ull;\n"
+                   f"  TM_STATS[0] = (i32)(sp < {big}ull ? sp : {big}ull);\n"
+                   f"  TM_STATS[1] = (i32)(dr < {big}ull ? dr : {big}ull);\n"
+                   "  TM_STATS[2] = (i32)(TM_CTL[2] - TM_CTL[48]);\n"
+                   "}")
 
     # tm_main
     body = []
@@ -827,8 +903,10 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
                                              else "tm_main")
     lb = f"{block}, {max(1, int(min_blocks) * block // 256)}" if min_blocks else f"{block}"
     body.append(f"extern \"C\" __global__ void __launch_bounds__({lb}) {entry}(const TmParams P, "
-                "const i64 n_items) {")
+                f"const i64 {'tm_n_arg' if Q is not None else 'n_items'}) {{")
     body.append("  u64* const tm_ctr = (u64*)P.p[%d];" % r_ctl)
+    if Q is not None:          # a later generation (tm_n_arg < 0) takes its item count from tm_qnext's word
+        body.append(f"  const i64 n_items = tm_n_arg >= 0 ? tm_n_arg : (i64)(tm_ctr[20] < {Q}ull ? tm_ctr[20] : {Q}ull);")
     for ri in rec_info:        # each wave's Records batch state (tm_rclaim) and the raw buffers' length
         j, w = ri["ctr"], block // 64
         body.append(f"  __shared__ u64 tm_rbase{j}[{w}], tm_rcnt{j}[{w}];")
@@ -892,6 +970,9 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append("  u32 tm_rc = 1u;                            // chunks in the wave's last reservation")
     body.append("  i32 tm_drop = 0;")
     body.append("  u32 tm_ntr = 0;")
+    if pb_h:
+        body.append("  bool tm_pend = false;                      // the item's condition failed, its POST waits")
+        body.append("  u32 tm_acc = 0;                            // the wave's waiting lane-iterations")
     body += decls
     body.append("//TM_LANE_DECLS")
     if compact_on:
@@ -904,7 +985,8 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
         body.append("  u32 tm_it = 0, tm_round = 0;")
     body.append("  while (true) {")
     body.append("    if (tm_more) {")
-    body.append("      const u64 tm_need = tm_ballot(!tm_live);")
+    free_ = "(!tm_live && !tm_pend)" if pb_h else "!tm_live"
+    body.append(f"      const u64 tm_need = tm_ballot({free_});")
     if mode == "step" and refill > 1:
         body.append(f"      if (tm_need != 0ull && (__builtin_popcountll(tm_need) >= {int(refill)} || "
                     "tm_ballot(tm_live) == 0ull)) {")
@@ -950,7 +1032,7 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append("        if (tm_cur < tm_end) {")
     body.append("          const u64 tm_av = tm_end - tm_cur;")
     body.append("          const u64 tm_n = (u64)__builtin_popcountll(tm_need);")
-    body.append("          if (!tm_live) {")
+    body.append(f"          if ({free_}) {{")
     body.append("            const u64 tm_r = tm_rank(tm_need);")
     body.append("            if (tm_r < tm_av) {")
     body.append("              tm_item = (i64)(tm_cur + tm_r);")
@@ -972,6 +1054,22 @@ def build(prog, block=BLOCK, schedule="step", refill=1, chunk=CHUNK, compact=COM
     body.append("    if (tm_live) {")
     body += step_lines
     body.append("    }")
+    if pb_h:
+        # the waiting items' POST: once the wave's waiting lane-iterations reach pb_h, when no lane of the wave is
+        # live, or once the queue is drained (then in the step they finish: the tail phase repacks live lanes only)
+        body.append("    {")
+        body.append("      const u64 tm_pm = tm_ballot(tm_pend);")
+        body.append("      if (tm_pm != 0ull) {")
+        body.append("        tm_acc += (u32)__builtin_popcountll(tm_pm);")
+        body.append(f"        if (tm_acc >= {pb_h}u || !tm_more || tm_ballot(tm_live) == 0ull) {{")
+        body.append("          tm_acc = 0u;")
+        body.append("          if (tm_pend) {")
+        body += post_lines
+        body.append("            tm_pend = false;")
+        body.append("          }")
+        body.append("        }")
+        body.append("      }")
+        body.append("    }")
     if not compact_on:
         body.append("    if (tm_ballot(tm_live || tm_more) == 0ull) break;")
     else:

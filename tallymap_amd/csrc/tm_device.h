@@ -76,6 +76,22 @@ TM_FN i64 tm_sar64(i64 x, u32 s) {
 }
 // u64 -> f32 rounded once, through an exact double (n < 2^53): the direct conversion lowers to a 64-bit shift
 TM_FN float tm_u64_f32(u64 n) { return (float)(double)n; }
+// u64 / i64 -> f32 for every value, rounded once (to nearest even) from 32-bit halves: the 32 leading significant
+// bits with a sticky bit for the bits below them (so the one rounding of the u32 -> f32 conversion is the rounding
+// of the whole value), then an exact scaling by a power of two.  The compiler's own expansion normalises the
+// operand with a 64-bit shift by its leading-zero count, a variable 64-bit shift (see tm_shl64).
+TM_FN float tm_u64f(u64 u) {
+  const u32 hi = (u32)(u >> 32), lo = (u32)u;
+  if (hi == 0u) return (float)lo;
+  const u32 n = (u32)__builtin_clz(hi);
+  const u32 m = n ? (hi << n) | (lo >> (32u - n)) : hi;
+  const u32 rest = n ? lo << n : lo;
+  return __builtin_ldexpf((float)(m | (rest != 0u ? 1u : 0u)), (int)(32u - n));
+}
+TM_FN float tm_i64f(i64 x) {
+  const float f = tm_u64f(x < 0 ? 0ull - (u64)x : (u64)x);
+  return x < 0 ? -f : f;
+}
 
 // ------------------------------------------------------------------------------------------- lax helpers
 template <class T> TM_FN T tm_fmax(T a, T b) {

@@ -257,13 +257,39 @@ int tm_register(long long id, const void* image, size_t n, const char* note) {
   return 0;
 }
 
+// the entry `name` of a loaded program's module (looked up once, then cached); 1 with the error set if absent
+static int aux_function(Loaded& L, long long id, const char* name, hipFunction_t* f) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = L.aux.find(name);
+  if (it != L.aux.end()) {
+    *f = it->second;
+    return 0;
+  }
+  if (g_rt.hipModuleGetFunction(f, L.mod, name) != hipSuccess) {
+    (void)g_rt.hipGetLastError();
+    g_err = "tallymap_rocm: program " + std::to_string(id) + " has no entry " + name;
+    return 1;
+  }
+  L.aux[name] = *f;
+  return 0;
+}
+
 int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, int flags, long long n_items,
               int block) {
   if (!g_hip_ok) return fail("tallymap_rocm: tm_init was not called");
   if (n < 1 || block < 64 || block > 1024 || block % 64) return fail("tallymap_rocm: bad launch shape");
   if (n_items < 0) return fail("tallymap_rocm: negative item count");
+  if ((flags & 4) && (n_zero > 0 || (flags & 2)))
+    return fail("tallymap_rocm: flags bit 4 (a later spawn generation) runs tm_main alone");
   std::shared_ptr<Loaded> L;
   if (loaded(id, &L)) return 1;
+  long long karg = n_items;
+  if (flags & 4) {           // the item count is on the device (tm_qnext); n_items bounds it and sizes the grid
+    hipFunction_t q = nullptr;
+    if (aux_function(*L, id, "tm_qnext", &q))
+      return fail("tallymap_rocm: flags bit 4 needs a spawning program (program %lld has no tm_qnext)", id);
+    karg = -1;
+  }
   int priv = 0;
   if (g_rt.hipFuncGetAttribute(&priv, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES, L->main) != hipSuccess) priv = 0;
   if (priv > MAX_PRIVATE)
@@ -273,7 +299,7 @@ int tm_launch(long long id, void* stream, void* const* bufs, int n, int n_zero, 
   if (occupancy(*L, block, &occ)) return 1;
   std::vector<char> args(sizeof(void*) * n + sizeof(long long));
   memcpy(args.data(), bufs, sizeof(void*) * n);
-  memcpy(args.data() + sizeof(void*) * n, &n_items, sizeof(long long));
+  memcpy(args.data() + sizeof(void*) * n, &karg, sizeof(long long));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (n_zero > 0 && L->zero && launch1(L->zero, 64, 256, s, args, "tm_zero")) return 1;
   if (n_items > 0) {
@@ -302,19 +328,7 @@ int tm_launch_aux(long long id, const char* name, void* stream, void* const* buf
   std::shared_ptr<Loaded> L;
   if (loaded(id, &L)) return 1;
   hipFunction_t f = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto it = L->aux.find(name);
-    if (it != L->aux.end()) {
-      f = it->second;
-    } else {
-      if (g_rt.hipModuleGetFunction(&f, L->mod, name) != hipSuccess) {
-        (void)g_rt.hipGetLastError();
-        return fail("tallymap_rocm: program %lld has no entry %s", id, name);
-      }
-      L->aux[name] = f;
-    }
-  }
+  if (aux_function(*L, id, name, &f)) return 1;
   std::vector<char> args(sizeof(void*) * n + sizeof(long long));
   memcpy(args.data(), bufs, sizeof(void*) * n);
   memcpy(args.data() + sizeof(void*) * n, &n_items, sizeof(long long));

@@ -58,9 +58,11 @@ def test_c1_truncation_poisons_float_tallies(oracle):
     assert np.all(np.isnan(_np(res.outputs["hist"])))
 
 
-@pytest.mark.parametrize("opts", [dict(schedule="item"), dict(block=64), dict(refill=8)])
+@pytest.mark.parametrize("opts", [dict(schedule="item"), dict(block=64), dict(refill=8), dict(post_batch=64),
+                                  dict(post_batch=0)])
 def test_c1_schedule_and_launch_shape_invariance(oracle, opts):
-    """per-item results do not depend on the schedule, block size or refill threshold (reference
+    """per-item results do not depend on the schedule, block size, refill threshold or POST deferral
+    (post_batch=64: every finished item waits for a shared POST pass; 0: none does) (reference
     docs/float_semantics.md:11-13, tests/invariants.py:290)."""
     print(f"case: C1 N=10000 {opts}", flush=True)
     xs, keys, theta = configs.c1_inputs()

@@ -44,12 +44,13 @@ VARIANTS = [dict(), dict(rev_tape=4), dict(rev_tape=2), dict(rev_tape=1), dict(s
             dict(rev_schedule="step"), dict(rev_schedule="step", rev_tape=4), dict(rev_schedule="step", rev_tape=2),
             dict(rev_schedule="step", rev_refill=1), dict(rev_schedule="step", rev_refill=64),
             dict(rev_schedule="item"), dict(rev_schedule="item", rev_checkpoints=4),
-            dict(rev_schedule="item", rev_checkpoints=1)]
+            dict(rev_schedule="item", rev_checkpoints=1), dict(post_batch=64), dict(post_batch=64, rev_residual=True)]
 
 
 @pytest.mark.parametrize("opts", VARIANTS, ids=["tape", "tape4", "tape2", "tape1", "tape-itemsched", "resid",
                                                 "resid-tape4", "resid-tape1", "step", "step-tape4", "step-tape2",
-                                                "step-refill1", "step-refill64", "item16", "item4", "item1"])
+                                                "step-refill1", "step-refill64", "item16", "item4", "item1",
+                                                "tape-postbatch", "resid-postbatch"])
 def test_c1_grad_xs_and_replay_variants(oracle, opts):
     """cotangents of xs (per item, through the loop state: the replay) and of theta with weights ct, against the
     oracle; the replay variants give bitwise the same per-item cotangents and broadcast cotangent (reference
@@ -57,8 +58,9 @@ def test_c1_grad_xs_and_replay_variants(oracle, opts):
     items recompute the states past the tape inside the reverse step; the item schedule of the forward template;
     the residual tape forced, alone and with 4- and 1-slot tapes whose later steps replay from the checkpoint),
     the single-kernel step-scheduled replay (an item overflowing a 4- or 2-slot tape takes the checkpointed sweep;
-    waves refilled by 1 or 64 free lanes) and the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its
-    segment re-runs)."""
+    waves refilled by 1 or 64 free lanes), the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its
+    segment re-runs), and the tape adjoint with every finished item's POST deferred to a shared pass
+    (post_batch=64; state and residual tapes)."""
     print(f"case: C1 vjp (xs, theta) {opts}", flush=True)
     xs, keys, theta = configs.c1_inputs()
     ct = np.linspace(0.5, 2.0, 16).astype(np.float32)

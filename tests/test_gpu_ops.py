@@ -215,7 +215,11 @@ def test_f64_ops_and_conversions():
 def test_signed_integer_ops(dt, bits):
     print(f"case: {np.dtype(dt).name} integer ops", flush=True)
     rng = np.random.default_rng(4)
-    spec = I32S if bits == 32 else np.concatenate([I32S, [2 ** 63 - 1, -2 ** 63, 2 ** 40 + 7, -(2 ** 53) - 1]])
+    # (64-bit: the extremes, and ties and near-ties of the conversion to float32 at 2^40, where its ulp is 2^17)
+    spec = I32S if bits == 32 else np.concatenate([I32S, [2 ** 63 - 1, -2 ** 63, 2 ** 40 + 7, -(2 ** 53) - 1,
+                                                          2 ** 40 + 2 ** 16, 2 ** 40 + 2 ** 16 + 1, 2 ** 40 + 3 * 2 ** 16,
+                                                          -(2 ** 40 + 3 * 2 ** 16), 2 ** 63 - 2 ** 38, 2 ** 32 - 1,
+                                                          2 ** 32, 2 ** 32 + 1, 2 ** 56 + 2 ** 32 + 1]])
     rnd = [rng.integers(-2 ** (bits - 1), 2 ** (bits - 1), 2048, dtype=np.int64 if bits == 64 else np.int32)
            for _ in range(2)]
     rnd[1][:1024] = rng.integers(-3, bits + 3, 1024)

@@ -81,8 +81,8 @@ def _bits(a):
     return np.asarray(a).view(np.uint32)
 
 
-@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(block=64), dict(refill=8)],
-                         ids=["step", "item", "block64", "refill8"])
+@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(block=64), dict(refill=8),
+                                  dict(post_batch=64)], ids=["step", "item", "block64", "refill8", "postbatch"])
 def test_records_canonical_layout_bitwise(opts):
     print(f"case: records walker N=65536 {opts}", flush=True)
     xs, keys, theta = configs.c1_inputs(1 << 16)

@@ -198,7 +198,8 @@ def _emulate_shower(roots, theta):
     return dep_terms, count, children, root_out
 
 
-@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(refill=8)], ids=["step", "item", "refill8"])
+@pytest.mark.parametrize("opts", [dict(), dict(schedule="item"), dict(refill=8), dict(post_batch=64)],
+                         ids=["step", "item", "refill8", "postbatch"])
 def test_spawn_shower_against_emulation(opts):
     """the exact deposit profile (each bin the correctly rounded sum of its deposits), the particles per
     generation, the children count and the roots' own results, bitwise against the numpy emulation of the tree."""

@@ -171,6 +171,16 @@ def test_shift64_helpers_match_native_shifts(tmp_path):
     assert r.returncode == 0 and r.stdout.strip() == "0 mismatches", r.stdout
 
 
+def test_int64_to_float32_without_64bit_shifts(tmp_path):
+    """tm_u64f / tm_i64f (32 leading bits from 32-bit halves, a sticky bit, one u32 -> f32 rounding) equal the host's
+    int64 / uint64 -> float32 conversions on edge values, ties and their neighbours at every exponent, and 2M
+    pseudo-random values at every magnitude."""
+    exe = _build("tests/native/i64f_check.cc", str(tmp_path / "i64f_check"))
+    r = subprocess.run([exe], capture_output=True, text=True)
+    bad, n = map(int, r.stdout.split())
+    assert r.returncode == 0 and bad == 0 and n > 2_000_000, r.stdout
+
+
 def test_shift_hazard_scanner_flags_only_block_end_amount_registers():
     from tallymap_amd.backend import compile as Cm
     dis = "\n".join([
