@@ -36,14 +36,14 @@ HBM_PEAK_GBS = 8000.0
 FWD_BYTES_PER_ITEM = 17
 GRAD_BYTES_PER_ITEM = 13
 # Counter-derived figures per launch at N = 4,194,304, each keyed by the code object it was measured on (the first
-# 16 hex digits of its hipRTC cache key: sha256 of compiler, options and source).  traffic: HBM bytes, 2 x FETCH_SIZE
-# + 1 x WRITE_SIZE (KiB), the factors those counters read on a plain 1 GiB device copy (profiles/
-# c2_random_walk_traffic.md); valu_insts: wave64 VALU instructions (SQ_INSTS_VALU, profiles/
+# 16 hex digits of its hipRTC cache key: sha256 of compiler, options and source).  traffic: HBM bytes,
+# FETCH_SIZE x 1.938 + WRITE_SIZE x 0.970 (KiB), the factors those counters read on a plain 1 GiB device copy in the
+# same runs (profiles/c2_random_walk_traffic.md); valu_insts: wave64 VALU instructions (SQ_INSTS_VALU, profiles/
 # c2_random_walk_sq_counters.md).  A kernel whose key differs from the one measured reports null with the reason,
 # so a changed kernel never carries a stale counter.
-MEASURED = {"fused": {"code": "73639312187f5055", "traffic": 76_491_312, "valu_insts": 7.0269e9},
-            "forward": {"code": "d7584779552f8ac6", "traffic": 77_243_849, "valu_insts": 7.0288e9},
-            "gradient": {"code": "d8efcabe853d96db", "traffic": 56_446_088, "valu_insts": 6.7209e9}}
+MEASURED = {"fused": {"code": "de6ce353efc17d73", "traffic": 73_476_525, "valu_insts": 6.9271e9},
+            "forward": {"code": "e4700a2063ecb470", "traffic": 74_111_030, "valu_insts": 6.9229e9},
+            "gradient": {"code": "2a35f5bb7a522946", "traffic": 54_704_455, "valu_insts": 6.7220e9}}
 # MI355X's VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per 4 cycles on a 16-lane SIMD, at the
 # 2.4 GHz peak engine clock
 VALU_PEAK = 1024 * 2.4e9 / 4
