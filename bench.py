@@ -20,6 +20,9 @@ configs: the other BASELINE configs at their own sizes (C1 10,000; C3, C4 4,194,
 gradient launches timed the same way, each with the oracle on a bounded sample beside it.
 atomics / emit_roofline: the atomic adds/s of the patterns the kernels issue (backend/atomics.py; MI355X publishes no
 atomic peak), and C2's forward emit rate against the peak of the LDS u64 adds its constant emits are counted with.
+published: the reference's own benchmark problems (random walk, transport, walk on spheres, ODE ensemble;
+tallymap_amd/problems.py) at the sizes of its published L40S kernel-backend timings, forward and loss gradient, the
+published times beside them.
 """
 import argparse
 import json
@@ -405,6 +408,57 @@ def bench_configs(steps, warmup, with_cpu):
     return out
 
 
+def bench_published(steps, warmup):
+    """the reference's own benchmark problems (tallymap_amd/problems.py, from benchmarks/vs_jax/problems/) at the
+    size and divergence level of its published L40S kernel-backend rows: the forward call and the gradient of the
+    problem's loss w.r.t. theta (the forward call, the loss's cotangent of the tally from its result, the adjoint),
+    each timed with HIP events on torch's current stream around the whole call, median of `steps` after `warmup`;
+    the published times beside them (jax.jit wall time per call, median of >= 7, on an NVIDIA L40S)."""
+    import torch
+
+    import tallymap_amd as tm
+    from tallymap_amd import problems as P
+    out = {}
+    stream = torch.cuda.current_stream()
+    for name, p in P.PROBLEMS.items():
+        n = p["n"]
+        args, extra = p["inputs"](n)
+        dev = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in args]
+        f = P.mapped(name)
+
+        def fwd():
+            return f(*dev)
+
+        def grad():
+            res, pull = tm.vjp(f, *dev, argnums=p["argnum"])
+            return pull(p["ct"](res.outputs, n, extra))
+
+        def timed(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+            for e in evs:
+                e[0].record(stream)
+                fn()
+                e[1].record(stream)
+            torch.cuda.synchronize()
+            return float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
+        r = fwd()
+        trips = r.per_item.double()
+        d = {"n_items": n, "fwd_ms": timed(fwd), "grad_ms": timed(grad),
+             "mean_trips": float(trips.mean().item()), "max_trips": int(trips.max().item()),
+             "truncated": int(r.stats["n_truncated"].item()),
+             "l40s_fwd_ms": p["published"]["fwd_ms"], "l40s_grad_ms": p["published"]["grad_ms"],
+             "l40s_source": p["published"]["source"]}
+        d["fwd_speedup_vs_l40s"] = d["l40s_fwd_ms"] / d["fwd_ms"]
+        d["grad_speedup_vs_l40s"] = d["l40s_grad_ms"] / d["grad_ms"]
+        out[name] = d
+        print(f"bench: published {name} done (fwd {d['fwd_ms']:.3f} ms, grad {d['grad_ms']:.3f} ms)",
+              file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -419,13 +473,13 @@ def main():
     ap.add_argument("--traffic-bytes", type=float, default=None,
                     help="HBM bytes per dominant-kernel launch (default: the rocprofv3 measurement of this kernel at "
                          "the default N, null at other N)")
-    ap.add_argument("--section", choices=("configs", "records", "spawn"), default=None,
+    ap.add_argument("--section", choices=("configs", "records", "spawn", "published"), default=None,
                     help="run only this section and print its JSON object (for profiling one workload)")
     a = ap.parse_args()
     if a.section:
         steps = max(3, a.steps // 4)
         run = {"configs": lambda: bench_configs(steps, 1, not a.no_cpu), "records": lambda: bench_records(steps, 1),
-               "spawn": lambda: bench_spawn(steps, 1)}[a.section]
+               "spawn": lambda: bench_spawn(steps, 1), "published": lambda: bench_published(max(7, steps), 2)}[a.section]
         print(json.dumps({a.section: run()}))
         return
     if a.gpus != 1:
@@ -560,6 +614,7 @@ def main():
         out["configs"] = bench_configs(max(3, a.steps // 4), 1, not a.no_cpu)
         out["records"] = bench_records(max(3, a.steps // 4), 1)
         out["spawn"] = bench_spawn(max(3, a.steps // 4), 1)
+        out["published"] = bench_published(7, 2)
     print(json.dumps(out))
 
 

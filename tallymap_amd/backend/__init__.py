@@ -445,23 +445,29 @@ def prebuild(entries, n=64):
     """compile (through hipRTC, no GPU needed) the forward and adjoint modules of each (name, config) in
     `entries` (config = dict(item, outputs, in_axes, max_steps); a config whose outputs are sized by N appears once
     per N) into the package's code-object cache -> [(name, tag, key)].  The operand shapes come from the config's
-    input generator at `n` items (per-item shapes do not depend on N)."""
+    input generator at `n` items (per-item shapes do not depend on N): configs.<name>_inputs, or the config's own
+    `inputs` (returning (args, extra)); a config with `argnum` is differentiated w.r.t. that broadcast argument
+    alone, others w.r.t. every differentiable argument and every broadcast one."""
     from .. import _core as C
     from .._api import build_program
     from .. import configs as CF
     done = []
     for name, cfg in entries:
-        args = getattr(CF, f"{name}_inputs")(n)
+        args = cfg["inputs"](n)[0] if "inputs" in cfg else getattr(CF, f"{name}_inputs")(n)
         axes = cfg["in_axes"]
         pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
         bav = [C.AVal(np.shape(a), np.asarray(a).dtype) for a, x in zip(args, axes) if x is None]
-        prog, _ = build_program(cfg["item"], cfg["outputs"], axes, pav, bav, cfg["max_steps"])
+        prog, _ = build_program(cfg["item"], cfg["outputs"], axes, pav, bav, cfg.get("max_steps"))
         src, _ = K.build(prog, block=K.BLOCK, schedule="step", refill=1)
         Cm.code_object(src, name=f"tm_{prog.tag}.hip", store_pkg=True)
         done.append((name, prog.tag, Cm._key(src)[:16]))
         from . import reverse as R
-        wp, wb = R.default_wrt(prog)
-        for wrt in ((wp, wb), ((), wb)):
+        if "argnum" in cfg:
+            wrts = [((), (sum(1 for x in axes[:cfg["argnum"]] if x is None),))]
+        else:
+            wp, wb = R.default_wrt(prog)
+            wrts = [(wp, wb), ((), wb)]
+        for wrt in wrts:
             adj = R.adjoint_program(prog, wrt)
             pl = R.plan(adj)
             if any(pl.car_act):          # the tape adjoint: its count and reverse programs (and value_and_grad's

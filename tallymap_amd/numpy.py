@@ -94,6 +94,61 @@ def sum(x):             # noqa: A001
     return C.reduce_sum(x) if C.is_traced(x) else _np.sum(x)
 
 
+def max(x):             # noqa: A001
+    """the largest element of a small array: lax.max folded left to right (NaN-propagating, as XLA's reduce_max;
+    its derivative goes through lax.max's rule, pairwise at ties)."""
+    if not C.is_traced(x):
+        return _np.max(x)
+    if not x.shape:
+        return x
+    acc = x[0]
+    for i in range(1, x.shape[0]):
+        acc = C.binop("max", acc, x[i])
+    return acc
+
+
+def min(x):             # noqa: A001
+    """the smallest element (lax.min folded left to right)."""
+    if not C.is_traced(x):
+        return _np.min(x)
+    if not x.shape:
+        return x
+    acc = x[0]
+    for i in range(1, x.shape[0]):
+        acc = C.binop("min", acc, x[i])
+    return acc
+
+
+def _arg(x, better):
+    best, idx = x[0], C.literal(0, C.I32, weak=False)
+    for i in range(1, x.shape[0]):
+        v = x[i]
+        take = better(v, best)
+        if _np.issubdtype(x.dtype, _np.floating):      # the first NaN wins, as jnp.argmin / argmax
+            take = C.binop("or", take, C.binop("and", C.binop("ne", v, v), C.binop("eq", best, best)))
+        best = C.select(take, v, best)
+        idx = C.select(take, C.literal(i, C.I32, weak=False), idx)
+    return idx
+
+
+def argmin(x):
+    """the index (int32) of the first smallest element of a small 1-d array; a NaN counts as the smallest."""
+    if not C.is_traced(x):
+        return _np.int32(_np.argmin(x))
+    if len(x.shape) != 1:
+        raise C.TraceError("argmin of an item value: 1-d arrays only")
+    return _arg(x, lambda v, b: C.binop("lt", v, b))
+
+
+def argmax(x):
+    """the index (int32) of the first largest element of a small 1-d array; a NaN counts as the largest."""
+    if not C.is_traced(x):
+        return _np.int32(_np.argmax(x))
+    if len(x.shape) != 1:
+        raise C.TraceError("argmax of an item value: 1-d arrays only")
+    return _arg(x, lambda v, b: C.binop("gt", v, b))
+
+
 def dot(a, b):
     """the dot product of two small vectors: (a0 b0 + a1 b1) + ..., left to right."""
     acc = a[0] * b[0]
