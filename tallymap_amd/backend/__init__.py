@@ -470,7 +470,7 @@ def prebuild(entries, n=64):
         for wrt in wrts:
             adj = R.adjoint_program(prog, wrt)
             pl = R.plan(adj)
-            if any(pl.car_act):          # the tape adjoint: its count and reverse programs (and value_and_grad's
+            if any(pl.sweep):            # the tape adjoint: its count and reverse programs (and value_and_grad's
                 from . import tape as T  # count program, which keeps the forward's outputs)
                 tp = T.programs(adj, pl)
                 progs = [tp.count, tp.reverse, T.programs(adj, pl, keep=True).count]
@@ -530,9 +530,11 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
     """the replay adjoint of prog: cotangents of the per-item operands wrt[0] ([N, ...] each) and the broadcast
     operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
     0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated).
-    When no loop carry needs a reverse sweep the adjoint is an ordinary item program (reverse.forward_only_program)
-    run by the forward template (step refill); otherwise the replay kernel opts['rev_schedule'] names: 'step' (the
-    default, replay.build: step refill over a tape) or 'item' (reverse.build: in-lane checkpoints).  With n_active
+    When no loop carry needs a reverse sweep (an accumulator carry, c' = c + d, does not: reverse.Plan.accum) the
+    adjoint is an ordinary item program (reverse.forward_only_program) run by the forward template (step refill);
+    otherwise the adjoint opts['rev_schedule'] names: 'tape' (the default, backend/tape.py: the count and reverse
+    launches of the forward template), 'step' (replay.build: one kernel, step refill over a tape) or 'item'
+    (reverse.build: in-lane checkpoints).  With n_active
     only the first n_active items run (the adjoint launches over them alone); the others get zero cotangents and
     add nothing to the broadcast ones, as they emitted nothing in the forward.
     forward: value_and_grad -- the launches that replay the forward (the forward-only adjoint; the tape adjoint's
@@ -580,7 +582,7 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
             ins_b.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
                                        else x, np.float32).reshape(-1))
     fo = None
-    if not any(pl.car_act):
+    if not any(pl.sweep):
         fkey = adj.digest() + ("|vg" if forward else "")
         q = _FWD_ONLY.get(fkey)
         if q is None:

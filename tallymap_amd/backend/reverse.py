@@ -201,6 +201,49 @@ class Plan:
     bconst_act: list        # per body constant: active and relevant (its cotangent accumulates per step)
     ft: list                # tally slots with a cotangent input (float32 sums)
     fy: list                # per-item results with a cotangent input (float32)
+    accum: list = None      # per carry: an active scalar accumulator (c' = c + d, c read nowhere else in the step,
+                            # d independent of every active carry): its cotangent is the same at every step
+
+    @property
+    def sweep(self):
+        """per carry: needs the reverse sweep (active, its cotangent can be nonzero, and it is no accumulator)"""
+        acc = self.accum or [False] * len(self.car_act)
+        return [a and not c for a, c in zip(self.car_act, acc)]
+
+
+def _accumulators(sp, car_act):
+    """per carry: whether it is an active float32 scalar whose step is c' = c + d, with c read by nothing else in
+    the step (the loop condition may read it) and d independent of every active carry.  Such a carry's cotangent
+    is the same before and after every step, so the adjoint needs no reverse sweep for it: the steps' VJPs with a
+    unit cotangent on it, summed in the forward loop, times its final cotangent."""
+    body = sp.body
+    nbc = len(sp.bconst)
+    uses = {}
+    for e in body.eqns:
+        for v in e.invars:
+            if isinstance(v, C.Var):
+                uses[v.id] = uses.get(v.id, 0) + 1
+        for sub in C.subjaxprs(e):
+            for i in _free(sub):
+                uses[i] = uses.get(i, 0) + 1
+    for v in body.outvars:
+        if isinstance(v, C.Var):
+            uses[v.id] = uses.get(v.id, 0) + 1
+    prod = {o.id: e for e in body.eqns for o in e.outvars}
+    dep = AD.activity(body, [False] * nbc + list(car_act))
+    out = []
+    for j, a in enumerate(car_act):
+        ok = False
+        vin, vout = body.invars[nbc + j], body.outvars[j]
+        e = prod.get(vout.id) if isinstance(vout, C.Var) else None
+        if a and e is not None and e.prim == "add" and vin.aval.shape == () and vin.aval.dtype == C.F32:
+            x, y = e.invars
+            d = y if isinstance(x, C.Var) and x.id == vin.id else (x if isinstance(y, C.Var) and y.id == vin.id
+                                                                    else None)
+            ok = (d is not None and uses.get(vin.id) == 1 and uses.get(vout.id) == 1
+                  and not (isinstance(d, C.Var) and d.id in dep))
+        out.append(ok)
+    return out
 
 
 def plan(adj):
@@ -237,7 +280,7 @@ def plan(adj):
     rb = AD.relevance(sp.body, rel)
     car_act = [f and r for f, r in zip(fwd, rel)]
     bconst_act = [f and r for f, r in zip(bconst_fwd, rb[:len(sp.bconst)])]
-    return Plan(sp, pre_act_in, P_act, car_act, bconst_act, ft, fy)
+    return Plan(sp, pre_act_in, P_act, car_act, bconst_act, ft, fy, _accumulators(sp, car_act))
 
 
 def _ct_reader(ft, S_of, arrays=None):
@@ -302,8 +345,9 @@ def emit_dense_ct(t, v, n):
 
 def forward_only_program(adj, pl, keep=False):
     """the adjoint as an ordinary item program, when no loop carry needs a reverse sweep: PRE, the loop with the
-    step VJPs of the body constants accumulated as extra carries, POST, POST's and PRE's VJPs, one exact emit per
-    differentiated broadcast element.  It runs through the forward kernel template (step refill).
+    step VJPs of the body constants accumulated as extra carries (and, per accumulator carry, the step VJPs with a
+    unit cotangent on it, scaled by its final cotangent after the loop), POST, POST's and PRE's VJPs, one exact
+    emit per differentiated broadcast element.  It runs through the forward kernel template (step refill).
     invars: tallies [forward tallies, discarded][ct of each differentiated broadcast operand, exact] + per-item
     [operands][result cotangents] + broadcast [operands][tally cotangents]; per-item results [operand
     cotangents][truncated].
@@ -321,7 +365,16 @@ def forward_only_program(adj, pl, keep=False):
     body_vjp, b_ctout, b_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + [False] * sp.ncar, _ct_reader(ft, S_of),
                                              {nbc + j: s for j, s in enumerate(sp.car_slot) if s is not None},
                                              ct_given=[False] * sp.ncar, sparse=sp_body, prune=True)
-    post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, pl.P_act + [False] * sp.ncar, _ct_reader(ft, S_of),
+    # accumulator carries (c' = c + d): the step's VJP with a unit cotangent on c, emits inert; summed over the
+    # steps in the forward loop and scaled by c's final cotangent (POST's VJP) after it
+    acc_j = [j for j, a in enumerate(pl.accum or []) if a]
+    acc_vjp = []
+    for j in acc_j:
+        vj, _, ci = AD.vjp_jaxpr(sp.body, pl.bconst_act + [False] * sp.ncar, None, None, emits_active=False,
+                                 ct_given=[i == j for i in range(sp.ncar)], prune=True)
+        acc_vjp.append((vj, [q for q in range(nbc) if ci[q]]))
+    post_act_car = [j in acc_j for j in range(sp.ncar)]
+    post_vjp, p_ctout, p_ctin = AD.vjp_jaxpr(sp.post, pl.P_act + post_act_car, _ct_reader(ft, S_of),
                                              {sp.nP + j: s for j, s in enumerate(sp.car_slot) if s is not None},
                                              sparse=sp_post, prune=True)
     pre_vjp, r_ctout, r_ctin = AD.vjp_jaxpr(sp.pre, pl.pre_act_in, _ct_reader(ft, S_of), {k: k for k in range(nT)},
@@ -348,18 +401,23 @@ def forward_only_program(adj, pl, keep=False):
         bcv = [cval(r) for r in sp.bconst]
         gq = [q for q in range(nbc) if b_ctin[q]]
         g0 = [np.zeros(sp.body.invars[q].aval.shape, np.float32)[()] for q in gq]
+        h0 = [[np.zeros(sp.body.invars[q].aval.shape, np.float32)[()] for q in qs] for _, qs in acc_vjp]
 
         def cond_f(c):
             return AD.eval_jaxpr(sp.cond, ccv + list(c[0]))[0]
 
         def body_f(c):
-            cars, g = list(c[0]), list(c[1])
+            cars, g, h = list(c[0]), list(c[1]), [list(x) for x in c[2]]
             vj = AD.eval_jaxpr(body_vjp, bcv + cars, ct_read, ct_emit)
             g = [gi + vj[k] for k, gi in enumerate(g)]
-            return (AD.eval_jaxpr(sp.body, bcv + cars), g)
+            for a, (vjp_a, _) in enumerate(acc_vjp):
+                va = AD.eval_jaxpr(vjp_a, bcv + cars + [np.float32(1.0)])
+                h[a] = [hi + va[k] for k, hi in enumerate(h[a])]
+            return (AD.eval_jaxpr(sp.body, bcv + cars), g, h)
         never = (not sp.cond.eqns and isinstance(sp.cond.outvars[0], C.Lit)
                  and not bool(sp.cond.outvars[0].val))          # (the loop split() adds to a loop-free item)
-        cars_f, g = L.while_loop(cond_f, body_f, (cars0, g0)) if sp.ncar and not never else (cars0, g0)
+        cars_f, g, h = (L.while_loop(cond_f, body_f, (cars0, g0, h0)) if sp.ncar and not never
+                        else (cars0, g0, h0))
         cars_f = list(cars_f)
         post_outs = AD.eval_jaxpr(sp.post, Pv + cars_f)
         post_cts = []
@@ -369,21 +427,31 @@ def forward_only_program(adj, pl, keep=False):
                 post_cts.append(cyin[fy.index(q)] if q >= 0 and q in fy else np.float32(0.0))
         pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read, ct_emit)
         gP = {}
+        lam = {}                                    # the accumulators' final (and so every step's) cotangents
         k = 0
         for q, m in enumerate(p_ctin):
             if m:
                 if q < sp.nP:
                     gP[q] = pv[k]
+                elif q - sp.nP in acc_j:
+                    lam[q - sp.nP] = pv[k]
                 k += 1
-        for kk, q in enumerate(gq):                 # body constants' step sums onto their P var
+
+        def onto_p(q, v):                           # a body constant's sum onto its P var
             r = sp.bconst[q]
             if r[0] == "P":
-                gP[r[1]] = g[kk] if r[1] not in gP else gP[r[1]] + g[kk]
+                gP[r[1]] = v if r[1] not in gP else gP[r[1]] + v
+        for kk, q in enumerate(gq):
+            onto_p(q, g[kk])
+        for a, (j, (_, qs)) in enumerate(zip(acc_j, acc_vjp)):
+            if j in lam:
+                for kk, q in enumerate(qs):
+                    onto_p(q, lam[j] * h[a][kk])
         pre_cts = []
         for j, (o, m) in enumerate(zip(sp.pre.outvars, r_ctout)):
             if m:
                 z = np.zeros(o.aval.shape, np.float32)[()]
-                pre_cts.append(gP.get(j - sp.ncar, z) if j >= sp.ncar else z)
+                pre_cts.append(gP.get(j - sp.ncar, z) if j >= sp.ncar else lam.get(j, z))
         gr = AD.eval_jaxpr(pre_vjp, tin[:nT] + pin + bin_ + pre_cts, ct_read, ct_emit)
         g_pi, g_bc = {}, {}
         k = 0

@@ -399,3 +399,44 @@ def test_table_read_cotangents_are_emitted_at_the_row_read():
             prims = [e.prim for e in C.walk_eqns(q.jaxpr)]
             assert prims.count("tallymap_emit_slot") == 1
             assert prims.count("select_n") < 40 and prims.count("tallymap_emit") <= 2
+
+
+def test_accumulator_carries_need_no_reverse_sweep():
+    """a carry whose step is c' = c + d (c read nowhere else in the step, d free of active carries) has the same
+    cotangent at every step: the plan marks it an accumulator and the forward-only adjoint handles it (the
+    walk-on-spheres estimator's sum); a carry that is also read in the step, scaled, or emitted stays a sweep
+    carry (the tape adjoint)."""
+    from tallymap_amd.backend import reverse as R
+
+    def item(kind):
+        def f(t, x, th):
+            def body(c):
+                k, y, acc = c
+                y = y * 0.5 + x
+                d = th * y
+                if kind == "acc":
+                    acc = acc + d
+                elif kind == "read":
+                    acc = acc + d * acc
+                elif kind == "scaled":
+                    acc = acc * 0.9 + d
+                return k + 1, y, acc
+            k, y, acc = lax.while_loop(lambda c: (c[0] < 8) & (c[2] < 100.0), body, (0, x, th * 2.0))
+            return t.add("h", 0, acc * acc), k
+        return f
+
+    def emitted(t, x, th):
+        def body(c):
+            k, acc, t_ = c
+            acc = acc + th * x
+            return k + 1, acc, t_.add("h", 0, acc)
+        return lax.while_loop(lambda c: c[0] < 8, body, (0, np.float32(0.0), t))[2]
+    pav, bav = [((), np.float32)], [((), np.float32)]
+    for f, want in ((item("acc"), True), (item("read"), False), (item("scaled"), False), (emitted, False)):
+        prog = _prog(f, {"h": tm.Sum((1,))}, pav, bav, (0, None))
+        pl = R.plan(R.adjoint_program(prog, ((), (0,))))
+        assert any(pl.car_act)
+        assert (not any(pl.sweep)) == want, f
+        if want:
+            q = R.forward_only_program(R.adjoint_program(prog, ((), (0,))), pl)
+            assert not any(e.prim == "tallymap_tape_put" for e in C.walk_eqns(q.jaxpr))

@@ -222,3 +222,35 @@ def test_value_and_grad_in_fewer_launches(name, inputs, argnums, weights):
     assert len(ya) == len(yb) and all(np.array_equal(x.view(np.uint8), y.view(np.uint8)) for x, y in zip(ya, yb))
     assert np.array_equal(_np(res.truncated), _np(ref.truncated))
     assert int(_np(res.stats["n_truncated"])) == int(_np(ref.stats["n_truncated"]))
+
+
+def test_accumulator_carry_forward_only_adjoint():
+    """an accumulator carry (acc' = acc + theta y_k, started at 2 theta, read by the loop condition, its square
+    emitted after the loop) is differentiated by the forward-only adjoint (no tape): d sum acc^2 / d theta =
+    sum 2 acc (2 + sum_k y_k), from a float32 emulation of y; and equal to forward mode."""
+    from tallymap_amd import lax
+
+    def item(t, x, th):
+        def body(c):
+            k, y, acc = c
+            y = y * 0.5 + x
+            return k + 1, y, acc + th * y
+        k, y, acc = lax.while_loop(lambda c: (c[0] < 8) & (c[2] < 100.0), body, (0, x, th * 2.0))
+        return t.add("h", 0, acc * acc), k
+    n = 50_000
+    print(f"case: accumulator carry N={n}", flush=True)
+    x = np.linspace(0.0, 1.0, n).astype(np.float32)
+    th = np.float32(0.5)
+    f = tm.vmap(item, outputs={"h": tm.Sum((1,))}, in_axes=(0, None))
+    g = float(_np(tm.grad(f, argnums=1)(x, th)))
+    y = x.copy()
+    S = np.zeros(n, np.float64)
+    acc = np.full(n, np.float32(th * np.float32(2.0)))
+    for _ in range(8):
+        y = (y * np.float32(0.5) + x).astype(np.float32)
+        S += y
+        acc = (acc + th * y).astype(np.float32)
+    want = float(np.sum(2.0 * acc.astype(np.float64) * (2.0 + S)))
+    assert abs(g - want) <= 1e-5 * abs(want), (g, want)
+    jf = float(_np(tm.jacfwd(f, argnums=1)(x, th)["h"][1]).reshape(-1)[0])
+    assert abs(g - jf) <= 1e-5 * abs(want), (g, jf)
