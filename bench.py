@@ -413,7 +413,9 @@ def bench_published(steps, warmup):
     size and divergence level of its published L40S kernel-backend rows: the forward call and the gradient of the
     problem's loss w.r.t. theta (the forward call, the loss's cotangent of the tally from its result, the adjoint),
     each timed with HIP events on torch's current stream around the whole call, median of `steps` after `warmup`;
-    the published times beside them (jax.jit wall time per call, median of >= 7, on an NVIDIA L40S)."""
+    the published times beside them (jax.jit wall time per call, median of >= 7, on an NVIDIA L40S).  Each mode the
+    reference publishes for a problem is timed: fwd, grad (reverse mode), jvp (a unit tangent on theta) and jacfwd
+    of the loss (a forward-mode lane per element of theta)."""
     import torch
 
     import tallymap_amd as tm
@@ -423,15 +425,31 @@ def bench_published(steps, warmup):
     for name, p in P.PROBLEMS.items():
         n = p["n"]
         args, extra = p["inputs"](n)
-        dev = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in args]
+        dev = [{k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in x.items()} if isinstance(x, dict)
+               else torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in args]
         f = P.mapped(name)
+        pub = p["published"]
+        runs = {"fwd": lambda: f(*dev)}
+        if "grad_ms" in pub:
+            def grad():
+                res, pull = tm.vjp(f, *dev, argnums=p["argnum"])
+                return pull(p["ct"](res.outputs, n, extra))
+            runs["grad"] = grad
+        if "jvp_ms" in pub:
+            tan = tuple(torch.ones_like(x) if i == p["argnum"] else None for i, x in enumerate(dev))
+            runs["jvp"] = lambda: tm.jvp(f, dev, tan)
+        if "jacfwd_ms" in pub:
+            jf = tm.jacfwd(f, argnums=p["argnum"], with_primal=True)
 
-        def fwd():
-            return f(*dev)
-
-        def grad():
-            res, pull = tm.vjp(f, *dev, argnums=p["argnum"])
-            return pull(p["ct"](res.outputs, n, extra))
+            def jacfwd():
+                # jax.jacfwd of the loss: d tally / d theta (one launch: a lane per element of theta, the primal
+                # beside them), contracted with the loss's derivative at the primal tally
+                jac, prim = jf(*dev)
+                ct = p["ct"](prim.outputs, n, extra)
+                a = p["argnum"]
+                return sum((ct[k].reshape(ct[k].shape + (1,)) * jac[k][a]).reshape(-1, jac[k][a].shape[-1]).sum(0)
+                           for k in ct)
+            runs["jacfwd"] = jacfwd
 
         def timed(fn):
             for _ in range(warmup):
@@ -444,18 +462,20 @@ def bench_published(steps, warmup):
                 e[1].record(stream)
             torch.cuda.synchronize()
             return float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
-        r = fwd()
-        trips = r.per_item.double()
-        d = {"n_items": n, "fwd_ms": timed(fwd), "grad_ms": timed(grad),
-             "mean_trips": float(trips.mean().item()), "max_trips": int(trips.max().item()),
-             "truncated": int(r.stats["n_truncated"].item()),
-             "l40s_fwd_ms": p["published"]["fwd_ms"], "l40s_grad_ms": p["published"]["grad_ms"],
-             "l40s_source": p["published"]["source"]}
-        d["fwd_speedup_vs_l40s"] = d["l40s_fwd_ms"] / d["fwd_ms"]
-        d["grad_speedup_vs_l40s"] = d["l40s_grad_ms"] / d["grad_ms"]
+        r = runs["fwd"]()
+        d = {"n_items": n, "truncated": int(r.stats["n_truncated"].item()), "l40s_source": pub["source"]}
+        if r.per_item is not None:
+            trips = (r.per_item[-1] if isinstance(r.per_item, (tuple, list)) else r.per_item).double()
+            d["mean_trips"], d["max_trips"] = float(trips.mean().item()), int(trips.max().item())
+        if "spawned" in r.stats:
+            d["children"] = int(r.stats["spawned"].item())
+        for mode, fn in runs.items():
+            d[f"{mode}_ms"] = timed(fn)
+            d[f"l40s_{mode}_ms"] = pub[f"{mode}_ms"]
+            d[f"{mode}_speedup_vs_l40s"] = pub[f"{mode}_ms"] / d[f"{mode}_ms"]
         out[name] = d
-        print(f"bench: published {name} done (fwd {d['fwd_ms']:.3f} ms, grad {d['grad_ms']:.3f} ms)",
-              file=sys.stderr, flush=True)
+        times = ", ".join("%s %.3f ms" % (m, d[m + "_ms"]) for m in runs)
+        print(f"bench: published {name} done ({times})", file=sys.stderr, flush=True)
     return out
 
 

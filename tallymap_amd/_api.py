@@ -1087,10 +1087,20 @@ def jvp(mapped, primals, tangents, n_active=None):
     return primal, Result(t_tal[0], t_ys[0], None, None)
 
 
-def jacfwd(mapped, argnums=0):
+def _host_meta(x):
+    """(shape, numpy dtype) of an argument, a numpy array or a (device) torch tensor alike, without a copy."""
+    if type(x).__module__.startswith("torch"):
+        return tuple(x.shape), np.dtype(str(x.dtype).replace("torch.", ""))
+    x = np.asarray(x)
+    return x.shape, x.dtype
+
+
+def jacfwd(mapped, argnums=0, with_primal=False):
     """the forward-mode Jacobian of every float output w.r.t. the BROADCAST float arguments in argnums (jax.jacfwd
     of a tallymap call): -> f(*args) -> {name: {argnum: array of shape output.shape + arg.shape}}.  The unit
-    tangents of the argument's elements run as dual lanes, up to 16 per fused kernel."""
+    tangents of the argument's elements run as dual lanes, up to 16 per fused kernel.  with_primal: f returns
+    (jacobian, the call's Result) -- the primal the first launch computes beside its lanes (what jax.jacfwd of a
+    loss of the outputs evaluates the loss's derivative at)."""
     an = (argnums,) if isinstance(argnums, int) else tuple(argnums)
 
     def jac(*args, n_active=None):
@@ -1101,21 +1111,25 @@ def jacfwd(mapped, argnums=0):
             if axes[a] == 0:
                 raise UnsupportedError("tallymap: jacfwd is supported w.r.t. broadcast (in_axes=None) arguments; "
                                        "use jvp for a per-item argument")
-            x = np.asarray(args[a])
-            if not np.issubdtype(x.dtype, np.floating):
-                raise TypeError(f"tallymap: jacfwd w.r.t. argument {a} of dtype {x.dtype}")
-            for i in range(x.size):
-                e = np.zeros(x.size, x.dtype)
+            shp, dt = _host_meta(args[a])
+            if not np.issubdtype(dt, np.floating):
+                raise TypeError(f"tallymap: jacfwd w.r.t. argument {a} of dtype {dt}")
+            size = int(np.prod(shp, dtype=np.int64))
+            for i in range(size):
+                e = np.zeros(size, dt)
                 e[i] = 1
-                dirs.append((a, e.reshape(x.shape)))
+                dirs.append((a, e.reshape(shp)))
         cols = {n: [] for n in m._names}
+        primal = None
         for s in range(0, len(dirs), MAX_LANES):
             chunk = dirs[s:s + MAX_LANES]
             tans = [None] * len(args)
             for a in an:
-                lanes = [d if aa == a else np.zeros_like(np.asarray(args[a])) for aa, d in chunk]
+                shp, dt = _host_meta(args[a])
+                lanes = [d if aa == a else np.zeros(shp, dt) for aa, d in chunk]
                 tans[a] = lanes
-            _, t_tal, _, _ = _run_tangents(m, args, tans, len(chunk), n_active)
+            pr, t_tal, _, _ = _run_tangents(m, args, tans, len(chunk), n_active)
+            primal = pr if primal is None else primal
             for l in range(len(chunk)):
                 for n in m._names:
                     if n in t_tal[l]:
@@ -1128,9 +1142,10 @@ def jacfwd(mapped, argnums=0):
             full = torch.stack(cs, dim=-1)
             per, k = {}, 0
             for a in an:
-                sz = int(np.asarray(args[a]).size)
-                per[a] = full[..., k:k + sz].reshape(tuple(full.shape[:-1]) + np.shape(args[a]))
+                shp, _ = _host_meta(args[a])
+                sz = int(np.prod(shp, dtype=np.int64))
+                per[a] = full[..., k:k + sz].reshape(tuple(full.shape[:-1]) + tuple(shp))
                 k += sz
             out[n] = per
-        return out
+        return (out, primal) if with_primal else out
     return jac

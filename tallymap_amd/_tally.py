@@ -71,6 +71,17 @@ class Tally:
                            f"{sorted([n for n in self._a if RSEP not in n] + list(self._records()))})")
         shape = self._shapes[name]
         t = self._a[name]
+        if not isinstance(index, tuple) and (np.ndim(index) > 0 if not C.is_traced(index) else index.shape != ()):
+            # an array of indices into a 1-d output: one emit per element (the value broadcast, or one per index),
+            # in order -- the reference's scatter-add of a value array (`_tally.py:29-99`)
+            n = len(index)
+            vec = (value.shape != ()) if C.is_traced(value) else np.ndim(value) > 0
+            if vec and len(value) != n:
+                raise ValueError(f"tallymap: t.add({name!r}, ...): {n} indices and {len(value)} values")
+            out = self
+            for i in range(n):
+                out = out.add(name, index[i], value[i] if vec else value)
+            return out
         if isinstance(index, tuple):
             if len(index) != len(shape):
                 raise IndexError(f"tallymap: output {name!r} has {len(shape)} dims, index has {len(index)}")

@@ -453,6 +453,8 @@ def prebuild(entries, n=64):
     from .. import configs as CF
     done = []
     for name, cfg in entries:
+        if cfg.get("queue"):
+            continue                 # (a spawning call's programs are compiled when first run)
         args = cfg["inputs"](n)[0] if "inputs" in cfg else getattr(CF, f"{name}_inputs")(n)
         axes = cfg["in_axes"]
         pav = [C.AVal(np.shape(a)[1:], np.asarray(a).dtype) for a, x in zip(args, axes) if x == 0]
@@ -463,7 +465,8 @@ def prebuild(entries, n=64):
         done.append((name, prog.tag, Cm._key(src)[:16]))
         from . import reverse as R
         if "argnum" in cfg:
-            wrts = [((), (sum(1 for x in axes[:cfg["argnum"]] if x is None),))]
+            wrts = ([((), (sum(1 for x in axes[:cfg["argnum"]] if x is None),))] if cfg["argnum"] is not None
+                    else [])
         else:
             wp, wb = R.default_wrt(prog)
             wrts = [(wp, wb), ((), wb)]

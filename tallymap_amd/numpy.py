@@ -149,6 +149,23 @@ def argmax(x):
     return _arg(x, lambda v, b: C.binop("gt", v, b))
 
 
+def arange(*a, dtype=None):
+    """a constant range (numpy's): an index array for t.add, say."""
+    return _np.arange(*a, dtype=dtype)
+
+
+def cumsum(x):
+    """the running sums of a small 1-d array, left to right."""
+    if not C.is_traced(x):
+        return _np.cumsum(x)
+    if len(x.shape) != 1:
+        raise C.TraceError("cumsum of an item value: 1-d arrays only")
+    acc = [x[0]]
+    for i in range(1, x.shape[0]):
+        acc.append(acc[-1] + x[i])
+    return C.stack(acc)
+
+
 def dot(a, b):
     """the dot product of two small vectors: (a0 b0 + a1 b1) + ..., left to right."""
     acc = a[0] * b[0]
