@@ -37,10 +37,12 @@ RESERVE = 4                # chunks a wave reserves per claim while far from the
 CLAIM_NS = 50              # reserve when a chunk lasted less than this many ns per resident wave (claims from every
                            # wave at that pace would take a quarter of the counter's ~83M claims/s)
 COMPACT = 16               # iterations between the tail-phase repacks of a workgroup's live items
-POST_BATCH = 1.0           # finished items wait for their POST until the wave's waiting lane-iterations reach this
+POST_BATCH = 2.0           # finished items wait for their POST until the wave's waiting lane-iterations reach this
                            # many times the (POST + refill) / step cost ratio x 64 (0: each item's POST at once) ...
-POST_BATCH_MIN = 24        # ... when that wait is at least this long: below it the wave's per-step bookkeeping costs
-                           # more than the shared passes save (C2's 11: 2.5 % slower; C4's 37-42: 16-20 % faster)
+POST_BATCH_MIN = 25        # ... when that wait is at least this long: below it the wave's per-step bookkeeping costs
+                           # more than the shared passes save.  Measured: at 1.0 and 24, C2's 11 ran 2.5 % slower
+                           # batched and C4's 37-42 16-20 % faster; at 2.0 the transport problem's 30 / 34 ran
+                           # 12 % faster, C2's fused 24 0.5 % slower (so 25)
 BCAST_REG = 16             # broadcast operands up to this many elements are loaded into registers
 
 
