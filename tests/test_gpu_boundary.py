@@ -67,3 +67,22 @@ def test_launch_refuses_a_program_past_the_private_segment_limit():
     assert rc != 0 and b"private bytes per lane" in lib.tm_last_error()
     torch.cuda.synchronize()
     assert float(buf.sum().item()) == 0.0
+
+
+def test_launch_flag_for_later_generations_needs_a_spawning_program():
+    """tm_launch's flags bit 4 (a later spawn generation: the item count from the control words) is refused for a
+    program without tm_qnext and together with tm_zero or tm_post, before any kernel is queued."""
+    from tallymap_amd import _core as CO
+    from tallymap_amd._api import build_program
+    print("case: flags bit 4 on a non-spawning program", flush=True)
+    C = configs.C1
+    xs, keys, theta = configs.c1_inputs(64)
+    pav = [CO.AVal(np.shape(xs)[1:], np.float32), CO.AVal(np.shape(keys)[1:], np.uint32)]
+    prog, _ = build_program(C["item"], C["outputs"], C["in_axes"], pav, [CO.AVal((), np.float32)], C["max_steps"])
+    c = B.compiled(prog, {})
+    lib = Cm.lib()
+    bufs = (ctypes.c_void_p * 1)(None)
+    assert lib.tm_launch(c.id, None, bufs, 1, 0, 4, 64, 256) != 0
+    assert b"tm_qnext" in lib.tm_last_error()
+    assert lib.tm_launch(c.id, None, bufs, 1, 1, 4, 64, 256) != 0
+    assert b"flags bit 4" in lib.tm_last_error()

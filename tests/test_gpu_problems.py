@@ -33,7 +33,9 @@ def test_problem_gradient_equals_forward_mode(name):
     g = _np(pull(ct)).astype(np.float64)
     torch.cuda.synchronize()
     assert int(_np(res.stats["n_truncated"])) == 0
-    jac = tm.jacfwd(f, argnums=p["argnum"])(*args)
+    jac, prim = tm.jacfwd(f, argnums=p["argnum"], with_primal=True)(*args)
+    for k, v in prim.outputs.items():              # (the primal beside the lanes: the forward call's outputs)
+        assert np.allclose(_np(v), _np(res.outputs[k]), rtol=1e-5, atol=1e-6), k
     fwd = np.zeros_like(g)
     for out, c in ct.items():
         J = _np(jac[out][p["argnum"]]).astype(np.float64)           # output.shape + theta.shape
