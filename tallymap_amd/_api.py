@@ -24,7 +24,7 @@ MAX_ITEMS = 2 ** 31 - 1
 SUM_DTYPES = (C.F32, C.F64, C.I32, C.U32, C.I64, C.U64)
 PROG_CACHE = 64
 OPTS = ("schedule", "block", "cuda_math", "min_blocks_per_sm", "rev_checkpoints", "refill", "compact", "rev_schedule",
-        "rev_tape", "rev_refill", "rev_residual", "post_batch")
+        "rev_tape", "rev_refill", "rev_residual", "rev_record", "post_batch")
 
 
 class UnsupportedError(NotImplementedError):
@@ -631,14 +631,18 @@ def vmap(fn=None, *, outputs, in_axes=0, max_steps=None, spawn=None, backend="au
     opts:      schedule 'step' (default: a lane refills at loop-step granularity) | 'item'; block (threads per
                block, default 256); refill (idle lanes a wave waits for before it claims, default 1); compact
                (iterations between the tail-phase repacks of a workgroup's live items, default 16; 0: off);
-               rev_schedule (reverse mode: 'step', the default, a step-refilled replay over a tape in HBM, or
-               'item', one item per lane with in-lane checkpoints); rev_tape (states a lane's tape holds, default
-               512; longer items are swept from checkpoints); rev_residual (the tape adjoint's tape: None, the
+               post_batch (the deferred item end: a lane whose item ended waits this many times the ski-rental
+               break-even for the wave's other ending lanes, default 2.0; 0: off); rev_schedule (reverse mode:
+               'tape', the default, a count launch that tapes the step states in HBM and a reverse launch over
+               the tape, both step-refilled; 'step', one step-refilled replay kernel over a tape; 'item', one item
+               per lane with in-lane checkpoints); rev_tape (states a lane's tape holds, default sized to the tape
+               budget; longer items are swept from checkpoints); rev_residual (the tape adjoint's tape: None, the
                default, tapes what the step's VJP reads when that is no wider than the step's state, True / False
-               force the residual / state tape); rev_refill (free lanes a wave waits for before the
-               step-scheduled replay hands it items, default 32; 64 suits items of equal length); rev_checkpoints (the 'item' schedule's C states per
-               checkpoint buffer); cuda_math and min_blocks_per_sm
-               are accepted for drop-in compatibility and have no meaning on ROCm.
+               force the residual / state tape); rev_record (vjp's forward call is the tape adjoint's count launch,
+               default True; False: the plain forward, and the whole adjoint at pullback time); rev_refill (free
+               lanes a wave waits for before the step-scheduled replay hands it items, default 32; 64 suits items
+               of equal length); rev_checkpoints (the 'item' schedule's C states per checkpoint buffer); cuda_math
+               and min_blocks_per_sm are accepted for drop-in compatibility and have no meaning on ROCm.
     """
     if fn is None:
         return lambda f: vmap(f, outputs=outputs, in_axes=in_axes, max_steps=max_steps, spawn=spawn, backend=backend,
@@ -792,7 +796,30 @@ def vjp(mapped, *args, argnums=None, n_active=None):
     ct_outputs: {name: array or scalar (broadcast to the output)}.  The pullback launches the replay adjoint: the
     reference's jax.vjp through tallymap_call (_primitive.py:565-667, _reverse.py:1079-1180).  n_active=n runs the
     forward and the adjoint over the first n items only (the others' cotangents are zero), as the reference's
-    n_active composes with jax.vjp (_api.py:469-472)."""
+    n_active composes with jax.vjp (_api.py:469-472).
+    Where the adjoint is the tape schedule's (a loop carry needs the reverse sweep), the forward call IS the
+    adjoint's count launch: it writes the step states' tape beside the forward's outputs, and the pullback is the
+    reverse launch alone (the tape stays allocated while the pullback lives; the option rev_record=False runs the
+    plain forward and the whole adjoint at pullback time instead)."""
+    m = mapped._sized(args, n_active)
+    prog, meta, pi, bc, N, axes = m._prepare(args)
+    if prog.spawn is None and not prog.records:
+        from . import backend as B
+        spec, wrt = _arg_leaves(prog, args, axes, _argnums(argnums, len(args)))
+        got = B.record(prog, wrt, pi, bc, N, m._opts, n_active=n_active)
+        if got is not None:
+            taped, fo = got
+
+            def pullback(ct_outputs=None, ct_per_item=None):
+                cys = {}
+                if ct_per_item is not None:
+                    for j, x in enumerate(flatten(ct_per_item)[0]):
+                        if x is not None:
+                            cys[j] = x
+                g_pi, g_bc, _ = B.run_vjp(prog, wrt, pi, bc, N, _tally_cts(prog, ct_outputs), cys, m._opts,
+                                          n_active=n_active, taped=taped)
+                return _arg_cotangents(spec, wrt, g_pi, g_bc)
+            return _result(prog, meta, fo, m._names, N), pullback
     res = mapped(*args, n_active=n_active)
     return res, _pullback(mapped, args, argnums, n_active)
 

@@ -473,8 +473,8 @@ def prebuild(entries, n=64):
         for wrt in wrts:
             adj = R.adjoint_program(prog, wrt)
             pl = R.plan(adj)
-            if any(pl.sweep):            # the tape adjoint: its count and reverse programs (and value_and_grad's
-                from . import tape as T  # count program, which keeps the forward's outputs)
+            if any(pl.sweep):            # the tape adjoint: its count and reverse programs (and the count program
+                from . import tape as T  # that keeps the forward's outputs: vjp's and value_and_grad's forward)
                 tp = T.programs(adj, pl)
                 progs = [tp.count, tp.reverse, T.programs(adj, pl, keep=True).count]
             else:
@@ -529,7 +529,107 @@ def _forward_outputs(prog, c, res, ys):
     return Outputs(tallies, res[L.r_stats - base], list(ys), ntr, {}, [])
 
 
-def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forward=False):
+def _adjoint(prog, wrt):
+    """(reverse.Adjoint, reverse.Plan) of prog w.r.t. wrt, cached."""
+    from . import reverse as R
+    if getattr(prog, "records", ()):
+        raise Cm.BackendError("tallymap_amd: reverse mode through a program with Records outputs is not supported by "
+                              "this backend yet (forward mode, jvp / jacfwd, is)")
+    key = (prog.digest(), tuple(tuple(w) for w in wrt))
+    hit = _ADJ.get(key)
+    if hit is None:
+        adj = R.adjoint_program(prog, wrt)
+        hit = _ADJ[key] = (adj, R.plan(adj))
+    return hit
+
+
+def _tape_programs(adj, pl, opts, keep):
+    from . import tape as T
+    rres = opts.get("rev_residual")
+    tkey = adj.digest() + ("|vg" if keep else "") + f"|{rres}"
+    tp = _TAPE.get(tkey)
+    if tp is None:
+        tp = _TAPE[tkey] = T.programs(adj, pl, keep=keep, residual=rres)
+    return tp
+
+
+def _active(N_all, n_active):
+    if n_active is None:
+        return N_all
+    N = int(n_active)
+    if not 0 <= N <= N_all:
+        raise ValueError(f"tallymap: n_active={N} outside [0, N={N_all}]")
+    return N
+
+
+def _pad_items(xs, N, N_all):
+    """per-item results over the first N items -> over N_all (zeros after)."""
+    import torch
+    if N == N_all:
+        return xs
+    full = []
+    for g in xs:
+        z = torch.zeros((N_all,) + tuple(g.shape[1:]), dtype=g.dtype, device=g.device)
+        z[:N] = g
+        full.append(z)
+    return full
+
+
+@dataclasses.dataclass
+class Taped:
+    """the tape adjoint's forward half, kept for its reverse launch: the count launch's tape and per-item results
+    ([K, the final stored state] + the truncation flag) over the first N of N_all items."""
+    tp: object
+    tape: object
+    cap: object
+    hand: list
+    N: int
+    N_all: int
+    key: tuple
+
+
+def _tape_count(prog, adj, pl, pi_t, bc_t, N, N_all, opts, keep):
+    """the count launch over the first N items -> (Taped, the forward's Outputs when keep, else None)."""
+    import torch
+
+    from . import tape as T
+    tp = _tape_programs(adj, pl, opts, keep)
+    cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"), tp.Wck, tp.block)
+    capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
+    tape = torch.empty((max(1, N * (cap * tp.Wp + tp.Wck)),), dtype=torch.uint32, device="cuda")
+    # the loop with its states taped -> K, the final state (and with keep, the forward's own outputs)
+    c1 = compiled(tp.count, opts)
+    r1 = launch(c1, pi_t + bc_t + [capt], N, tape=tape)
+    hand = [r1[r - c1.layout.n_in] for r in c1.layout.r_ys]
+    nh = 1 + tp.n_fin
+    fo = None
+    if keep:
+        fo = _forward_outputs(prog, c1, r1, hand[nh:])
+        fo.ys = _pad_items(fo.ys, N, N_all)
+        hand = hand[:nh] + ([hand[tp.count.trunc]] if prog.trunc is not None else [])
+    return Taped(tp, tape, capt, hand, N, N_all, (adj.digest(), N)), fo
+
+
+def record(prog, wrt, pi, bc, N, opts, n_active=None):
+    """vjp's forward as the tape adjoint's count launch: -> (Taped, the forward's Outputs), or None where the
+    adjoint is not the tape schedule's (the forward-only adjoint, another rev_schedule, Records outputs): the
+    caller then runs the plain forward and the whole adjoint at pullback time.  run_vjp(..., taped=) then launches
+    the reverse program alone.  The tape stays allocated while the Taped object lives."""
+    if getattr(prog, "records", ()) or getattr(prog, "spawn", None) is not None:
+        return None
+    if opts.get("rev_schedule", "tape") != "tape" or not opts.get("rev_record", True):
+        return None
+    adj, pl = _adjoint(prog, wrt)
+    if not any(pl.sweep):
+        return None
+    N_all = N
+    N = _active(N_all, n_active)
+    pi_t = [device_tensor(x, a.dtype)[:N] for x, a in zip(pi, prog.p_avals())]
+    bc_t = [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+    return _tape_count(prog, adj, pl, pi_t, bc_t, N, N_all, opts, True)
+
+
+def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forward=False, taped=None):
     """the replay adjoint of prog: cotangents of the per-item operands wrt[0] ([N, ...] each) and the broadcast
     operands wrt[1] (exact float32 sums), given the cotangents of the float tallies (ct_tallies[slot], missing ->
     0) and of the float per-item results (ct_ys[j], missing -> 0).  -> (g_pi list, g_bc list, n_truncated).
@@ -542,53 +642,47 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
     add nothing to the broadcast ones, as they emitted nothing in the forward.
     forward: value_and_grad -- the launches that replay the forward (the forward-only adjoint; the tape adjoint's
     count program) also return the forward's outputs, so no separate forward launch is needed: -> (g_pi, g_bc,
-    n_truncated, Outputs of the forward)."""
+    n_truncated, Outputs of the forward).
+    taped: a record() of the same program, operands and n_active -- the count launch already ran (as the forward
+    call), only the reverse launch runs."""
     import torch
 
-    from . import reverse as R
-    if getattr(prog, "records", ()):
-        raise Cm.BackendError("tallymap_amd: reverse mode through a program with Records outputs is not supported by "
-                              "this backend yet (forward mode, jvp / jacfwd, is)")
-    key = (prog.digest(), tuple(tuple(w) for w in wrt))
-    hit = _ADJ.get(key)
-    if hit is None:
-        adj = R.adjoint_program(prog, wrt)
-        hit = _ADJ[key] = (adj, R.plan(adj))
-    adj, pl = hit
+    adj, pl = _adjoint(prog, wrt)
     yav = prog.y_avals()
     wide = [prog.tallies[k].name for k in (ct_tallies or {}) if prog.tallies[k].dtype == np.float64]
     wide += [f"per-item result {j}" for j in (ct_ys or {}) if yav[j].dtype == np.float64]
     if wide:
         raise Cm.BackendError(f"tallymap_amd: reverse mode through float64 outputs ({', '.join(wide)}) is not "
                               "supported by this backend (float32 outputs and per-item results only)")
-    ins_p = [device_tensor(x, a.dtype) for x, a in zip(pi, prog.p_avals())]
+    N_all = N
+    N = _active(N_all, n_active)
+    pi_t = [device_tensor(x, a.dtype)[:N] for x, a in zip(pi, prog.p_avals())]
+    cy_t = []
     for j in pl.fy:
         x = ct_ys.get(j) if ct_ys else None
-        a = yav[j]
-        ins_p.append(device_tensor(x, a.dtype) if x is not None
-                     else torch.zeros((N,) + tuple(a.shape), dtype=torch.float32, device="cuda"))
-    N_all = N
-    if n_active is not None:
-        N = int(n_active)
-        if not 0 <= N <= N_all:
-            raise ValueError(f"tallymap: n_active={N} outside [0, N={N_all}]")
-        ins_p = [t[:N] for t in ins_p]
-    ins_b = [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+        cy_t.append(device_tensor(x, yav[j].dtype)[:N] if x is not None
+                    else torch.zeros((N,) + tuple(yav[j].shape), dtype=torch.float32, device="cuda"))
+    bc_t = [device_tensor(x, a.dtype) for x, a in zip(bc, prog.b_avals())]
+    ct_t = []
     for k in pl.ft:
         s = prog.tallies[k]
         x = ct_tallies.get(k) if ct_tallies else None
         if x is None:
-            ins_b.append(torch.zeros((s.S,), dtype=torch.float32, device="cuda"))
+            ct_t.append(torch.zeros((s.S,), dtype=torch.float32, device="cuda"))
         elif isinstance(x, (int, float, np.floating, np.integer)):
-            ins_b.append(torch.full((s.S,), float(x), dtype=torch.float32, device="cuda"))
+            ct_t.append(torch.full((s.S,), float(x), dtype=torch.float32, device="cuda"))
         else:
-            ins_b.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
-                                       else x, np.float32).reshape(-1))
+            ct_t.append(device_tensor(np.broadcast_to(np.asarray(x, np.float32), s.shape) if not hasattr(x, "device")
+                                      else x, np.float32).reshape(-1))
+    ins_p, ins_b = pi_t + cy_t, bc_t + ct_t
     fo = None
+    if taped is not None and (taped.key != (adj.digest(), N) or taped.N_all != N_all):
+        raise ValueError("tallymap_amd: a recorded tape of another program, operands or n_active")
     if not any(pl.sweep):
         fkey = adj.digest() + ("|vg" if forward else "")
         q = _FWD_ONLY.get(fkey)
         if q is None:
+            from . import reverse as R
             q = _FWD_ONLY[fkey] = R.forward_only_program(adj, pl, keep=forward)
         c = compiled(q, opts)
         res = launch(c, ins_p + ins_b, N)
@@ -599,29 +693,15 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
         ys = [res[r - base] for r in L.r_ys]
         g_pi = ys[:len(adj.wrt_pi)]
         if forward:
-            fo = _forward_outputs(prog, c, res, ys[len(adj.wrt_pi):])
+            fo = _forward_outputs(prog, c, res, _pad_items(ys[len(adj.wrt_pi):], N, N_all))
     elif opts.get("rev_schedule", "tape") == "tape":
-        from . import tape as T
-        rres = opts.get("rev_residual")
-        tkey = adj.digest() + ("|vg" if forward else "") + f"|{rres}"
-        tp = _TAPE.get(tkey)
-        if tp is None:
-            tp = _TAPE[tkey] = T.programs(adj, pl, keep=forward, residual=rres)
-        cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"), tp.Wck, tp.block)
-        capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
-        tape = torch.empty((max(1, N * (cap * tp.Wp + tp.Wck)),), dtype=torch.uint32, device="cuda")
-        # count: the loop with its states taped, POST's VJP -> K, lambda, P cotangents, truncation (and with
-        # `forward`, the forward's own outputs)
-        c1 = compiled(tp.count, opts)
-        r1 = launch(c1, ins_p + ins_b + [capt], N, tape=tape)
-        hand = [r1[r - c1.layout.n_in] for r in c1.layout.r_ys]
-        if forward:
-            nh = 1 + len(tp.n_lam) + len(tp.n_gp)
-            fo = _forward_outputs(prog, c1, r1, hand[nh:])
-            hand = hand[:nh] + ([hand[tp.count.trunc]] if prog.trunc is not None else [])
-        # reverse: the steps' VJPs newest first from the tape, PRE's VJP -> the cotangents
+        if taped is None:
+            taped, fo = _tape_count(prog, adj, pl, pi_t, bc_t, N, N_all, opts, forward)
+        tp = taped.tp
+        # reverse: POST's VJP from the final state, the steps' VJPs newest first from the tape, PRE's VJP -> the
+        # cotangents
         c = compiled(tp.reverse, opts)
-        res = launch(c, ins_p + hand + ins_b + [capt], N, tape=tape)
+        res = launch(c, ins_p + taped.hand + ins_b + [taped.cap], N, tape=taped.tape)
         L = c.layout
         base = L.n_in
         g_bc = [res[L.r_out[k] - base].reshape(prog.b_avals()[j].shape)
@@ -637,18 +717,7 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
         g_bc = [res[L.r_out[j] - base] for j in adj.wrt_bc]
         g_pi = [res[r - base] for r in L.r_ys[:len(adj.wrt_pi)]]
     ntr = res[L.r_ctl - base][2:3].view(torch.int32)[0] if prog.trunc is not None else None
-
-    def pad(xs):
-        full = []
-        for g in xs:
-            z = torch.zeros((N_all,) + tuple(g.shape[1:]), dtype=g.dtype, device=g.device)
-            z[:N] = g
-            full.append(z)
-        return full
-    if N != N_all:
-        g_pi = pad(g_pi)
-        if fo is not None:
-            fo.ys = pad(fo.ys)
+    g_pi = _pad_items(g_pi, N, N_all)
     if forward:
         return g_pi, g_bc, ntr, fo
     return g_pi, g_bc, ntr

@@ -85,7 +85,7 @@ def state_words(sp):
     return _pad_words(W)
 
 
-BLOCK = 4                   # slots per block read of the residual tape's reverse step
+BLOCK = 4                   # slots per block (at least: 64 bytes) of the tape's four-slot stores and reads
 
 
 def tape_cap(N, Wp, want=None, Wck=0, block=1):
@@ -94,7 +94,8 @@ def tape_cap(N, Wp, want=None, Wck=0, block=1):
     if want:
         return -(-max(1, int(want)) // block) * block
     per = (BUDGET // max(1, int(N) * 4) - Wck) // max(1, Wp)
-    return int(max(CAP_MIN, min(CAP_MAX, per // 16 * 16)))
+    q = 32 if Wp & 1 else 16               # (cap Wp / 16 even: the row stride an odd number of 64-byte units)
+    return int(max(CAP_MIN, min(CAP_MAX, per // q * q)))
 
 
 def _pad_words(W):
@@ -156,19 +157,21 @@ class Residuals:
 
 
 def _words32(avals):
-    """True when every leaf is a 32-bit scalar or vector (a slot rebuilt from u32 words by _from_words)."""
-    return all(a.dtype.itemsize == 4 and len(a.shape) <= 1 for a in avals)
+    """True when every leaf is a 32-bit or boolean scalar or vector (a slot rebuilt from u32 words by _from_words:
+    a boolean takes a word of its own, 0 or 1)."""
+    return all((a.dtype.itemsize == 4 or a.dtype == C.BOOL) and len(a.shape) <= 1 for a in avals)
 
 
 def _to_words(leaves, W):
-    """the u32 words of 32-bit scalar or vector leaves, zero-padded to W (traced u32 scalars)."""
+    """the u32 words of 32-bit or boolean scalar or vector leaves, zero-padded to W (traced u32 scalars)."""
     out = []
     for x in leaves:
         els = [x] if not C.is_traced(x) or x.shape == () else [x[i] for i in range(x.shape[0])]
         for e in els:
             if not C.is_traced(e):
                 e = C.Tracer(C.bind("copy", [C.literal(np.asarray(e))], [C.literal(np.asarray(e)).aval.strong()])[0].var)
-            out.append(e if e.dtype == C.U32 else L.bitcast_convert_type(e, C.U32))
+            out.append(e if e.dtype == C.U32 else (C.convert(e, C.U32) if e.dtype == C.BOOL
+                                                     else L.bitcast_convert_type(e, C.U32)))
     zero = C.Tracer(C.bind("copy", [C.literal(0, C.U32, False)], [C.AVal((), C.U32)])[0].var) if len(out) < W else None
     return out + [zero] * (W - len(out))
 
@@ -178,7 +181,8 @@ def _from_words(ws, avals):
     out, w = [], 0
     for a in avals:
         n = max(1, a.size)
-        parts = [ws[w + i] if a.dtype == C.U32 else L.bitcast_convert_type(ws[w + i], a.dtype) for i in range(n)]
+        parts = [ws[w + i] if a.dtype == C.U32 else ((ws[w + i] != 0) if a.dtype == C.BOOL
+                                                     else L.bitcast_convert_type(ws[w + i], a.dtype)) for i in range(n)]
         w += n
         out.append(parts[0] if a.shape == () else C.stack(parts))
     return out
@@ -235,6 +239,14 @@ def _get(j, cap, avals, Wp, ck=False):
     return C.bind("tallymap_tape_get", [C.as_var(j), C.as_var(cap)], list(avals), words=Wp, ck=bool(ck))
 
 
+def _tracer_of(x, aval):
+    """x as a traced value of aval (a constant: a copy of the literal)."""
+    if C.is_traced(x):
+        return x
+    return C.Tracer(C.bind("copy", [C.literal(np.broadcast_to(np.asarray(x, aval.dtype), aval.shape).copy(),
+                                              aval.dtype)], [C.AVal(aval.shape, aval.dtype)])[0].var)
+
+
 def _consts(sp, Pv):
     def cval(ref):
         kind, x = ref
@@ -252,19 +264,21 @@ class TapePrograms:
     count: ItemProgram
     reverse: ItemProgram
     Wp: int                 # u32 words of a tape slot
-    n_lam: list             # per active carry j (in order): its cotangent per-item result of `count`
-    n_gp: list              # per P var q with a cotangent from POST: (q, aval)
-    Wck: int = 0            # u32 words of a row's checkpoint (the residual tape: the state before step cap)
+    n_fin: int              # per-item results of `count` after K: the item's final stored state, one per carry
+    Wck: int = 0            # u32 words of a row after its slots: the residual tape's checkpoint (the state before
+                            # step cap), padded so rows are an odd number of 64-byte units apart
     block: int = 1          # slots per block read (the residual tape's reverse reads BLOCK slots at once)
 
 
 def programs(adj, pl, keep=False, residual=None):
     """-> TapePrograms of adj (reverse.Adjoint) under pl (reverse.Plan); raises ReverseError when no loop carry
-    needs the reverse sweep (the forward-only adjoint applies then).  keep: the count program (which replays the
-    whole forward) also returns the forward's own outputs, for value_and_grad in two launches instead of three:
-    its tallies keep their kinds and its per-item results are [K, lambda, P cotangents] + [the forward's per-item
-    results, its truncation flag among them].  residual: True / False forces the residual / state tape (None: the
-    residual tape when its slot is no wider)."""
+    needs the reverse sweep (the forward-only adjoint applies then).  The count program runs the forward with its
+    states taped and takes no cotangent: its per-item results are [K, the final stored state], and the reverse
+    program starts with POST's VJP from that final state and the cotangents.  keep: the count program also returns
+    the forward's own outputs (its tallies keep their kinds, its per-item results gain the forward's, the truncation
+    flag among them), so the forward call itself can be the count launch (vjp: the pullback is then the reverse
+    launch alone; value_and_grad: two launches).  residual: True / False forces the residual / state tape (None:
+    the residual tape when its slot is no wider)."""
     if not any(pl.car_act):
         raise ReverseError("internal: the tape adjoint is for programs with an active loop carry")
     prog, sp = adj.prog, pl.sp
@@ -287,8 +301,8 @@ def programs(adj, pl, keep=False, residual=None):
     disc = [dataclasses.replace(s, kind="discard") for s in prog.tallies]
     I32, F32 = C.I32, C.F32
     # the step's VJP and PRE's (the broadcast tables read at a traced index in the loop body or PRE: their read
-    # cotangents are emitted where the read's VJP runs; POST's VJP runs in the count program, which has no
-    # cotangent tallies: dense there)
+    # cotangents are emitted where the read's VJP runs; POST's VJP, at the start of the reverse program, keeps its
+    # P cotangents dense)
     sp_pre, sp_body, _ = sparse_tables(adj, sp)
     info = {}
     body_vjp, f_ctout, f_ctin = AD.vjp_jaxpr(sp.body, pl.bconst_act + list(pl.car_act), _ct_reader(ft, S_of),
@@ -306,10 +320,19 @@ def programs(adj, pl, keep=False, residual=None):
         rp = None
     # (the residual row: cap slots, then the checkpoint padded to 64 bytes, so every row and block is 64-byte aligned)
     Wt, Wck = (rp.Wv, -(-Wp // 16) * 16) if rp is not None else (Wp, 0)
+    # rows an odd number of 64-byte units apart (the slots take an even number: tape_cap): with a power-of-two row
+    # stride (barrier's 512 slots of 8 bytes = 4 KiB) every lane of a wave wrote the same offset of its own 4 KiB
+    # and the stores of a wave queued at one HBM channel
+    if (Wck // 16) % 2 == 0:
+        Wck += 16
     # block reads (BLOCK slots per lane at once, kept in registers) when a slot's leaves are 32-bit scalars or
     # vectors and the block's words fit: the residual tape's slots, or the state's
     st_av = [car_av[j] for j in stc]
-    blk = BLOCK * Wt <= 32 and (rp.words32() if rp is not None else _words32(st_av))
+    NB = BLOCK                  # slots per block: at least 64 bytes (a slot of 1 or 2 words: 16 or 8 slots)
+    while NB * 2 * Wt <= 16:
+        NB *= 2
+    SH = NB.bit_length() - 1
+    blk = NB * Wt <= 32 and (rp.words32() if rp is not None else _words32(st_av))
 
     # ------------------------------------------------------------------------------------------ count
     tspecs = (list(prog.tallies) if keep else disc) + [TSpec("tm_tape", (1,), np.dtype(np.float32), kind="discard")]
@@ -318,11 +341,8 @@ def programs(adj, pl, keep=False, residual=None):
     try:
         tin = [C.Tracer(b.new_invar(C.AVal((s.S,), s.dtype))) for s in tspecs]
         pin = [C.Tracer(b.new_invar(a)) for a in pav]
-        cyin = [C.Tracer(b.new_invar(C.AVal(yav[j].shape, F32))) for j in fy]
         bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
-        ctin = [C.Tracer(b.new_invar(C.AVal((prog.tallies[k].S,), F32))) for k in ft]
         cap = C.Tracer(b.new_invar(C.AVal((), I32)))
-        ct_read = _ct_reader(ft, S_of, ctin)
         pre_outs = AD.eval_jaxpr(sp.pre, tin[:nT] + pin + bin_)
         cars0, Pv = list(pre_outs[:sp.ncar]), list(pre_outs[sp.ncar:])
         ccv, bcv = _consts(sp, Pv)
@@ -341,53 +361,32 @@ def programs(adj, pl, keep=False, residual=None):
                 leaves = rp.pack(vals)
             if not blk:
                 return (outs, k + 1, _put(tok, k, cap, leaves, Wt))
-            # the slot goes into row k mod BLOCK of the lane's block buffer; a full block is stored at once (64 or
+            # the slot goes into row k mod NB of the lane's block buffer; a full block is stored at once (64 or
             # 96 bytes), so a lane's tape stores complete their lines instead of landing as partial-line writes
             ws = _to_words(leaves, Wt)
-            wb, r = c[3], k & (BLOCK - 1)
-            wb = C.stack([C.stack([L.select(r == q, ws[w], wb[q][w]) for w in range(Wt)]) for q in range(BLOCK)])
-            tok = L.cond(r == BLOCK - 1, lambda t: _put(t, k - (BLOCK - 1), cap, [wb], BLOCK * Wt), lambda t: t, tok)
+            wb, r = c[3], k & (NB - 1)
+            wb = C.stack([C.stack([L.select(r == q, ws[w], wb[q][w]) for w in range(Wt)]) for q in range(NB)])
+            tok = L.cond(r == NB - 1, lambda t: _put(t, k - (NB - 1), cap, [wb], NB * Wt), lambda t: t, tok)
             return (outs, k + 1, tok, wb)
         tok0 = tin[nT]
         if sp.ncar and not _never(sp):
-            init = (cars0, np.int32(0), tok0) + ((np.zeros((BLOCK, Wt), np.uint32),) if blk else ())
+            init = (cars0, np.int32(0), tok0) + ((np.zeros((NB, Wt), np.uint32),) if blk else ())
             fin = L.while_loop(cond_f, body_f, init)
             cars_f, K_, tok = fin[0], fin[1], fin[2]
             if blk:                  # the last, partial block
                 wbf = fin[3]
-                tok = L.cond((K_ & (BLOCK - 1)) != 0,
-                             lambda t: _put(t, K_ - (K_ & (BLOCK - 1)), cap, [wbf], BLOCK * Wt), lambda t: t, tok)
+                tok = L.cond((K_ & (NB - 1)) != 0,
+                             lambda t: _put(t, K_ - (K_ & (NB - 1)), cap, [wbf], NB * Wt), lambda t: t, tok)
         else:
             cars_f, K_, tok = cars0, C.Tracer(C.bind("copy", [C.literal(0, I32, False)], [C.AVal((), I32)])[0].var), tok0
         cars_f = list(cars_f)
         post_outs = AD.eval_jaxpr(sp.post, Pv + cars_f)
-        post_cts = []
-        for j, m in enumerate(p_ctout):
-            if m:
-                q = j - nT
-                post_cts.append(cyin[fy.index(q)] if q >= 0 and q in fy else np.float32(0.0))
-        pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read)
-        got, k = {}, 0
-        for q, m in enumerate(p_ctin):
-            if m:
-                got[q] = pv[k]
-                k += 1
-
-        def tracer_of(x, aval):
-            if C.is_traced(x):
-                return x
-            return C.Tracer(C.bind("copy", [C.literal(np.broadcast_to(np.asarray(x, aval.dtype), aval.shape)
-                                                      .copy(), aval.dtype)], [C.AVal(aval.shape, aval.dtype)])[0].var)
-        ys = [tracer_of(K_, C.AVal((), I32))]
-        for j in lam_j:
-            ys.append(tracer_of(got.get(sp.nP + j, np.float32(0.0)), C.AVal(car_av[j].shape, F32)))
-        for q in gp_q:
-            ys.append(tracer_of(got[q], C.AVal(P_av[q].shape, F32)))
+        ys = [_tracer_of(K_, C.AVal((), I32))] + [_tracer_of(cars_f[j], car_av[j]) for j in stc]
         trunc = None
         if keep:
             nh = len(ys)
             for j, a in enumerate(yav):
-                ys.append(tracer_of(post_outs[nT + j], a))
+                ys.append(_tracer_of(post_outs[nT + j], a))
             trunc = nh + prog.trunc if prog.trunc is not None else None
         elif prog.trunc is not None:
             ys.append(post_outs[nT + prog.trunc])
@@ -398,7 +397,7 @@ def programs(adj, pl, keep=False, residual=None):
         C._STACK.pop()
     jx = C.Jaxpr(b.invars, outs, b.eqns)
     check_tallies(jx, len(tspecs), adj.where)
-    count = ItemProgram(jx, tuple(tspecs), nP + len(fy), nB + len(ft) + 1, trunc,
+    count = ItemProgram(jx, tuple(tspecs), nP, nB + 1, trunc,
                         adj.tag + "-count" + ("-vg" if keep else ""), adj.where)
     count.tape_words, count.tape_ck_words = Wt, Wck
     count.entry = "tm_fused" if keep else "tm_count"
@@ -415,8 +414,7 @@ def programs(adj, pl, keep=False, residual=None):
         pin = [C.Tracer(b.new_invar(a)) for a in pav]
         cyin = [C.Tracer(b.new_invar(C.AVal(yav[j].shape, F32))) for j in fy]
         kin = C.Tracer(b.new_invar(C.AVal((), I32)))
-        lamin = [C.Tracer(b.new_invar(C.AVal(car_av[j].shape, F32))) for j in lam_j]
-        gpin = [C.Tracer(b.new_invar(C.AVal(P_av[q].shape, F32))) for q in gp_q]
+        finin = [C.Tracer(b.new_invar(car_av[j])) for j in stc]
         trin = C.Tracer(b.new_invar(C.AVal((), C.BOOL))) if prog.trunc is not None else None
         bin_ = [C.Tracer(b.new_invar(a)) for a in bav]
         ctin = [C.Tracer(b.new_invar(C.AVal((prog.tallies[k].S,), F32))) for k in ft]
@@ -436,6 +434,25 @@ def programs(adj, pl, keep=False, residual=None):
                 cars[j] = x
             return cars
 
+        # POST's VJP from the final state (the stored carries as the count program left them, the step counters
+        # from K) -> the carries' cotangents lambda before the last step and the P vars' cotangents from POST
+        fin_of = dict(zip(stc, finin))
+        tc0 = [cars0[j] for j in tcj]
+        cars_f = assemble([fin_of[q] if q in fin_of else kin + aff[q] for q in sc], tc0)
+        post_cts = []
+        for j, m in enumerate(p_ctout):
+            if m:
+                q = j - nT
+                post_cts.append(cyin[fy.index(q)] if q >= 0 and q in fy else np.float32(0.0))
+        pv = AD.eval_jaxpr(post_vjp, Pv + cars_f + post_cts, ct_read)
+        got, k = {}, 0
+        for q, m in enumerate(p_ctin):
+            if m:
+                got[q] = pv[k]
+                k += 1
+        lamin = [_tracer_of(got.get(sp.nP + j, np.float32(0.0)), C.AVal(car_av[j].shape, F32)) for j in lam_j]
+        gpin = [_tracer_of(got[q], C.AVal(P_av[q].shape, F32)) for q in gp_q]
+
         def rcond(c):
             return c[0] >= 0
 
@@ -450,13 +467,13 @@ def programs(adj, pl, keep=False, residual=None):
         def rbody(c):
             j, lam, gk, tc = c[0], list(c[1]), list(c[2]), list(c[3])
             if blk:
-                # the block of BLOCK slots holding slot j, read once per BLOCK steps into registers: a lane's
+                # the block of NB slots holding slot j, read once per NB steps into registers: a lane's
                 # reads of one 64-byte block no longer depend on the block staying in L2 between its steps
                 bj, tb = c[4], c[5]
                 jb = j if rp is not None else L.min(j, cap - 1)      # (the state tape: slot cap-1 past the tape)
-                b = jb >> 2
+                b = jb >> SH
                 need = (b != bj) & (j < cap) if rp is not None else (b != bj)
-                tb = L.cond(need, lambda t: _get(b * BLOCK, cap, [C.AVal((BLOCK, Wt), C.U32)], BLOCK * Wt)[0],
+                tb = L.cond(need, lambda t: _get(b * NB, cap, [C.AVal((NB, Wt), C.U32)], NB * Wt)[0],
                             lambda t: t, tb)
                 bj = L.select(need, b, bj)
             cts = []
@@ -467,7 +484,7 @@ def programs(adj, pl, keep=False, residual=None):
             if rp is None:
                 jj = L.min(j, cap - 1)
                 if blk:
-                    got_ = dict(zip(stc, _from_words(tb[jj & (BLOCK - 1)], st_av)))
+                    got_ = dict(zip(stc, _from_words(tb[jj & (NB - 1)], st_av)))
                 else:
                     got_ = dict(zip(stc, _get(jj, cap, st_av, Wp)))
                 st = [got_[q] if q in got_ else jj + aff[q] for q in sc]
@@ -478,7 +495,7 @@ def programs(adj, pl, keep=False, residual=None):
             else:
                 def from_tape(t):
                     if blk:
-                        vals = rp.unpack(rp.from_words(tb[j & (BLOCK - 1)]))
+                        vals = rp.unpack(rp.from_words(tb[j & (NB - 1)]))
                     else:
                         vals = rp.unpack(_get(j, cap, rp.slot_avals(), Wt))
                     return list(AD.eval_jaxpr(rp.back, bcv + vals + cts, ct_read, ct_emit)), list(t)
@@ -505,11 +522,10 @@ def programs(adj, pl, keep=False, residual=None):
                 return j - 1, lam2, gk2, tc, bj, tb
             return j - 1, lam2, gk2, tc
         g0 = [np.zeros(sp.body.invars[q].aval.shape, np.float32)[()] for q in gq]
-        tc0 = [cars0[j] for j in tcj]
         if sp.ncar and not _never(sp):
             init = (kin - 1, list(lamin), g0, tc0)
             if blk:
-                init += (np.int32(-1), np.zeros((BLOCK, Wt), np.uint32))
+                init += (np.int32(-1), np.zeros((NB, Wt), np.uint32))
             _, lam_f, gk_f, tc_f = L.while_loop(rcond, rbody, init)[:4]
         else:
             lam_f, gk_f, tc_f = list(lamin), g0, tc0
@@ -555,8 +571,8 @@ def programs(adj, pl, keep=False, residual=None):
         C._STACK.pop()
     jx = C.Jaxpr(b.invars, outs, b.eqns)
     check_tallies(jx, len(tspecs), adj.where)
-    nPr = nP + len(fy) + 1 + len(lam_j) + len(gp_q) + (1 if trin is not None else 0)
+    nPr = nP + len(fy) + 1 + len(stc) + (1 if trin is not None else 0)
     rev = ItemProgram(jx, tuple(tspecs), nPr, nB + len(ft) + 1, trunc, adj.tag + "-reverse", adj.where)
     rev.poison_ys = True
     rev.tape_words, rev.tape_ck_words = Wt, Wck
-    return TapePrograms(count, rev, Wt, lam_j, [(q, P_av[q]) for q in gp_q], Wck, BLOCK if blk else 1)
+    return TapePrograms(count, rev, Wt, len(stc), Wck, NB if blk else 1)

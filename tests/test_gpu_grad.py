@@ -44,13 +44,14 @@ VARIANTS = [dict(), dict(rev_tape=4), dict(rev_tape=2), dict(rev_tape=1), dict(s
             dict(rev_schedule="step"), dict(rev_schedule="step", rev_tape=4), dict(rev_schedule="step", rev_tape=2),
             dict(rev_schedule="step", rev_refill=1), dict(rev_schedule="step", rev_refill=64),
             dict(rev_schedule="item"), dict(rev_schedule="item", rev_checkpoints=4),
-            dict(rev_schedule="item", rev_checkpoints=1), dict(post_batch=64), dict(post_batch=64, rev_residual=True)]
+            dict(rev_schedule="item", rev_checkpoints=1), dict(post_batch=64), dict(post_batch=64, rev_residual=True),
+            dict(rev_record=False)]
 
 
 @pytest.mark.parametrize("opts", VARIANTS, ids=["tape", "tape4", "tape2", "tape1", "tape-itemsched", "resid",
                                                 "resid-tape4", "resid-tape1", "step", "step-tape4", "step-tape2",
                                                 "step-refill1", "step-refill64", "item16", "item4", "item1",
-                                                "tape-postbatch", "resid-postbatch"])
+                                                "tape-postbatch", "resid-postbatch", "tape-replayed"])
 def test_c1_grad_xs_and_replay_variants(oracle, opts):
     """cotangents of xs (per item, through the loop state: the replay) and of theta with weights ct, against the
     oracle; the replay variants give bitwise the same per-item cotangents and broadcast cotangent (reference
@@ -59,8 +60,9 @@ def test_c1_grad_xs_and_replay_variants(oracle, opts):
     the residual tape forced, alone and with 4- and 1-slot tapes whose later steps replay from the checkpoint),
     the single-kernel step-scheduled replay (an item overflowing a 4- or 2-slot tape takes the checkpointed sweep;
     waves refilled by 1 or 64 free lanes), the one-item-per-lane schedule with C checkpoints (C = 4, 1 force its
-    segment re-runs), and the tape adjoint with every finished item's POST deferred to a shared pass
-    (post_batch=64; state and residual tapes)."""
+    segment re-runs), the tape adjoint with every finished item's POST deferred to a shared pass (post_batch=64;
+    state and residual tapes), and the tape adjoint whose count launch runs at pullback time (rev_record=False)
+    instead of as vjp's forward."""
     print(f"case: C1 vjp (xs, theta) {opts}", flush=True)
     xs, keys, theta = configs.c1_inputs()
     ct = np.linspace(0.5, 2.0, 16).astype(np.float32)
@@ -254,3 +256,40 @@ def test_accumulator_carry_forward_only_adjoint():
     assert abs(g - want) <= 1e-5 * abs(want), (g, want)
     jf = float(_np(tm.jacfwd(f, argnums=1)(x, th)["h"][1]).reshape(-1)[0])
     assert abs(g - jf) <= 1e-5 * abs(want), (g, jf)
+
+
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_vjp_forward_records_the_tape(name):
+    """vjp's forward call is the tape adjoint's count launch (the pullback is the reverse launch alone): its outputs
+    equal the plain forward call's (float32 atomic-order tolerance; per-item results and truncation bitwise), and
+    its cotangents are bitwise those of the replayed adjoint (rev_record=False: the plain forward, then the count
+    and reverse launches at pullback time) -- for two pullbacks of one vjp with different cotangents (the tape is
+    read, not consumed), and with n_active."""
+    import torch
+    n = 65_536 if name == "c3" else 4096
+    print(f"case: vjp records the tape {name} N={n}", flush=True)
+    cfg = configs.SIZED[name](n) if name in configs.SIZED else configs.CONFIGS[name]
+    args = configs.c3_inputs(n) if name == "c3" else configs.c5_inputs(n)
+    argnums = 1 if name == "c3" else (0, 3)
+    f, f0 = _mapped(cfg), _mapped(cfg, rev_record=False)
+    for n_active in (None, n // 3):
+        res, pull = tm.vjp(f, *args, argnums=argnums, n_active=n_active)
+        ref = f(*args, n_active=n_active)
+        _, pull0 = tm.vjp(f0, *args, argnums=argnums, n_active=n_active)
+        torch.cuda.synchronize()
+        for k in ref.outputs:
+            a, b = _np(res.outputs[k]), _np(ref.outputs[k])
+            assert a.shape == b.shape and np.allclose(a, b, rtol=1e-5, atol=1e-6 * float(np.abs(b).max())), k
+        assert np.array_equal(_np(res.truncated), _np(ref.truncated))
+        if ref.per_item is not None:
+            assert np.array_equal(_np(res.per_item).view(np.uint8), _np(ref.per_item).view(np.uint8))
+        for scale in (1.0, -0.5):
+            ct = {k: (scale * np.linspace(0.5, 2.0, v.numel())).astype(np.float32).reshape(tuple(v.shape))
+                  for k, v in ref.outputs.items()}
+            got = pull(ct)
+            want = pull0(ct)
+            torch.cuda.synchronize()
+            got, want = (got, want) if isinstance(got, tuple) else ((got,), (want,))
+            for x, y in zip(got, want):
+                assert np.array_equal(np.atleast_1d(_np(x)).view(np.uint32), np.atleast_1d(_np(y)).view(np.uint32))
+            assert any(np.any(_np(x) != 0) for x in got)
