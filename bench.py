@@ -427,6 +427,10 @@ def bench_published(steps, warmup):
         args, extra = p["inputs"](n)
         dev = [{k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in x.items()} if isinstance(x, dict)
                else torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in args]
+        # the losses' constant arrays resident on the device, as a jitted loss holds them (a host array would be
+        # copied on every call, and a pageable copy waits for the stream)
+        extra = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() if isinstance(v, np.ndarray) else v
+                 for k, v in extra.items()}
         f = P.mapped(name)
         pub = p["published"]
         runs = {"fwd": lambda: f(*dev)}

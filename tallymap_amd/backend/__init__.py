@@ -595,7 +595,10 @@ def _tape_count(prog, adj, pl, pi_t, bc_t, N, N_all, opts, keep):
     from . import tape as T
     tp = _tape_programs(adj, pl, opts, keep)
     cap = T.tape_cap(N, tp.Wp, opts.get("rev_tape"), tp.Wck, tp.block)
-    capt = torch.tensor(cap, dtype=torch.int32, device="cuda")
+    ck = (torch.cuda.current_device(), cap)
+    capt = _CAPS.get(ck)
+    if capt is None:         # (a read-only operand, made once: a new one per call is a pageable copy that waits for
+        capt = _CAPS[ck] = torch.tensor(cap, dtype=torch.int32, device="cuda")     # the stream to drain)
     tape = torch.empty((max(1, N * (cap * tp.Wp + tp.Wck)),), dtype=torch.uint32, device="cuda")
     # the loop with its states taped -> K, the final state (and with keep, the forward's own outputs)
     c1 = compiled(tp.count, opts)
@@ -724,5 +727,6 @@ def run_vjp(prog, wrt, pi, bc, N, ct_tallies, ct_ys, opts, n_active=None, forwar
 
 
 _FWD_ONLY = {}
+_CAPS = {}                  # (device, tape slots per item) -> the int32 operand of the tape programs
 _TAPE = {}                  # adjoint digest -> tape.TapePrograms
 _ADJ = {}                   # (program digest, wrt) -> (reverse.Adjoint, reverse.Plan)
