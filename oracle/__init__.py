@@ -41,6 +41,8 @@ def lib():
         L.tmref_split.argtypes = [_p, ctypes.c_uint64, _p]
         L.tmref_uniform.restype = _f
         L.tmref_uniform.argtypes = [_p, _f, _f]
+        L.tmref_uniform_at.restype = _f
+        L.tmref_uniform_at.argtypes = [_p, _u32]
         L.tmref_normal.restype = _f
         L.tmref_normal.argtypes = [_p]
         L.tmref_bits32.restype = _u32
@@ -105,6 +107,12 @@ def split(key, n):
 def uniform(key, lo=0.0, hi=1.0):
     key = np.ascontiguousarray(key, np.uint32)
     return np.float32(lib().tmref_uniform(_ptr(key), float(np.float32(lo)), float(np.float32(hi))))
+
+
+def uniform_at(key, j):
+    """element j of jax.random.uniform(key, (n,)) for any n > j."""
+    key = np.ascontiguousarray(key, np.uint32)
+    return np.float32(lib().tmref_uniform_at(_ptr(key), int(j)))
 
 
 def normal(key):

@@ -29,9 +29,12 @@
  * noted.  Config 2: a pure-Python walker with an independent normal() (trip counts and counts bitwise), the
  * drifted-Brownian exit laws with Siegmund's overshoot correction, N(0, 1) moments and a KS test of normal().
  * Config 3's gradient with scattering: photon by photon against the float64 closed form along the frozen path.
- *   PARITY UNPINNED: fold_in / split / uniform / normal LAYERING on the threefry core (which counters and keys
- *   JAX's partitionable PRNG feeds threefry): JAX is absent here, and its restatements (this file, the numpy one in
- *   tallymap_amd.random, the Python one in tests/test_oracle.py) agree with each other only.
+ * The split / fold_in / uniform LAYERING on the threefry core (which keys and counters JAX's PRNG feeds threefry;
+ * JAX itself is absent here) is pinned by data the reference published from JAX's own PRNG: walkers restated from
+ * its transport and walk-on-spheres benchmark problems, driven by this file's split / fold_in / uniform_at,
+ * reproduce the mean, 99th percentile and maximum of its published trip counts at N = 4096
+ * (docs/performance_detail.md:278, :385), whose maxima are extreme values of those particular draws.  normal()
+ * adds erf_inv to the same bits (pinned by its moments and KS above).
  */
 #include <fenv.h>
 #include <math.h>
@@ -161,6 +164,7 @@ static inline i32 f2i(float x) {
 void tmref_fold_in(const u32* k, u32 d, u32* o) { fold_in(k, d, o); }
 void tmref_split(const u32* k, u64 n, u32* out) { for (u64 i = 0; i < n; ++i) split_i(k, i, out + 2 * i); }
 float tmref_uniform(const u32* k, float lo, float hi) { return uniform_f32(k, lo, hi); }
+float tmref_uniform_at(const u32* k, u32 j) { return uniform_at(k, j); }
 float tmref_normal(const u32* k) { return normal_f32(k); }
 u32 tmref_bits32(const u32* k) { return bits32(k); }
 
