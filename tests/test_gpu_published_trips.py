@@ -78,3 +78,31 @@ def test_trip_counts_equal_published_tables(name):
     else:
         bad = [(g, w) for g, w in got if g != w]
     assert not bad, f"{name}: (measured, published {src}) differ: {bad}"
+
+
+# transport's divergence levels differ only in theta (benchmarks/vs_jax/problems/transport.py:37-38, TH0)
+TRANSPORT_LEVELS = {
+    "high": ((0.05, 0.5), "docs/performance_detail.md:288-289", [(4096, "159", "309", "338"),
+                                                                 (524288, "161", "307", "371")]),
+    "low": ((0.5, 0.5), "docs/performance_detail.md:295-296", [(4096, "4.49", "16.1", "35"),
+                                                               (524288, "4.51", "17", "45")]),
+}
+
+
+@pytest.mark.parametrize("level", list(TRANSPORT_LEVELS))
+def test_transport_trip_counts_at_other_divergence_levels(level):
+    import torch
+    th, src, rows = TRANSPORT_LEVELS[level]
+    f = P.mapped("transport")
+    bad = []
+    for n, mean, p99, mx in rows:
+        print(f"case: published trips transport {level} N={n}", flush=True)
+        (p0, keys, _, eff), _ = P.tr_inputs(n)
+        r = f(p0, keys, np.array(th, np.float32), eff)
+        assert int(r.stats["n_truncated"].item()) == 0
+        k = r.per_item.cpu().numpy().astype(np.int64)
+        torch.cuda.synchronize()
+        got = (n, _fmt(float(k.mean())), _fmt(float(np.percentile(k, 99))), _fmt(int(k.max())))
+        if got != (n, mean, p99, mx):
+            bad.append((got, (n, mean, p99, mx)))
+    assert not bad, f"transport {level}: (measured, published {src}) differ: {bad}"
