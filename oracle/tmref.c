@@ -33,8 +33,9 @@
  * JAX itself is absent here) is pinned by data the reference published from JAX's own PRNG: walkers restated from
  * its transport and walk-on-spheres benchmark problems, driven by this file's split / fold_in / uniform_at,
  * reproduce the mean, 99th percentile and maximum of its published trip counts at N = 4096
- * (docs/performance_detail.md:278, :385), whose maxima are extreme values of those particular draws.  normal()
- * adds erf_inv to the same bits (pinned by its moments and KS above).
+ * (docs/performance_detail.md:278, :385), whose maxima are extreme values of those particular draws; and
+ * normal(fold_in(key, k)) driving the reference's barrier path reproduces its published small-N mean trip counts
+ * (228, 222, 215 at N = 16, 64, 256: docs/performance_detail.md:1125-1127).
  */
 #include <fenv.h>
 #include <math.h>

@@ -651,3 +651,30 @@ def test_rng_layering_reproduces_published_walk_on_spheres_trips(oracle):
             k += 1
         trips[i] = k
     assert _published_trip_stats(trips) == ("8.88", "32", "48")
+
+
+def test_normal_layering_reproduces_published_small_n_trips(oracle):
+    """normal(fold_in(key, k)) of the oracle against the reference's published `small_n` rows: its barrier path
+    (benchmarks/vs_jax/problems/barrier.py:43-57, small_n.py:31-43; keys = split(PRNGKey(3), N), barrier 1.3 S0,
+    252 daily steps) knocked out after a mean of 228, 222 and 215 steps at N = 16, 64 and 256, and never at N = 1
+    and 4 (docs/performance_detail.md:1123-1127).  At these sizes the mean is a property of the particular draws."""
+    lm = _glibc_f32("expf")
+    F = np.float32
+    th0, th1, s0 = F(0.25), F(0.03), F(100.0)
+    dt = 1.0 / 252
+    drift = F(F(th1 - F(F(F(0.5) * th0) * th0)) * F(dt))
+    vol = F(th0 * F(np.sqrt(dt)))
+    bar = F(F(1.3) * s0)
+    keys = oracle.split(np.array([0, 3], np.uint32), 256)
+    trips = np.zeros(256, np.int64)
+    for i in range(256):
+        k, S = 0, s0
+        while k < 252:
+            z = oracle.normal(oracle.fold_in(keys[i], k))
+            S = F(S * F(lm.expf(float(F(drift + F(vol * z))))))
+            k += 1
+            if not S < bar:
+                break
+        trips[i] = k
+    for n, want in ((1, "252"), (4, "252"), (16, "228"), (64, "222"), (256, "215")):
+        assert f"{trips[:n].mean():.3g}" == want, (n, trips[:n].mean())
