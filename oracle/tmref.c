@@ -35,7 +35,8 @@
  * reproduce the mean, 99th percentile and maximum of its published trip counts at N = 4096
  * (docs/performance_detail.md:278, :385), whose maxima are extreme values of those particular draws; and
  * normal(fold_in(key, k)) driving the reference's barrier path reproduces its published small-N mean trip counts
- * (228, 222, 215 at N = 16, 64, 256: docs/performance_detail.md:1125-1127).
+ * (228, 222, 215 at N = 16, 64, 256: docs/performance_detail.md:1125-1127); and the branching shower's children,
+ * keyed fold_in(fold_in(key, n), 1), reproduce its published steps per particle (:653-654).
  */
 #include <fenv.h>
 #include <math.h>

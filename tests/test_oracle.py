@@ -678,3 +678,35 @@ def test_normal_layering_reproduces_published_small_n_trips(oracle):
         trips[i] = k
     for n, want in ((1, "252"), (4, "252"), (16, "228"), (64, "222"), (256, "215")):
         assert f"{trips[:n].mean():.3g}" == want, (n, trips[:n].mean())
+
+
+def test_spawn_layering_reproduces_published_shower_trips(oracle):
+    """The children's keys (fold_in(fold_in(key, n), 1)) and the three-element draws of the reference's branching
+    shower (benchmarks/vs_jax/problems/shower.py:51-99, 107-120: every particle of every generation, roots from
+    split(PRNGKey(0), N) with E ~ U(1, 2) from numpy's default_rng(0)), driven by the oracle's RNG with glibc's
+    log1pf: the mean, p99 and max of the steps per particle equal the published rows at N = 512 and 4096
+    (docs/performance_detail.md:653-654: 19.6 / 24 / 24 and 19.5 / 24 / 24)."""
+    lm = _glibc_f32("log1pf")
+    F = np.float32
+    th0, th1, half, emin, psplit = F(0.2), F(0.6), F(0.5), F(1e-3), F(0.03)
+    for n, want in ((512, ("19.6", "24", "24")), (4096, ("19.5", "24", "24"))):
+        E0 = np.random.default_rng(0).uniform(1.0, 2.0, n).astype(F)
+        todo = [(E0[i], F(0.0), key, 0) for i, key in enumerate(oracle.split(np.array([0, 0], np.uint32), n))]
+        steps = []
+        while todo:
+            E, z, key, g = todo.pop()
+            k, did = 0, False
+            while E > emin and k < 24:
+                kk = oracle.fold_in(key, k)
+                u0, u1, u2 = (oracle.uniform_at(kk, j) for j in range(3))
+                z = F(z - F(F(lm.log1pf(float(-u0))) * half))
+                dep = F(E * th0)
+                split = u1 < psplit and g < 6 and not did and E > emin
+                ec = F(F(F(E - dep) * th1) * F(half + F(half * u2)))
+                if split:
+                    todo.append((ec, z, oracle.fold_in(kk, 1), g + 1))
+                E = F(F(E - dep) - (ec if split else F(0.0)))
+                did = did or split
+                k += 1
+            steps.append(k)
+        assert _published_trip_stats(np.array(steps)) == want, (n, len(steps))
